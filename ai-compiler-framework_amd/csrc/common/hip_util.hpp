@@ -1,0 +1,92 @@
+// HIP helpers shared by the gfx950 kernels: launch-status mapping, 16-bit
+// float conversions, vector types and wave64 reductions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "host_util.hpp"
+
+namespace aicf::hip {
+
+// Maps the launch-error state to Status (reference pattern: cudaGetLastError
+// after every launch, e.g. gemm/launcher.cu:28-33).
+inline Status launch_status(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e == hipSuccess) return Status::Ok;
+  set_last_error(what, hipGetErrorString(e));
+  return Status::Internal;
+}
+
+inline Status hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return Status::Ok;
+  set_last_error(what, hipGetErrorString(e));
+  return Status::Internal;
+}
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Grid size for a 1-D launch: enough blocks to cover n items, at most cap.
+inline unsigned grid_1d(int64_t n, int threads, int64_t cap) {
+  int64_t b = (n + threads - 1) / threads;
+  if (b < 1) b = 1;
+  if (b > cap) b = cap;
+  return static_cast<unsigned>(b);
+}
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+
+// ---- 16-bit float storage (raw bits) <-> fp32 -----------------------------
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+// Round-to-nearest-even; NaN stays a quiet NaN.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+  _Float16 x;
+  __builtin_memcpy(&x, &h, 2);
+  return static_cast<float>(x);
+}
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+  _Float16 x = static_cast<_Float16>(f);  // round-to-nearest-even
+  uint16_t h;
+  __builtin_memcpy(&h, &x, 2);
+  return h;
+}
+
+// ---- wave64 reductions (butterfly over all 64 lanes) ----------------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// ---- GELU (tanh approximation) ---------------------------------------------
+// gelu(x) = 0.5 x (1 + tanh(u)),  u = sqrt(2/pi) (x + 0.044715 x^3)
+// gelu'(x) = 0.5 (1 + t) + 0.5 x (1 - t^2) sqrt(2/pi) (1 + 3*0.044715 x^2)
+__device__ __forceinline__ float gelu_tanh_f(float x) {
+  const float k0 = 0.7978845608028654f, k1 = 0.044715f;
+  const float u = k0 * (x + k1 * x * x * x);
+  return 0.5f * x * (1.0f + tanhf(u));
+}
+__device__ __forceinline__ float gelu_tanh_grad_f(float x) {
+  const float k0 = 0.7978845608028654f, k1 = 0.044715f;
+  const float x2 = x * x;
+  const float t = tanhf(k0 * (x + k1 * x2 * x));
+  return 0.5f * (1.0f + t) + 0.5f * x * (1.0f - t * t) * k0 * (1.0f + 3.0f * k1 * x2);
+}
+
+}  // namespace aicf::hip

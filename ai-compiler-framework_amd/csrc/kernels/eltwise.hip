@@ -1,0 +1,734 @@
+// Elementwise kernels for gfx950: add, relu, relu_bwd, bias_add, copy,
+// grad_zero, mse_grad (+ fused MSE loss value), gelu and gelu_bwd.
+//
+// Reference contracts (src/backends/cuda/ops/...):
+//   add       add/launcher.cu:44-66 (math), :118-140 (checks)
+//   relu      relu/launcher.cu:44-74 (math), :83-133 (checks)
+//   relu_bwd  relu_bwd/launcher.cu:37-77 (math), :119-164 (checks)
+//   bias_add  bias_add/launcher.cu:36-76 (math), :96-189 (attrs, checks)
+//   copy      copy/kernels.cuh:8-18, copy/launcher.cu:66-181
+//   grad_zero grad_zero/launcher.cu:45-119
+//   mse_grad  mse_grad/launcher.cu:36-98 (attrs, math), :140-298 (checks, variants)
+//
+// All kernels are one pass over 16-byte vectors where the contract allows
+// (contiguous buffers, vector-aligned) with a scalar path for the rest.
+// f16 arithmetic uses native v_*_f16 instructions, which round once, as the
+// reference's __hadd/__hmul2/__hsub2 do.  grad_zero writes zeros with a
+// kernel, not a memset, so it is safe inside captured graphs.
+#include "../common/hip_util.hpp"
+
+namespace aicf::hip {
+
+namespace {
+
+size_t no_workspace(const TensorDesc*, int, const void*) { return 0; }
+
+KernelVariant make(const char* name, LaunchFn l, SupportedFn s) {
+  KernelVariant v;
+  v.name = name;
+  v.launch = l;
+  v.supported = s;
+  v.query_workspace = no_workspace;
+  return v;
+}
+
+__device__ __forceinline__ _Float16 h_of(uint16_t u) {
+  _Float16 h;
+  __builtin_memcpy(&h, &u, 2);
+  return h;
+}
+__device__ __forceinline__ uint16_t u_of(_Float16 h) {
+  uint16_t u;
+  __builtin_memcpy(&u, &h, 2);
+  return u;
+}
+
+// ---------------------------------------------------------------------------
+// Generic unary / binary elementwise launch over n elements of 4-byte or
+// 2-byte storage: each thread handles one 16-byte vector (4 or 8 elements),
+// with a guarded scalar tail.
+// ---------------------------------------------------------------------------
+template <typename T, int V, typename F>
+__global__ __launch_bounds__(256) void map1_kernel(const T* __restrict__ x, T* __restrict__ y,
+                                                   int64_t n, F f) {
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * V;
+  if (i + V <= n) {
+    typedef T vec __attribute__((ext_vector_type(V)));
+    vec a = *reinterpret_cast<const vec*>(x + i);
+    vec r;
+#pragma unroll
+    for (int c = 0; c < V; ++c) r[c] = f(a[c]);
+    *reinterpret_cast<vec*>(y + i) = r;
+  } else {
+    for (int64_t j = i; j < n; ++j) y[j] = f(x[j]);
+  }
+}
+
+template <typename T, int V, typename F>
+__global__ __launch_bounds__(256) void map2_kernel(const T* __restrict__ x0, const T* __restrict__ x1,
+                                                   T* __restrict__ y, int64_t n, F f) {
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * V;
+  if (i + V <= n) {
+    typedef T vec __attribute__((ext_vector_type(V)));
+    vec a = *reinterpret_cast<const vec*>(x0 + i);
+    vec b = *reinterpret_cast<const vec*>(x1 + i);
+    vec r;
+#pragma unroll
+    for (int c = 0; c < V; ++c) r[c] = f(a[c], b[c]);
+    *reinterpret_cast<vec*>(y + i) = r;
+  } else {
+    for (int64_t j = i; j < n; ++j) y[j] = f(x0[j], x1[j]);
+  }
+}
+
+template <typename T>
+constexpr int vec_of() {
+  return 16 / (int)sizeof(T);
+}
+
+template <typename T, typename F>
+Status launch_map1(const void* x, void* y, int64_t n, F f, void* stream, const char* what) {
+  if (n <= 0) return Status::Ok;
+  constexpr int V = vec_of<T>();
+  const bool vec_ok = aligned(x, 16) && aligned(y, 16);
+  if (vec_ok) {
+    map1_kernel<T, V, F><<<grid_1d((n + V - 1) / V, 256, INT32_MAX), 256, 0, as_stream(stream)>>>(
+        (const T*)x, (T*)y, n, f);
+  } else {
+    map1_kernel<T, 1, F><<<grid_1d(n, 256, INT32_MAX), 256, 0, as_stream(stream)>>>((const T*)x,
+                                                                                  (T*)y, n, f);
+  }
+  return launch_status(what);
+}
+
+template <typename T, typename F>
+Status launch_map2(const void* x0, const void* x1, void* y, int64_t n, F f, void* stream,
+                   const char* what) {
+  if (n <= 0) return Status::Ok;
+  constexpr int V = vec_of<T>();
+  const bool vec_ok = aligned(x0, 16) && aligned(x1, 16) && aligned(y, 16);
+  if (vec_ok) {
+    map2_kernel<T, V, F><<<grid_1d((n + V - 1) / V, 256, INT32_MAX), 256, 0, as_stream(stream)>>>(
+        (const T*)x0, (const T*)x1, (T*)y, n, f);
+  } else {
+    map2_kernel<T, 1, F><<<grid_1d(n, 256, INT32_MAX), 256, 0, as_stream(stream)>>>(
+        (const T*)x0, (const T*)x1, (T*)y, n, f);
+  }
+  return launch_status(what);
+}
+
+// ---- functors ---------------------------------------------------------------
+struct AddF32 {
+  __device__ float operator()(float a, float b) const { return a + b; }
+};
+struct AddF16 {
+  __device__ uint16_t operator()(uint16_t a, uint16_t b) const { return u_of(h_of(a) + h_of(b)); }
+};
+// relu: x > 0 ? x : +0  (NaN -> 0, -0 -> +0), compared in the storage type.
+struct ReluF32 {
+  __device__ float operator()(float x) const { return x > 0.0f ? x : 0.0f; }
+};
+struct ReluF16 {
+  __device__ uint16_t operator()(uint16_t x) const {
+    return h_of(x) > (_Float16)0.0f ? x : (uint16_t)0;
+  }
+};
+// relu_bwd: (Y > 0) ? dOut : 0, inputs (dOut, Y).
+struct ReluBwdF32 {
+  __device__ float operator()(float d, float y) const { return y > 0.0f ? d : 0.0f; }
+};
+struct ReluBwdF16 {
+  __device__ uint16_t operator()(uint16_t d, uint16_t y) const {
+    return h_of(y) > (_Float16)0.0f ? d : (uint16_t)0;
+  }
+};
+struct IdentityF32 {
+  __device__ float operator()(float x) const { return x; }
+};
+struct IdentityU16 {
+  __device__ uint16_t operator()(uint16_t x) const { return x; }
+};
+struct ZeroF32 {
+  __device__ float operator()(float) const { return 0.0f; }
+};
+struct ZeroU16 {
+  __device__ uint16_t operator()(uint16_t) const { return 0; }
+};
+struct GeluF32 {
+  __device__ float operator()(float x) const { return gelu_tanh_f(x); }
+};
+struct GeluBF16 {
+  __device__ uint16_t operator()(uint16_t x) const { return f32_to_bf16(gelu_tanh_f(bf16_to_f32(x))); }
+};
+struct GeluBwdF32 {
+  __device__ float operator()(float d, float z) const { return d * gelu_tanh_grad_f(z); }
+};
+struct GeluBwdBF16 {
+  __device__ uint16_t operator()(uint16_t d, uint16_t z) const {
+    return f32_to_bf16(bf16_to_f32(d) * gelu_tanh_grad_f(bf16_to_f32(z)));
+  }
+};
+struct MseF32 {
+  float s;
+  __device__ float operator()(float p, float t) const { return (p - t) * s; }
+};
+struct MseF16Scalar {  // fp32 math, RNE store (mse_grad/launcher.cu:73-85)
+  float s;
+  __device__ uint16_t operator()(uint16_t p, uint16_t t) const {
+    return f32_to_f16((f16_to_f32(p) - f16_to_f32(t)) * s);
+  }
+};
+struct MseF16Half {  // half math (mse_grad/launcher.cu:87-98)
+  _Float16 s;
+  __device__ uint16_t operator()(uint16_t p, uint16_t t) const {
+    return u_of((_Float16)(h_of(p) - h_of(t)) * s);
+  }
+};
+
+// ---- shared checks ------------------------------------------------------------
+bool same3(const TensorDesc& a, const TensorDesc& b, const TensorDesc& c) {
+  return same_shape(a, b) && same_shape(a, c);
+}
+
+// ---------------------------------------------------------------------------
+// add: inputs (A, B) -> O, same dtype/shape, contiguous flag, numel > 0.
+// ---------------------------------------------------------------------------
+bool add_check(const TensorDesc* in, int ni, const TensorDesc* out, int no, DType d) {
+  if (!in || !out || ni != 2 || no != 1) return false;
+  const TensorDesc &A = in[0], &B = in[1], &O = out[0];
+  if (dt(A) != d || dt(B) != d || dt(O) != d) return false;
+  if (!A.contiguous || !B.contiguous || !O.contiguous) return false;
+  if (!same3(A, B, O)) return false;
+  return numel_of(O) > 0;
+}
+bool vec2_ok(const TensorDesc* in, int ni, const TensorDesc* out) {
+  if ((numel_of(out[0]) & 1) != 0) return false;
+  for (int i = 0; i < ni; ++i)
+    if (!aligned(in[i].data, 4)) return false;
+  return aligned(out[0].data, 4);
+}
+bool add_f32_sup(const TensorDesc* i, int ni, const TensorDesc* o, int no, const void*) {
+  return add_check(i, ni, o, no, DType::kF32);
+}
+bool add_f16_sup(const TensorDesc* i, int ni, const TensorDesc* o, int no, const void*) {
+  return add_check(i, ni, o, no, DType::kF16);
+}
+bool add_f16v2_sup(const TensorDesc* i, int ni, const TensorDesc* o, int no, const void*) {
+  return add_check(i, ni, o, no, DType::kF16) && vec2_ok(i, 2, o);
+}
+Status add_f32_launch(const TensorDesc* i, int ni, TensorDesc* o, int no, const void* a, void*,
+                      size_t, void* s) {
+  if (!add_f32_sup(i, ni, o, no, a)) return Status::InvalidArgument;
+  return launch_map2<float>(i[0].data, i[1].data, o[0].data, numel_of(o[0]), AddF32{}, s, "add_f32");
+}
+Status add_f16_launch(const TensorDesc* i, int ni, TensorDesc* o, int no, const void* a, void*,
+                      size_t, void* s) {
+  if (!add_f16_sup(i, ni, o, no, a)) return Status::InvalidArgument;
+  return launch_map2<uint16_t>(i[0].data, i[1].data, o[0].data, numel_of(o[0]), AddF16{}, s,
+                               "add_f16");
+}
+Status add_f16v2_launch(const TensorDesc* i, int ni, TensorDesc* o, int no, const void* a, void*,
+                        size_t, void* s) {
+  if (!add_f16v2_sup(i, ni, o, no, a)) return Status::InvalidArgument;
+  return launch_map2<uint16_t>(i[0].data, i[1].data, o[0].data, numel_of(o[0]), AddF16{}, s,
+                               "add_f16_vec2");
+}
+
+// ---------------------------------------------------------------------------
+// relu: X -> O, same shape, row-major strides, 0 < numel <= INT_MAX.
+// ---------------------------------------------------------------------------
+bool relu_check(const TensorDesc* in, int ni, const TensorDesc* out, int no, DType d) {
+  if (!in || !out || ni != 1 || no != 1) return false;
+  if (dt(in[0]) != d || dt(out[0]) != d) return false;
+  if (!same_shape(in[0], out[0])) return false;
+  if (!strides_rowmajor(in[0]) || !strides_rowmajor(out[0])) return false;
+  const int64_t n = numel_of(out[0]);
+  return n > 0 && n <= (int64_t)INT32_MAX;
+}
+bool relu_f32_sup(const TensorDesc* i, int ni, const TensorDesc* o, int no, const void*) {
+  return relu_check(i, ni, o, no, DType::kF32);
+}
+bool relu_f16_sup(const TensorDesc* i, int ni, const TensorDesc* o, int no, const void*) {
+  return relu_check(i, ni, o, no, DType::kF16);
+}
+bool relu_f16v2_sup(const TensorDesc* i, int ni, const TensorDesc* o, int no, const void*) {
+  return relu_check(i, ni, o, no, DType::kF16) && vec2_ok(i, 1, o);
+}
+Status relu_f32_launch(const TensorDesc* i, int ni, TensorDesc* o, int no, const void* a, void*,
+                       size_t, void* s) {
+  if (!relu_f32_sup(i, ni, o, no, a)) return Status::InvalidArgument;
+  return launch_map1<float>(i[0].data, o[0].data, numel_of(o[0]), ReluF32{}, s, "relu_f32");
+}
+Status relu_f16_launch(const TensorDesc* i, int ni, TensorDesc* o, int no, const void* a, void*,
+                       size_t, void* s) {
+  if (!relu_f16_sup(i, ni, o, no, a)) return Status::InvalidArgument;
+  return launch_map1<uint16_t>(i[0].data, o[0].data, numel_of(o[0]), ReluF16{}, s, "relu_f16");
+}
+Status relu_f16v2_launch(const TensorDesc* i, int ni, TensorDesc* o, int no, const void* a, void*,
+                         size_t, void* s) {
+  if (!relu_f16v2_sup(i, ni, o, no, a)) return Status::InvalidArgument;
+  return launch_map1<uint16_t>(i[0].data, o[0].data, numel_of(o[0]), ReluF16{}, s, "relu_f16_vec2");
+}
+
+// ---------------------------------------------------------------------------
+// relu_bwd: inputs (dOut, Y) -> dY, contiguous flag, same shape, numel > 0.
+// Covers every element (the reference's grid cap skips indices >= 16,776,960).
+// ---------------------------------------------------------------------------
+bool relu_bwd_check(const TensorDesc* in, int ni, const TensorDesc* out, int no, DType d) {
+  if (!in || !out || ni != 2 || no != 1) return false;
+  const TensorDesc &dO = in[0], &Y = in[1], &dY = out[0];
+  for (const TensorDesc* t : {&dO, &Y, &dY})
+    if (dt(*t) != d || !t->contiguous) return false;
+  if (Y.rank < 1 || !same_shape(Y, dO) || !same_shape(Y, dY)) return false;
+  int64_t n;
+  return numel_pos(Y, &n);
+}
+bool relu_bwd_f32_sup(const TensorDesc* i, int ni, const TensorDesc* o, int no, const void*) {
+  return relu_bwd_check(i, ni, o, no, DType::kF32);
+}
+bool relu_bwd_f16_sup(const TensorDesc* i, int ni, const TensorDesc* o, int no, const void*) {
+  return relu_bwd_check(i, ni, o, no, DType::kF16);
+}
+bool relu_bwd_f16v2_sup(const TensorDesc* i, int ni, const TensorDesc* o, int no, const void*) {
+  return relu_bwd_check(i, ni, o, no, DType::kF16) && vec2_ok(i, 2, o);
+}
+Status relu_bwd_f32_launch(const TensorDesc* i, int ni, TensorDesc* o, int no, const void* a,
+                           void*, size_t, void* s) {
+  if (!relu_bwd_f32_sup(i, ni, o, no, a)) return Status::InvalidArgument;
+  return launch_map2<float>(i[0].data, i[1].data, o[0].data, numel_of(o[0]), ReluBwdF32{}, s,
+                            "relu_bwd_f32");
+}
+Status relu_bwd_f16_launch(const TensorDesc* i, int ni, TensorDesc* o, int no, const void* a,
+                           void*, size_t, void* s) {
+  if (!relu_bwd_f16_sup(i, ni, o, no, a)) return Status::InvalidArgument;
+  return launch_map2<uint16_t>(i[0].data, i[1].data, o[0].data, numel_of(o[0]), ReluBwdF16{}, s,
+                               "relu_bwd_f16");
+}
+Status relu_bwd_f16v2_launch(const TensorDesc* i, int ni, TensorDesc* o, int no, const void* a,
+                             void*, size_t, void* s) {
+  if (!relu_bwd_f16v2_sup(i, ni, o, no, a)) return Status::InvalidArgument;
+  return launch_map2<uint16_t>(i[0].data, i[1].data, o[0].data, numel_of(o[0]), ReluBwdF16{}, s,
+                               "relu_bwd_f16_vec2");
+}
+
+// ---------------------------------------------------------------------------
+// bias_add: inputs (Y [...,N], b [N]) -> O, last dim only.  Axis from schema
+// BADD <q> or schema 0 with a payload; default -1 (bias_add/launcher.cu:104-124).
+// 2-D grid: blockIdx.y walks row tiles, threads walk columns, so no per-element
+// integer modulo is needed.
+// ---------------------------------------------------------------------------
+int64_t read_bias_axis(const void* attr) {
+  const AttrBlob& a = blob(attr);
+  if (a.schema_id != 0 && a.schema_id != AICF_SCHEMA_BADD) return -1;
+  if (!payload_ok(a, 8)) return -1;
+  return field<int64_t>(a, 0);
+}
+
+bool bias_add_check(const TensorDesc* in, int ni, const TensorDesc* out, int no, const void* attr,
+                    DType d) {
+  if (!in || !out || ni != 2 || no != 1) return false;
+  const TensorDesc &Y = in[0], &B = in[1], &O = out[0];
+  if (dt(Y) != d || !Y.contiguous || Y.rank < 2) return false;
+  if (dt(O) != d || !O.contiguous || O.rank < 2) return false;
+  if (!(B.contiguous && B.rank == 1 && dt(B) == d)) return false;
+  const int64_t axis = read_bias_axis(attr);
+  if (!(axis == -1 || axis == Y.rank - 1)) return false;
+  if (!same_shape(Y, O)) return false;
+  int64_t M, N;
+  if (!rows_cols(Y, &M, &N)) return false;
+  return B.shape[0] == N;
+}
+
+template <typename T, bool F16>
+__global__ __launch_bounds__(256) void bias_add_kernel(const T* __restrict__ Y, const T* __restrict__ b,
+                                                       T* __restrict__ O, int64_t M, int64_t N,
+                                                       int rows_per_block) {
+  const int64_t col = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (col >= N) return;
+  const T bv = b[col];
+  const int64_t r0 = (int64_t)blockIdx.y * rows_per_block;
+  const int64_t r1 = r0 + rows_per_block < M ? r0 + rows_per_block : M;
+  for (int64_t r = r0; r < r1; ++r) {
+    const int64_t i = r * N + col;
+    if constexpr (F16) {
+      O[i] = u_of(h_of(Y[i]) + h_of(bv));
+    } else {
+      O[i] = Y[i] + bv;
+    }
+  }
+}
+
+template <typename T, bool F16>
+Status bias_add_run(const TensorDesc* in, TensorDesc* out, void* stream, const char* what) {
+  int64_t M, N;
+  rows_cols(in[0], &M, &N);
+  const int rpb = 16;
+  const unsigned gx = (unsigned)((N + 255) / 256);
+  const int64_t gy = (M + rpb - 1) / rpb;
+  if (gy > 65535 * 64) return Status::InvalidArgument;
+  // rows beyond the y-grid limit are folded into more rows per block
+  int rows = rpb;
+  int64_t gyy = gy;
+  while (gyy > 65535) {
+    rows *= 2;
+    gyy = (M + rows - 1) / rows;
+  }
+  dim3 grid(gx, (unsigned)gyy);
+  bias_add_kernel<T, F16><<<grid, 256, 0, as_stream(stream)>>>((const T*)in[0].data,
+                                                               (const T*)in[1].data, (T*)out[0].data,
+                                                               M, N, rows);
+  return launch_status(what);
+}
+
+bool bias_add_f32_sup(const TensorDesc* i, int ni, const TensorDesc* o, int no, const void* a) {
+  return bias_add_check(i, ni, o, no, a, DType::kF32);
+}
+bool bias_add_f16_sup(const TensorDesc* i, int ni, const TensorDesc* o, int no, const void* a) {
+  return bias_add_check(i, ni, o, no, a, DType::kF16);
+}
+bool bias_add_f16v2_sup(const TensorDesc* i, int ni, const TensorDesc* o, int no, const void* a) {
+  if (!bias_add_check(i, ni, o, no, a, DType::kF16)) return false;
+  return (i[0].shape[i[0].rank - 1] & 1) == 0 && aligned(i[0].data, 4) && aligned(i[1].data, 4) &&
+         aligned(o[0].data, 4);
+}
+Status bias_add_f32_launch(const TensorDesc* i, int ni, TensorDesc* o, int no, const void* a,
+                           void*, size_t, void* s) {
+  if (!bias_add_f32_sup(i, ni, o, no, a)) return Status::InvalidArgument;
+  return bias_add_run<float, false>(i, o, s, "bias_add_f32");
+}
+Status bias_add_f16_launch(const TensorDesc* i, int ni, TensorDesc* o, int no, const void* a,
+                           void*, size_t, void* s) {
+  if (!bias_add_f16_sup(i, ni, o, no, a)) return Status::InvalidArgument;
+  return bias_add_run<uint16_t, true>(i, o, s, "bias_add_f16");
+}
+Status bias_add_f16v2_launch(const TensorDesc* i, int ni, TensorDesc* o, int no, const void* a,
+                             void*, size_t, void* s) {
+  if (!bias_add_f16v2_sup(i, ni, o, no, a)) return Status::InvalidArgument;
+  return bias_add_run<uint16_t, true>(i, o, s, "bias_add_f16_vec2");
+}
+
+// ---------------------------------------------------------------------------
+// copy: X -> Y, same dtype/shape, contiguous flag.
+// ---------------------------------------------------------------------------
+bool copy_check(const TensorDesc* in, int ni, const TensorDesc* out, int no, DType d) {
+  if (!in || !out || ni != 1 || no != 1) return false;
+  if (dt(in[0]) != d || dt(out[0]) != d) return false;
+  if (!in[0].contiguous || !out[0].contiguous) return false;
+  return same_shape(in[0], out[0]);
+}
+bool copy_f32_sup(const TensorDesc* i, int ni, const TensorDesc* o, int no, const void*) {
+  return copy_check(i, ni, o, no, DType::kF32);
+}
+bool copy_f16_sup(const TensorDesc* i, int ni, const TensorDesc* o, int no, const void*) {
+  return copy_check(i, ni, o, no, DType::kF16);
+}
+bool copy_bf16_sup(const TensorDesc* i, int ni, const TensorDesc* o, int no, const void*) {
+  return copy_check(i, ni, o, no, DType::kBF16);
+}
+Status copy_f32_launch(const TensorDesc* i, int ni, TensorDesc* o, int no, const void* a, void*,
+                       size_t, void* s) {
+  if (!copy_f32_sup(i, ni, o, no, a)) return Status::InvalidArgument;
+  return launch_map1<float>(i[0].data, o[0].data, numel_of(i[0]), IdentityF32{}, s, "copy_f32");
+}
+Status copy_u16_launch(const TensorDesc* i, int ni, TensorDesc* o, int no, const void* a, void*,
+                       size_t, void* s) {
+  if (!copy_check(i, ni, o, no, dt(i[0])) || (dt(i[0]) != DType::kF16 && dt(i[0]) != DType::kBF16))
+    return Status::InvalidArgument;
+  return launch_map1<uint16_t>(i[0].data, o[0].data, numel_of(i[0]), IdentityU16{}, s, "copy_u16");
+}
+
+// ---------------------------------------------------------------------------
+// grad_zero: X -> Y (zeros), same dtype/shape, contiguous, f32/f16 (+bf16).
+// ---------------------------------------------------------------------------
+bool grad_zero_sup(const TensorDesc* in, int ni, const TensorDesc* out, int no, const void*) {
+  if (!in || !out || ni != 1 || no != 1) return false;
+  if (dt(in[0]) != dt(out[0])) return false;
+  if (!same_shape(in[0], out[0])) return false;
+  if (!in[0].contiguous || !out[0].contiguous) return false;
+  const DType d = dt(in[0]);
+  return d == DType::kF32 || d == DType::kF16 || d == DType::kBF16;
+}
+Status grad_zero_launch(const TensorDesc* i, int ni, TensorDesc* o, int no, const void* a, void*,
+                        size_t, void* s) {
+  if (!grad_zero_sup(i, ni, o, no, a)) return Status::InvalidArgument;
+  const int64_t n = numel_of(o[0]);
+  if (dt(o[0]) == DType::kF32)
+    return launch_map1<float>(o[0].data, o[0].data, n, ZeroF32{}, s, "grad_zero");
+  return launch_map1<uint16_t>(o[0].data, o[0].data, n, ZeroU16{}, s, "grad_zero");
+}
+
+// ---------------------------------------------------------------------------
+// mse_grad: inputs (pred, target) -> dPred = (pred - target) * scale.
+// scale from schema MSEG <f>, else 2/numel computed in fp32 on the host.
+// ---------------------------------------------------------------------------
+bool read_mse_scale(const void* attr, float* s) {
+  const AttrBlob& a = blob(attr);
+  if (!attr || a.schema_id != AICF_SCHEMA_MSEG || !payload_ok(a, 4)) return false;
+  *s = field<float>(a, 0);
+  return true;
+}
+
+bool mse_check(const TensorDesc* in, int ni, const TensorDesc* out, int no, DType d) {
+  if (!in || !out || ni != 2 || no != 1) return false;
+  const TensorDesc &P = in[0], &T = in[1], &G = out[0];
+  for (const TensorDesc* t : {&P, &T, &G})
+    if (dt(*t) != d || !t->contiguous) return false;
+  if (P.rank < 1 || !same_shape(P, T) || !same_shape(P, G)) return false;
+  int64_t n;
+  return numel_pos(P, &n);
+}
+bool mse_f32_sup(const TensorDesc* i, int ni, const TensorDesc* o, int no, const void*) {
+  return mse_check(i, ni, o, no, DType::kF32);
+}
+bool mse_f16_sup(const TensorDesc* i, int ni, const TensorDesc* o, int no, const void*) {
+  return mse_check(i, ni, o, no, DType::kF16);
+}
+float mse_scale(const void* attr, int64_t n) {
+  float s;
+  if (read_mse_scale(attr, &s)) return s;
+  return 2.0f / (float)n;
+}
+Status mse_f32_launch(const TensorDesc* i, int ni, TensorDesc* o, int no, const void* a, void*,
+                      size_t, void* s) {
+  if (!mse_f32_sup(i, ni, o, no, a)) return Status::InvalidArgument;
+  const int64_t n = numel_of(i[0]);
+  return launch_map2<float>(i[0].data, i[1].data, o[0].data, n, MseF32{mse_scale(a, n)}, s,
+                            "mse_grad_f32");
+}
+// The f16 variant picks the half2 math path when numel is even and all
+// pointers are 4-byte aligned, like mse_grad/launcher.cu:272-283.
+Status mse_f16_launch(const TensorDesc* i, int ni, TensorDesc* o, int no, const void* a, void*,
+                      size_t, void* s) {
+  if (!mse_f16_sup(i, ni, o, no, a)) return Status::InvalidArgument;
+  const int64_t n = numel_of(i[0]);
+  const float sc = mse_scale(a, n);
+  if (vec2_ok(i, 2, o))
+    return launch_map2<uint16_t>(i[0].data, i[1].data, o[0].data, n, MseF16Half{(_Float16)sc}, s,
+                                 "mse_grad_f16x2");
+  return launch_map2<uint16_t>(i[0].data, i[1].data, o[0].data, n, MseF16Scalar{sc}, s,
+                               "mse_grad_f16");
+}
+
+// ---------------------------------------------------------------------------
+// Fused MSE loss + gradient (no reference counterpart: the reference emits
+// only the gradient).  inputs (pred f32|bf16, target f32), outputs
+// (dPred same dtype as pred, loss f32 scalar, partials f32 [>= kMseBlocks]).
+//   dPred = (pred - target) * scale          (scale as mse_grad)
+//   loss  = mean((pred - target)^2)
+// Pass 1: kMseBlocks workgroups stride over the data, each writes its partial
+// sum of squares to partials[b].  Pass 2: one workgroup sums the partials in
+// a fixed order.  The result is deterministic for a given size.
+// ---------------------------------------------------------------------------
+constexpr int kMseBlocks = 1024;
+
+template <bool BF16>
+__global__ __launch_bounds__(256) void mse_loss_grad_pass1(const void* __restrict__ pred,
+                                                           const float* __restrict__ tgt,
+                                                           void* __restrict__ dpred,
+                                                           float* __restrict__ partial, int64_t n,
+                                                           float scale) {
+  __shared__ float red[4];
+  float acc = 0.0f;
+  const int64_t nv = n / 4;
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t v = (int64_t)blockIdx.x * 256 + threadIdx.x; v < nv; v += stride) {
+    const f32x4 t = reinterpret_cast<const f32x4*>(tgt)[v];
+    f32x4 p;
+    if constexpr (BF16) {
+      const u16x4 pb = reinterpret_cast<const u16x4*>(pred)[v];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) p[c] = bf16_to_f32(pb[c]);
+    } else {
+      p = reinterpret_cast<const f32x4*>(pred)[v];
+    }
+    f32x4 d;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float e = p[c] - t[c];
+      acc = fmaf(e, e, acc);
+      d[c] = e * scale;
+    }
+    if constexpr (BF16) {
+      u16x4 db;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) db[c] = f32_to_bf16(d[c]);
+      reinterpret_cast<u16x4*>(dpred)[v] = db;
+    } else {
+      reinterpret_cast<f32x4*>(dpred)[v] = d;
+    }
+  }
+  // tail (n % 4) handled by block 0
+  if (blockIdx.x == 0) {
+    for (int64_t i = nv * 4 + threadIdx.x; i < n; i += 256) {
+      const float p = BF16 ? bf16_to_f32(((const uint16_t*)pred)[i]) : ((const float*)pred)[i];
+      const float e = p - tgt[i];
+      acc = fmaf(e, e, acc);
+      if (BF16)
+        ((uint16_t*)dpred)[i] = f32_to_bf16(e * scale);
+      else
+        ((float*)dpred)[i] = e * scale;
+    }
+  }
+  acc = wave_sum(acc);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) partial[blockIdx.x] = (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+__global__ __launch_bounds__(256) void mse_loss_grad_pass2(const float* __restrict__ partial,
+                                                           int nparts, float* __restrict__ loss,
+                                                           double inv_n) {
+  __shared__ double red[4];
+  double acc = 0.0;
+  for (int i = threadIdx.x; i < nparts; i += 256) acc += (double)partial[i];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) loss[0] = (float)(((red[0] + red[1]) + (red[2] + red[3])) * inv_n);
+}
+
+bool mse_loss_check(const TensorDesc* in, int ni, const TensorDesc* out, int no) {
+  if (!in || !out || ni != 2 || no != 3) return false;
+  const TensorDesc &P = in[0], &T = in[1], &G = out[0], &L = out[1], &W = out[2];
+  if (dt(P) != DType::kF32 && dt(P) != DType::kBF16) return false;
+  if (dt(T) != DType::kF32 || dt(G) != dt(P)) return false;
+  if (!P.contiguous || !T.contiguous || !G.contiguous) return false;
+  if (P.rank < 1 || !same_shape(P, T) || !same_shape(P, G)) return false;
+  if (dt(L) != DType::kF32 || numel_of(L) != 1) return false;
+  if (dt(W) != DType::kF32 || !W.contiguous || numel_of(W) < kMseBlocks) return false;
+  int64_t n;
+  if (!numel_pos(P, &n)) return false;
+  const int psz = dt(P) == DType::kF32 ? 16 : 8;
+  return aligned(P.data, psz) && aligned(G.data, psz) && aligned(T.data, 16);
+}
+bool mse_loss_sup(const TensorDesc* i, int ni, const TensorDesc* o, int no, const void*) {
+  return mse_loss_check(i, ni, o, no);
+}
+Status mse_loss_launch(const TensorDesc* in, int ni, TensorDesc* out, int no, const void* a, void*,
+                       size_t, void* stream) {
+  if (!mse_loss_check(in, ni, out, no)) return Status::InvalidArgument;
+  const int64_t n = numel_of(in[0]);
+  const float sc = mse_scale(a, n);
+  hipStream_t s = as_stream(stream);
+  if (dt(in[0]) == DType::kBF16)
+    mse_loss_grad_pass1<true><<<kMseBlocks, 256, 0, s>>>(in[0].data, (const float*)in[1].data,
+                                                         out[0].data, (float*)out[2].data, n, sc);
+  else
+    mse_loss_grad_pass1<false><<<kMseBlocks, 256, 0, s>>>(in[0].data, (const float*)in[1].data,
+                                                          out[0].data, (float*)out[2].data, n, sc);
+  mse_loss_grad_pass2<<<1, 256, 0, s>>>((const float*)out[2].data, kMseBlocks,
+                                        (float*)out[1].data, 1.0 / (double)n);
+  return launch_status("mse_loss_grad_v0");
+}
+
+// ---------------------------------------------------------------------------
+// gelu (tanh) forward and backward, f32 and bf16 storage, fp32 math.
+//   gelu:     X -> Y
+//   gelu_bwd: (dOut, Z) -> dZ = dOut * gelu'(Z)
+// ---------------------------------------------------------------------------
+bool unary_same(const TensorDesc* in, int ni, const TensorDesc* out, int no, DType d) {
+  if (!in || !out || ni != 1 || no != 1) return false;
+  if (dt(in[0]) != d || dt(out[0]) != d || !in[0].contiguous || !out[0].contiguous) return false;
+  int64_t n;
+  return same_shape(in[0], out[0]) && numel_pos(in[0], &n);
+}
+bool binary_same(const TensorDesc* in, int ni, const TensorDesc* out, int no, DType d) {
+  if (!in || !out || ni != 2 || no != 1) return false;
+  for (const TensorDesc* t : {&in[0], &in[1], &out[0]})
+    if (dt(*t) != d || !t->contiguous) return false;
+  int64_t n;
+  return same3(in[0], in[1], out[0]) && numel_pos(in[0], &n);
+}
+bool gelu_f32_sup(const TensorDesc* i, int ni, const TensorDesc* o, int no, const void*) {
+  return unary_same(i, ni, o, no, DType::kF32);
+}
+bool gelu_bf16_sup(const TensorDesc* i, int ni, const TensorDesc* o, int no, const void*) {
+  return unary_same(i, ni, o, no, DType::kBF16);
+}
+bool gelu_bwd_f32_sup(const TensorDesc* i, int ni, const TensorDesc* o, int no, const void*) {
+  return binary_same(i, ni, o, no, DType::kF32);
+}
+bool gelu_bwd_bf16_sup(const TensorDesc* i, int ni, const TensorDesc* o, int no, const void*) {
+  return binary_same(i, ni, o, no, DType::kBF16);
+}
+Status gelu_f32_launch(const TensorDesc* i, int ni, TensorDesc* o, int no, const void* a, void*,
+                       size_t, void* s) {
+  if (!gelu_f32_sup(i, ni, o, no, a)) return Status::InvalidArgument;
+  return launch_map1<float>(i[0].data, o[0].data, numel_of(o[0]), GeluF32{}, s, "gelu_f32");
+}
+Status gelu_bf16_launch(const TensorDesc* i, int ni, TensorDesc* o, int no, const void* a, void*,
+                        size_t, void* s) {
+  if (!gelu_bf16_sup(i, ni, o, no, a)) return Status::InvalidArgument;
+  return launch_map1<uint16_t>(i[0].data, o[0].data, numel_of(o[0]), GeluBF16{}, s, "gelu_bf16");
+}
+Status gelu_bwd_f32_launch(const TensorDesc* i, int ni, TensorDesc* o, int no, const void* a,
+                           void*, size_t, void* s) {
+  if (!gelu_bwd_f32_sup(i, ni, o, no, a)) return Status::InvalidArgument;
+  return launch_map2<float>(i[0].data, i[1].data, o[0].data, numel_of(o[0]), GeluBwdF32{}, s,
+                            "gelu_bwd_f32");
+}
+Status gelu_bwd_bf16_launch(const TensorDesc* i, int ni, TensorDesc* o, int no, const void* a,
+                            void*, size_t, void* s) {
+  if (!gelu_bwd_bf16_sup(i, ni, o, no, a)) return Status::InvalidArgument;
+  return launch_map2<uint16_t>(i[0].data, i[1].data, o[0].data, numel_of(o[0]), GeluBwdBF16{}, s,
+                               "gelu_bwd_bf16");
+}
+
+}  // namespace
+
+KernelVariant make_add_f32_variant() { return make("add_f32", add_f32_launch, add_f32_sup); }
+KernelVariant make_add_f16_variant() { return make("add_f16", add_f16_launch, add_f16_sup); }
+KernelVariant make_add_f16_vec2_variant() {
+  return make("add_f16_vec2", add_f16v2_launch, add_f16v2_sup);
+}
+KernelVariant make_relu_f32_variant() { return make("relu_f32", relu_f32_launch, relu_f32_sup); }
+KernelVariant make_relu_f16_variant() { return make("relu_f16", relu_f16_launch, relu_f16_sup); }
+KernelVariant make_relu_f16_vec2_variant() {
+  return make("relu_f16_vec2", relu_f16v2_launch, relu_f16v2_sup);
+}
+KernelVariant make_relu_bwd_f32_variant() {
+  return make("relu_bwd_f32", relu_bwd_f32_launch, relu_bwd_f32_sup);
+}
+KernelVariant make_relu_bwd_f16_variant() {
+  return make("relu_bwd_f16", relu_bwd_f16_launch, relu_bwd_f16_sup);
+}
+KernelVariant make_relu_bwd_f16_vec2_variant() {
+  return make("relu_bwd_f16_vec2", relu_bwd_f16v2_launch, relu_bwd_f16v2_sup);
+}
+KernelVariant make_bias_add_f32_variant() {
+  return make("bias_add_f32", bias_add_f32_launch, bias_add_f32_sup);
+}
+KernelVariant make_bias_add_f16_variant() {
+  return make("bias_add_f16", bias_add_f16_launch, bias_add_f16_sup);
+}
+KernelVariant make_bias_add_f16_vec2_variant() {
+  return make("bias_add_f16_vec2", bias_add_f16v2_launch, bias_add_f16v2_sup);
+}
+KernelVariant make_copy_f32_variant() { return make("copy_f32", copy_f32_launch, copy_f32_sup); }
+KernelVariant make_copy_f16_variant() { return make("copy_f16", copy_u16_launch, copy_f16_sup); }
+KernelVariant make_copy_bf16_variant() { return make("copy_bf16", copy_u16_launch, copy_bf16_sup); }
+KernelVariant make_grad_zero_variant() {
+  return make("grad_zero_fill", grad_zero_launch, grad_zero_sup);
+}
+KernelVariant make_mse_grad_f32_variant() {
+  return make("mse_grad_f32", mse_f32_launch, mse_f32_sup);
+}
+KernelVariant make_mse_grad_f16_variant() {
+  return make("mse_grad_f16", mse_f16_launch, mse_f16_sup);
+}
+KernelVariant make_mse_loss_grad_variant() {
+  return make("mse_loss_grad", mse_loss_launch, mse_loss_sup);
+}
+KernelVariant make_gelu_f32_variant() { return make("gelu_f32", gelu_f32_launch, gelu_f32_sup); }
+KernelVariant make_gelu_bf16_variant() {
+  return make("gelu_bf16", gelu_bf16_launch, gelu_bf16_sup);
+}
+KernelVariant make_gelu_bwd_f32_variant() {
+  return make("gelu_bwd_f32", gelu_bwd_f32_launch, gelu_bwd_f32_sup);
+}
+KernelVariant make_gelu_bwd_bf16_variant() {
+  return make("gelu_bwd_bf16", gelu_bwd_bf16_launch, gelu_bwd_bf16_sup);
+}
+
+}  // namespace aicf::hip

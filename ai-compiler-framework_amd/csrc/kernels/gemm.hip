@@ -1,0 +1,648 @@
+// GEMM and GEMM + fused epilogue for gfx950 on the MFMA matrix cores.
+//
+//   C[M,N] = epi( op(A)[M,K] . op(B)[K,N] )
+//
+// Reference contracts:
+//   Gemm          src/backends/cuda/ops/gemm/launcher.cu:41-70 (attrs <ii> transA,
+//                 transB under schema 0 or GEMM), :75-148 (2-D views, checks),
+//                 :342-359 (f16 path needs a row-major contiguous C)
+//   GemmEpilogue  src/backends/cuda/ops/gemm_epilogue/launcher.cu:49-80 (attrs
+//                 <iii> transA, transB, relu under schema 0 or GPEL, relu
+//                 default 1), :153-193 (checks: bias rank 1, length N)
+//                 plus the executor's GEPI layout <iii> transA, transB, kind
+//                 (core_v2/exec.py:211-252), honoured here as documented.
+//
+// Kernel design (one templated kernel, all dtypes):
+//   * workgroup tile BM x BN x BK, WM x WN waves, each wave owns a
+//     (BM/WM) x (BN/WN) block of 32x32 MFMA tiles with fp32 accumulators;
+//   * 16-bit inputs use v_mfma_f32_32x32x16_{bf16,f16}, fp32 inputs use
+//     v_mfma_f32_32x32x2f32 (true fp32 products, no reduced-precision path);
+//   * A and B tiles live in LDS as [rows][BK] with K contiguous; 16-byte
+//     chunks of a row are XOR-swizzled by (row mod chunks-per-row) so the
+//     fragment reads of 32 consecutive rows spread over all banks;
+//   * operands whose K stride is 1 are copied with 16-byte loads; operands
+//     whose M/N stride is 1 (transposed views) are loaded 16 bytes along
+//     M/N and transposed on the LDS write; anything else is gathered per
+//     element;
+//   * two LDS buffers: the global loads of tile k+1 are in flight while the
+//     MFMAs of tile k run, with one barrier per K step;
+//   * workgroup ids are remapped so that consecutive tiles of one XCD share
+//     A rows (grouped column-major raster per XCD).
+#include "../common/hip_util.hpp"
+
+namespace aicf::hip {
+
+namespace {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+enum InKind { IN_F32 = 0, IN_F16 = 1, IN_BF16 = 2 };
+enum OutKind { OUT_F32 = 0, OUT_F16 = 1, OUT_BF16 = 2 };
+enum Act { ACT_NONE = 0, ACT_RELU = 1, ACT_GELU = 2, ACT_DGELU = 3 };
+enum LoadMode { LD_KCONTIG = 0, LD_MNCONTIG = 1, LD_GATHER = 2 };
+
+struct GemmParams {
+  const void* A;
+  const void* B;
+  void* C;
+  const void* bias;  // nullptr = no bias
+  void* aux;         // pre-activation out (GELU) or Z in (DGELU); nullptr = none
+  int64_t M, N, K;
+  int64_t a_rs, a_cs;  // logical A[M,K] strides (elements)
+  int64_t b_rs, b_cs;  // logical B[K,N] strides
+  int64_t c_rs, c_cs;
+  int64_t bias_s;
+  int64_t aux_rs;
+  int a_mode, b_mode;
+  int act;
+  int bias_f32;  // bias stored as fp32 (else in the output type)
+  int tiles_m, tiles_n;
+};
+
+template <int IN>
+struct InTraits;
+template <>
+struct InTraits<IN_F32> {
+  typedef float T;
+  static constexpr int CE = 4;    // elements per 16-byte chunk
+  static constexpr int KPM = 2;   // K per MFMA
+  static constexpr int EPL = 1;   // elements per lane per MFMA operand
+};
+template <>
+struct InTraits<IN_F16> {
+  typedef uint16_t T;
+  static constexpr int CE = 8;
+  static constexpr int KPM = 16;
+  static constexpr int EPL = 8;
+};
+template <>
+struct InTraits<IN_BF16> {
+  typedef uint16_t T;
+  static constexpr int CE = 8;
+  static constexpr int KPM = 16;
+  static constexpr int EPL = 8;
+};
+
+template <int OUT>
+__device__ __forceinline__ void store_out(void* base, int64_t idx, float v) {
+  if constexpr (OUT == OUT_F32) {
+    ((float*)base)[idx] = v;
+  } else if constexpr (OUT == OUT_F16) {
+    ((uint16_t*)base)[idx] = f32_to_f16(v);
+  } else {
+    ((uint16_t*)base)[idx] = f32_to_bf16(v);
+  }
+}
+template <int OUT>
+__device__ __forceinline__ float load_out(const void* base, int64_t idx) {
+  if constexpr (OUT == OUT_F32) {
+    return ((const float*)base)[idx];
+  } else if constexpr (OUT == OUT_F16) {
+    return f16_to_f32(((const uint16_t*)base)[idx]);
+  } else {
+    return bf16_to_f32(((const uint16_t*)base)[idx]);
+  }
+}
+
+// XOR swizzle of the 16-byte chunk index inside one LDS row.
+template <int NCH>
+__device__ __forceinline__ int swz(int row, int chunk) {
+  return chunk ^ (row & (NCH - 1));
+}
+
+// Loads one operand tile (ROWS x BK, rows along M or N) from global memory
+// into registers, then writes it to LDS.  `rs` steps along the tile rows
+// (M or N), `cs` along K.
+template <int IN, int ROWS, int BK, int THREADS>
+struct TileLoader {
+  typedef typename InTraits<IN>::T T;
+  static constexpr int CE = InTraits<IN>::CE;
+  static constexpr int NCH = BK / CE;                    // chunks per LDS row
+  static constexpr int CHUNKS = ROWS * BK / CE;          // 16-byte chunks per tile
+  static constexpr int PER_THREAD = (CHUNKS + THREADS - 1) / THREADS;
+  typedef T vec __attribute__((ext_vector_type(CE)));
+  vec r[PER_THREAD];
+
+  // mode LD_KCONTIG: chunk c covers row c / NCH, k chunk c % NCH.
+  // mode LD_MNCONTIG: chunk c covers k row c / (ROWS/CE), row chunk c % (ROWS/CE).
+  __device__ void load(const T* __restrict__ g, int mode, int64_t row0, int64_t rows_total,
+                       int64_t k0, int64_t K, int64_t rs, int64_t cs, bool vec_ok) {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < PER_THREAD; ++i) {
+      const int c = t + i * THREADS;
+      vec v;
+#pragma unroll
+      for (int e = 0; e < CE; ++e) v[e] = T(0);
+      if (c < CHUNKS) {
+        if (mode == LD_KCONTIG) {
+          const int row = c / NCH, kc = c % NCH;
+          const int64_t gr = row0 + row, gk = k0 + (int64_t)kc * CE;
+          if (gr < rows_total) {
+            if (vec_ok && gk + CE <= K) {
+              v = *reinterpret_cast<const vec*>(g + gr * rs + gk);
+            } else {
+#pragma unroll
+              for (int e = 0; e < CE; ++e)
+                if (gk + e < K) v[e] = g[gr * rs + (gk + e) * cs];
+            }
+          }
+        } else {
+          constexpr int RCH = ROWS / CE;
+          const int kr = c / RCH, rc = c % RCH;
+          const int64_t gk = k0 + kr, gr = row0 + (int64_t)rc * CE;
+          if (gk < K) {
+            if (mode == LD_MNCONTIG && vec_ok && gr + CE <= rows_total) {
+              v = *reinterpret_cast<const vec*>(g + gk * cs + gr);
+            } else {
+#pragma unroll
+              for (int e = 0; e < CE; ++e)
+                if (gr + e < rows_total) v[e] = g[(gr + e) * rs + gk * cs];
+            }
+          }
+        }
+      }
+      r[i] = v;
+    }
+  }
+
+  __device__ void store(T* __restrict__ lds, int mode) const {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < PER_THREAD; ++i) {
+      const int c = t + i * THREADS;
+      if (c >= CHUNKS) continue;
+      if (mode == LD_KCONTIG) {
+        const int row = c / NCH, kc = c % NCH;
+        *reinterpret_cast<vec*>(lds + row * BK + swz<NCH>(row, kc) * CE) = r[i];
+      } else {
+        constexpr int RCH = ROWS / CE;
+        const int kr = c / RCH, rc = c % RCH;
+        const int kc = kr / CE, ke = kr % CE;
+#pragma unroll
+        for (int e = 0; e < CE; ++e) {
+          const int row = rc * CE + e;
+          lds[row * BK + swz<NCH>(row, kc) * CE + ke] = r[i][e];
+        }
+      }
+    }
+  }
+};
+
+template <int IN>
+__device__ __forceinline__ floatx16 mfma32(const typename InTraits<IN>::T* a,
+                                          const typename InTraits<IN>::T* b, floatx16 acc);
+
+template <>
+__device__ __forceinline__ floatx16 mfma32<IN_F32>(const float* a, const float* b, floatx16 acc) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a[0], b[0], acc, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ floatx16 mfma32<IN_BF16>(const uint16_t* a, const uint16_t* b,
+                                                   floatx16 acc) {
+  const bf16x8 av = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8*>(a));
+  const bf16x8 bv = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8*>(b));
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv, acc, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ floatx16 mfma32<IN_F16>(const uint16_t* a, const uint16_t* b,
+                                                  floatx16 acc) {
+  const f16x8 av = __builtin_bit_cast(f16x8, *reinterpret_cast<const u16x8*>(a));
+  const f16x8 bv = __builtin_bit_cast(f16x8, *reinterpret_cast<const u16x8*>(b));
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, acc, 0, 0, 0);
+}
+
+// Grouped raster: workgroup w of XCD x (dispatch order w*8+x) gets
+// tile (tm, tn) so that each XCD sweeps a contiguous run of tiles and
+// GROUP_M consecutive tile rows share B columns in its L2.
+__device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int total = tiles_m * tiles_n;
+  int id = blockIdx.x;
+  // XCD-aware remap: hardware id i runs on XCD (i % 8); give every XCD a
+  // contiguous range of logical ids.
+  if ((total & 7) == 0) {
+    const int per = total >> 3;
+    id = (id & 7) * per + (id >> 3);
+  }
+  constexpr int GROUP_M = 8;
+  const int group = id / (GROUP_M * tiles_n);
+  const int first_m = group * GROUP_M;
+  const int gsize = (tiles_m - first_m) < GROUP_M ? (tiles_m - first_m) : GROUP_M;
+  const int in_group = id % (GROUP_M * tiles_n);
+  tm = first_m + in_group % gsize;
+  tn = in_group / gsize;
+}
+
+template <int IN, int OUT, int BM, int BN, int BK, int WM, int WN>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_kernel(GemmParams p) {
+  typedef typename InTraits<IN>::T T;
+  constexpr int THREADS = 64 * WM * WN;
+  constexpr int CE = InTraits<IN>::CE;
+  constexpr int KPM = InTraits<IN>::KPM;
+  constexpr int EPL = InTraits<IN>::EPL;
+  constexpr int NCH = BK / CE;
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int TM = WTM / 32, TN = WTN / 32;
+  static_assert(TM >= 1 && TN >= 1, "wave tile must hold a 32x32 block");
+
+  __shared__ __attribute__((aligned(16))) T lds_a[2][BM * BK];
+  __shared__ __attribute__((aligned(16))) T lds_b[2][BN * BK];
+
+  int tm_i, tn_i;
+  tile_coords(p.tiles_m, p.tiles_n, tm_i, tn_i);
+  const int64_t m0 = (int64_t)tm_i * BM, n0 = (int64_t)tn_i * BN;
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+
+  const T* A = (const T*)p.A;
+  const T* B = (const T*)p.B;
+  // vector loads need 16-byte aligned rows and base
+  const int a_lead = p.a_mode == LD_KCONTIG ? 0 : 1;
+  const bool a_vec = (p.a_mode != LD_GATHER) && ((uintptr_t)A % 16 == 0) &&
+                     (((a_lead == 0 ? p.a_rs : p.a_cs) * (int64_t)sizeof(T)) % 16 == 0);
+  const bool b_vec = (p.b_mode != LD_GATHER) && ((uintptr_t)B % 16 == 0) &&
+                     (((p.b_mode == LD_KCONTIG ? p.b_cs : p.b_rs) * (int64_t)sizeof(T)) % 16 == 0);
+
+  TileLoader<IN, BM, BK, THREADS> la;
+  TileLoader<IN, BN, BK, THREADS> lb;
+  // A tile rows are M (row stride a_rs, k stride a_cs); B tile rows are N
+  // (row stride b_cs, k stride b_rs).
+  floatx16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  const int nk = (int)((p.K + BK - 1) / BK);
+  la.load(A, p.a_mode, m0, p.M, 0, p.K, p.a_rs, p.a_cs, a_vec);
+  lb.load(B, p.b_mode, n0, p.N, 0, p.K, p.b_cs, p.b_rs, b_vec);
+  la.store(lds_a[0], p.a_mode);
+  lb.store(lds_b[0], p.b_mode);
+  __syncthreads();
+
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < nk) {
+      la.load(A, p.a_mode, m0, p.M, (int64_t)(kt + 1) * BK, p.K, p.a_rs, p.a_cs, a_vec);
+      lb.load(B, p.b_mode, n0, p.N, (int64_t)(kt + 1) * BK, p.K, p.b_cs, p.b_rs, b_vec);
+    }
+    const T* sa = lds_a[cur];
+    const T* sb = lds_b[cur];
+#pragma unroll
+    for (int ks = 0; ks < BK / KPM; ++ks) {
+      // fragment k position of this lane inside the tile
+      const int k = ks * KPM + (lane >> 5) * EPL;
+      const int kc = k / CE, ke = k % CE;
+      T fa[TM][EPL], fb[TN][EPL];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int row = wm * WTM + i * 32 + (lane & 31);
+        const T* src = sa + row * BK + swz<NCH>(row, kc) * CE + ke;
+        if constexpr (EPL == 8) {
+          *reinterpret_cast<u16x8*>(fa[i]) = *reinterpret_cast<const u16x8*>(src);
+        } else {
+          fa[i][0] = src[0];
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int row = wn * WTN + j * 32 + (lane & 31);
+        const T* src = sb + row * BK + swz<NCH>(row, kc) * CE + ke;
+        if constexpr (EPL == 8) {
+          *reinterpret_cast<u16x8*>(fb[j]) = *reinterpret_cast<const u16x8*>(src);
+        } else {
+          fb[j][0] = src[0];
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32<IN>(fa[i], fb[j], acc[i][j]);
+    }
+    if (kt + 1 < nk) {
+      la.store(lds_a[cur ^ 1], p.a_mode);
+      lb.store(lds_b[cur ^ 1], p.b_mode);
+    }
+    __syncthreads();
+  }
+
+  // Epilogue.  Accumulator r of lane l in tile (i, j) holds
+  // row 8*(r/4) + 4*(l/32) + r%4 and column l%32 of that 32x32 block.
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int64_t n = n0 + wn * WTN + j * 32 + (lane & 31);
+      if (n >= p.N) continue;
+      float bv = 0.0f;
+      if (p.bias) {
+        bv = p.bias_f32 ? ((const float*)p.bias)[n * p.bias_s] : load_out<OUT>(p.bias, n * p.bias_s);
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t m = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (m >= p.M) continue;
+        float v = acc[i][j][r];
+        if (p.act == ACT_DGELU) {
+          v = v * gelu_tanh_grad_f(load_out<OUT>(p.aux, m * p.aux_rs + n));
+        } else {
+          v += bv;
+          if (p.act == ACT_RELU) {
+            v = v > 0.0f ? v : 0.0f;
+          } else if (p.act == ACT_GELU) {
+            if (p.aux) store_out<OUT>(p.aux, m * p.aux_rs + n, v);
+            v = gelu_tanh_f(v);
+          }
+        }
+        store_out<OUT>(p.C, m * p.c_rs + n * p.c_cs, v);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+struct View2D {
+  const void* data;
+  int64_t rows, cols, rs, cs;
+};
+
+View2D view2d(const TensorDesc& t, bool trans) {
+  if (!trans) return {t.data, t.shape[0], t.shape[1], t.stride[0], t.stride[1]};
+  return {t.data, t.shape[1], t.shape[0], t.stride[1], t.stride[0]};
+}
+
+bool stride_valid_2d(const TensorDesc& t) {
+  return t.rank == 2 && t.stride[0] > 0 && t.stride[1] > 0;
+}
+
+// gemm/launcher.cu:48-70
+void read_gemm_attr(const void* attr, bool* ta, bool* tb) {
+  *ta = *tb = false;
+  const AttrBlob& a = blob(attr);
+  if (!attr) return;
+  if (a.schema_id != 0 && a.schema_id != AICF_SCHEMA_GEMM) return;
+  if (!payload_ok(a, 8)) return;
+  *ta = field<int32_t>(a, 0) != 0;
+  *tb = field<int32_t>(a, 4) != 0;
+}
+
+// Epilogue attributes: GPEL <iii> (transA, transB, relu; relu default 1,
+// gemm_epilogue/launcher.cu:57-80) or GEPI <iii> (transA, transB, kind).
+struct EpiAttr {
+  bool ta = false, tb = false;
+  int kind = AICF_EPI_BIAS_RELU;
+};
+EpiAttr read_epi_attr(const void* attr) {
+  EpiAttr e;
+  const AttrBlob& a = blob(attr);
+  if (!attr) return e;
+  if (a.schema_id == AICF_SCHEMA_GEPI) {
+    if (!payload_ok(a, 12)) return e;
+    e.ta = field<int32_t>(a, 0) != 0;
+    e.tb = field<int32_t>(a, 4) != 0;
+    e.kind = field<int32_t>(a, 8);
+    return e;
+  }
+  if (a.schema_id != 0 && a.schema_id != AICF_SCHEMA_GPEL) return e;
+  if (!payload_ok(a, 12)) return e;
+  e.ta = field<int32_t>(a, 0) != 0;
+  e.tb = field<int32_t>(a, 4) != 0;
+  e.kind = field<int32_t>(a, 8) != 0 ? AICF_EPI_BIAS_RELU : AICF_EPI_BIAS;
+  return e;
+}
+
+bool epi_kind_valid(int k) { return k >= AICF_EPI_BIAS_RELU && k <= AICF_EPI_DGELU; }
+
+// gemm/launcher.cu:116-148: A[M,K] . B[K,N] -> C[M,N] with positive strides.
+bool gemm_views_ok(const TensorDesc& A0, const TensorDesc& B0, const TensorDesc& C0, bool ta,
+                   bool tb) {
+  if (A0.rank != 2 || B0.rank != 2 || C0.rank != 2) return false;
+  if (!stride_valid_2d(A0) || !stride_valid_2d(B0) || !stride_valid_2d(C0)) return false;
+  const View2D A = view2d(A0, ta), B = view2d(B0, tb), C = view2d(C0, false);
+  const int64_t M = A.rows, K = A.cols, N = B.cols;
+  if (M <= 0 || N <= 0 || K <= 0) return false;
+  if (B.rows != K || C.rows != M || C.cols != N) return false;
+  if (M > INT32_MAX / 2 || N > INT32_MAX / 2) return false;
+  return true;
+}
+
+int load_mode(int64_t rs_rows, int64_t cs_k) {
+  if (cs_k == 1) return LD_KCONTIG;
+  if (rs_rows == 1) return LD_MNCONTIG;
+  return LD_GATHER;
+}
+
+template <int IN, int OUT, int BM, int BN, int BK, int WM, int WN>
+Status run_cfg(GemmParams& p, hipStream_t s) {
+  p.tiles_m = (int)((p.M + BM - 1) / BM);
+  p.tiles_n = (int)((p.N + BN - 1) / BN);
+  const int64_t total = (int64_t)p.tiles_m * p.tiles_n;
+  if (total > INT32_MAX) return Status::InvalidArgument;
+  gemm_mfma_kernel<IN, OUT, BM, BN, BK, WM, WN><<<(unsigned)total, 64 * WM * WN, 0, s>>>(p);
+  return launch_status("gemm_mfma");
+}
+
+template <int IN, int OUT>
+Status run_gemm(GemmParams& p, hipStream_t s) {
+  // Large problems: 128x128 workgroup tiles (4 waves, 64x64 per wave).
+  // Smaller ones: 64x64 tiles so that enough workgroups exist.
+  const int64_t big_tiles = ((p.M + 127) / 128) * ((p.N + 127) / 128);
+  if (big_tiles >= 512) return run_cfg<IN, OUT, 128, 128, (IN == IN_F32 ? 32 : 64), 2, 2>(p, s);
+  return run_cfg<IN, OUT, 64, 64, (IN == IN_F32 ? 32 : 64), 2, 2>(p, s);
+}
+
+int in_kind(DType d) {
+  return d == DType::kF32 ? IN_F32 : d == DType::kF16 ? IN_F16 : IN_BF16;
+}
+
+Status dispatch_gemm(GemmParams& p, DType din, DType dout, hipStream_t s) {
+  const int ik = in_kind(din);
+  if (ik == IN_F32 && dout == DType::kF32) return run_gemm<IN_F32, OUT_F32>(p, s);
+  if (ik == IN_F16 && dout == DType::kF16) return run_gemm<IN_F16, OUT_F16>(p, s);
+  if (ik == IN_F16 && dout == DType::kF32) return run_gemm<IN_F16, OUT_F32>(p, s);
+  if (ik == IN_BF16 && dout == DType::kBF16) return run_gemm<IN_BF16, OUT_BF16>(p, s);
+  if (ik == IN_BF16 && dout == DType::kF32) return run_gemm<IN_BF16, OUT_F32>(p, s);
+  return Status::InvalidArgument;
+}
+
+void fill_operands(GemmParams& p, const TensorDesc& A0, const TensorDesc& B0, const TensorDesc& C0,
+                   bool ta, bool tb) {
+  const View2D A = view2d(A0, ta), B = view2d(B0, tb), C = view2d(C0, false);
+  p.A = A.data;
+  p.B = B.data;
+  p.C = const_cast<void*>(C.data);
+  p.M = A.rows;
+  p.K = A.cols;
+  p.N = B.cols;
+  p.a_rs = A.rs;
+  p.a_cs = A.cs;
+  p.b_rs = B.rs;
+  p.b_cs = B.cs;
+  p.c_rs = C.rs;
+  p.c_cs = C.cs;
+  p.a_mode = load_mode(A.rs, A.cs);
+  p.b_mode = load_mode(B.cs, B.rs);  // B tile rows are N, K stride is b_rs
+  p.bias = nullptr;
+  p.aux = nullptr;
+  p.act = ACT_NONE;
+}
+
+// ---- Gemm variants --------------------------------------------------------
+bool gemm_check(const TensorDesc* in, int ni, const TensorDesc* out, int no, const void* attr,
+                DType din, DType dout, bool c_rowmajor) {
+  if (!in || !out || ni != 2 || no != 1) return false;
+  if (dt(in[0]) != din || dt(in[1]) != din || dt(out[0]) != dout) return false;
+  bool ta, tb;
+  read_gemm_attr(attr, &ta, &tb);
+  if (!gemm_views_ok(in[0], in[1], out[0], ta, tb)) return false;
+  return !c_rowmajor || is_contig_2d_rowmajor(out[0]);
+}
+
+Status gemm_launch_common(const TensorDesc* in, TensorDesc* out, const void* attr, DType din,
+                          DType dout, void* stream) {
+  bool ta, tb;
+  read_gemm_attr(attr, &ta, &tb);
+  GemmParams p{};
+  fill_operands(p, in[0], in[1], out[0], ta, tb);
+  return dispatch_gemm(p, din, dout, as_stream(stream));
+}
+
+#define GEMM_VARIANT(NAME, DIN, DOUT, CROW)                                                       \
+  bool NAME##_sup(const TensorDesc* i, int ni, const TensorDesc* o, int no, const void* a) {     \
+    return gemm_check(i, ni, o, no, a, DIN, DOUT, CROW);                                          \
+  }                                                                                               \
+  Status NAME##_launch(const TensorDesc* i, int ni, TensorDesc* o, int no, const void* a, void*, \
+                       size_t, void* s) {                                                         \
+    if (!NAME##_sup(i, ni, o, no, a)) return Status::InvalidArgument;                            \
+    return gemm_launch_common(i, o, a, DIN, DOUT, s);                                             \
+  }
+
+GEMM_VARIANT(gemm_f32, DType::kF32, DType::kF32, false)
+GEMM_VARIANT(gemm_f16, DType::kF16, DType::kF16, true)
+GEMM_VARIANT(gemm_bf16, DType::kBF16, DType::kBF16, false)
+GEMM_VARIANT(gemm_bf16_f32out, DType::kBF16, DType::kF32, false)
+
+// ---- GemmEpilogue variants ------------------------------------------------
+// inputs (A, B, X): X is the bias [N] (kinds 0..4) or Z [M,N] (kind 5).
+// outputs (C) or (C, Zaux) for BIAS_GELU.
+bool epi_check(const TensorDesc* in, int ni, const TensorDesc* out, int no, const void* attr,
+               DType din, DType dout, bool c_rowmajor) {
+  if (!in || !out || ni != 3 || (no != 1 && no != 2)) return false;
+  if (dt(in[0]) != din || dt(in[1]) != din || dt(out[0]) != dout) return false;
+  const EpiAttr e = read_epi_attr(attr);
+  if (!epi_kind_valid(e.kind)) return false;
+  if (!gemm_views_ok(in[0], in[1], out[0], e.ta, e.tb)) return false;
+  if (c_rowmajor && !is_contig_2d_rowmajor(out[0])) return false;
+  const View2D C = view2d(out[0], false);
+  const TensorDesc& X = in[2];
+  if (e.kind == AICF_EPI_DGELU) {
+    if (no != 1) return false;
+    if (dt(X) != dout || X.rank != 2 || X.shape[0] != C.rows || X.shape[1] != C.cols) return false;
+    if (X.stride[1] != 1 || X.stride[0] <= 0) return false;
+  } else {
+    // bias: rank 1, length N, positive stride; dtype = input dtype, or fp32
+    if (X.rank != 1 || X.stride[0] <= 0 || X.shape[0] != C.cols) return false;
+    if (dt(X) != din && dt(X) != DType::kF32) return false;
+    if (dt(X) != dout && dt(X) != DType::kF32) return false;
+  }
+  if (no == 2) {
+    if (e.kind != AICF_EPI_BIAS_GELU) return false;
+    const TensorDesc& Z = out[1];
+    if (dt(Z) != dout || Z.rank != 2 || Z.shape[0] != C.rows || Z.shape[1] != C.cols) return false;
+    if (Z.stride[1] != 1 || Z.stride[0] <= 0) return false;
+  }
+  return true;
+}
+
+Status epi_launch_common(const TensorDesc* in, int no, TensorDesc* out, const void* attr, DType din,
+                         DType dout, void* stream) {
+  const EpiAttr e = read_epi_attr(attr);
+  GemmParams p{};
+  fill_operands(p, in[0], in[1], out[0], e.ta, e.tb);
+  const TensorDesc& X = in[2];
+  switch (e.kind) {
+    case AICF_EPI_BIAS_RELU: p.act = ACT_RELU; break;
+    case AICF_EPI_BIAS: p.act = ACT_NONE; break;
+    case AICF_EPI_RELU: p.act = ACT_RELU; break;
+    case AICF_EPI_BIAS_GELU: p.act = ACT_GELU; break;
+    case AICF_EPI_GELU: p.act = ACT_GELU; break;
+    case AICF_EPI_DGELU: p.act = ACT_DGELU; break;
+  }
+  const bool with_bias = e.kind == AICF_EPI_BIAS_RELU || e.kind == AICF_EPI_BIAS ||
+                         e.kind == AICF_EPI_BIAS_GELU;
+  if (with_bias) {
+    p.bias = X.data;
+    p.bias_s = X.stride[0];
+    p.bias_f32 = dt(X) == DType::kF32 ? 1 : 0;
+  }
+  if (e.kind == AICF_EPI_DGELU) {
+    p.aux = const_cast<void*>(X.data);
+    p.aux_rs = X.stride[0];
+  } else if (no == 2) {
+    p.aux = out[1].data;
+    p.aux_rs = out[1].stride[0];
+  }
+  return dispatch_gemm(p, din, dout, as_stream(stream));
+}
+
+#define EPI_VARIANT(NAME, DIN, DOUT, CROW)                                                        \
+  bool NAME##_sup(const TensorDesc* i, int ni, const TensorDesc* o, int no, const void* a) {     \
+    return epi_check(i, ni, o, no, a, DIN, DOUT, CROW);                                           \
+  }                                                                                               \
+  Status NAME##_launch(const TensorDesc* i, int ni, TensorDesc* o, int no, const void* a, void*, \
+                       size_t, void* s) {                                                         \
+    if (!NAME##_sup(i, ni, o, no, a)) return Status::InvalidArgument;                            \
+    return epi_launch_common(i, no, o, a, DIN, DOUT, s);                                          \
+  }
+
+EPI_VARIANT(epi_f32, DType::kF32, DType::kF32, false)
+EPI_VARIANT(epi_f16, DType::kF16, DType::kF16, true)
+EPI_VARIANT(epi_bf16, DType::kBF16, DType::kBF16, false)
+EPI_VARIANT(epi_bf16_f32out, DType::kBF16, DType::kF32, false)
+
+size_t no_workspace(const TensorDesc*, int, const void*) { return 0; }
+
+KernelVariant make(const char* name, LaunchFn l, SupportedFn s) {
+  KernelVariant v;
+  v.name = name;
+  v.launch = l;
+  v.supported = s;
+  v.query_workspace = no_workspace;
+  return v;
+}
+
+}  // namespace
+
+KernelVariant make_gemm_f32_naive_variant() {
+  return make("gemm_f32_mfma", gemm_f32_launch, gemm_f32_sup);
+}
+KernelVariant make_gemm_f16_tc_wmma_out_f16_variant() {
+  return make("gemm_f16_mfma", gemm_f16_launch, gemm_f16_sup);
+}
+KernelVariant make_gemm_bf16_variant() {
+  return make("gemm_bf16_mfma", gemm_bf16_launch, gemm_bf16_sup);
+}
+KernelVariant make_gemm_bf16_f32out_variant() {
+  return make("gemm_bf16_mfma_f32out", gemm_bf16_f32out_launch, gemm_bf16_f32out_sup);
+}
+KernelVariant make_gemm_bias_relu_f32_naive_variant() {
+  return make("gemm_epilogue_f32_mfma", epi_f32_launch, epi_f32_sup);
+}
+KernelVariant make_gemm_bias_relu_f16_tc_wmma_out_f16_variant() {
+  return make("gemm_epilogue_f16_mfma", epi_f16_launch, epi_f16_sup);
+}
+KernelVariant make_gemm_epilogue_bf16_variant() {
+  return make("gemm_epilogue_bf16_mfma", epi_bf16_launch, epi_bf16_sup);
+}
+KernelVariant make_gemm_epilogue_bf16_f32out_variant() {
+  return make("gemm_epilogue_bf16_mfma_f32out", epi_bf16_f32out_launch, epi_bf16_f32out_sup);
+}
+
+}  // namespace aicf::hip

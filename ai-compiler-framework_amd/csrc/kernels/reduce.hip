@@ -1,0 +1,615 @@
+// Reductions for gfx950: column sum (bias gradient), row max / row sum,
+// row softmax with fused row statistics, and fused softmax cross-entropy.
+//
+// Reference contracts:
+//   reduce_sum  src/backends/cuda/ops/reduce_sum/launcher.cu:33-85 (attrs, shapes),
+//               :244-304 (checks), :494-503 (direct API)
+//   row max/sum, softmax, softmax-xent: no reference counterpart (appended
+//   OpKinds RowReduce, RowSoftmax, SoftmaxXent).
+//
+// Row kernels keep a whole row in registers: a row is owned by LPR lanes
+// (a fraction of a wave, one wave, or several waves of one workgroup), each
+// holding VPT 16-byte vectors, so X is read from HBM exactly once and every
+// output is written once.  Shapes that do not match a register-resident
+// configuration use a looping kernel that reads the row twice.
+#include "../common/hip_util.hpp"
+
+namespace aicf::hip {
+
+namespace {
+
+size_t no_workspace(const TensorDesc*, int, const void*) { return 0; }
+
+KernelVariant make(const char* name, LaunchFn l, SupportedFn s, uint32_t schema = 0) {
+  KernelVariant v;
+  v.name = name;
+  v.launch = l;
+  v.supported = s;
+  v.query_workspace = no_workspace;
+  v.expected_attr_schema_id = schema;
+  return v;
+}
+
+// ===========================================================================
+// Column sum: dY [M, N] (leading dims flattened) -> out [N].
+// Each lane owns one column (waves read 64 consecutive columns per row);
+// the RS row-slices of a workgroup are combined in LDS in a fixed order.
+// With a partials buffer [P, N] the rows are also split over P workgroup
+// rows and a second pass adds the P partials in order.
+// ===========================================================================
+template <typename TI, bool BF16IN>
+__device__ __forceinline__ float load_elem(const TI* p, int64_t i) {
+  if constexpr (sizeof(TI) == 4) {
+    return p[i];
+  } else if constexpr (BF16IN) {
+    return bf16_to_f32(p[i]);
+  } else {
+    return f16_to_f32(p[i]);
+  }
+}
+
+constexpr int kColRS = 4;  // row slices (waves) per workgroup
+
+template <typename TI, bool BF16IN, bool OUT_F16>
+__global__ __launch_bounds__(256) void colsum_kernel(const TI* __restrict__ x, void* __restrict__ out,
+                                                     float* __restrict__ partial, int64_t M,
+                                                     int64_t N, int64_t rows_per_part) {
+  __shared__ float red[kColRS][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t col = (int64_t)blockIdx.x * 64 + lane;
+  const int64_t r0 = (int64_t)blockIdx.y * rows_per_part;
+  const int64_t r1 = r0 + rows_per_part < M ? r0 + rows_per_part : M;
+  float acc = 0.0f;
+  if (col < N) {
+    int64_t r = r0 + w;
+    // 4 independent loads in flight per lane
+    for (; r + 3 * kColRS < r1; r += 4 * kColRS) {
+      const float a0 = load_elem<TI, BF16IN>(x, r * N + col);
+      const float a1 = load_elem<TI, BF16IN>(x, (r + kColRS) * N + col);
+      const float a2 = load_elem<TI, BF16IN>(x, (r + 2 * kColRS) * N + col);
+      const float a3 = load_elem<TI, BF16IN>(x, (r + 3 * kColRS) * N + col);
+      acc += (a0 + a1) + (a2 + a3);
+    }
+    for (; r < r1; r += kColRS) acc += load_elem<TI, BF16IN>(x, r * N + col);
+  }
+  red[w][lane] = acc;
+  __syncthreads();
+  if (w == 0 && col < N) {
+    const float s = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
+    if (partial) {
+      partial[(int64_t)blockIdx.y * N + col] = s;
+    } else if constexpr (OUT_F16) {
+      ((uint16_t*)out)[col] = f32_to_f16(s);
+    } else {
+      ((float*)out)[col] = s;
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void colsum_finish_kernel(const float* __restrict__ partial,
+                                                            float* __restrict__ out, int64_t P,
+                                                            int64_t N) {
+  const int64_t col = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (col >= N) return;
+  float s = 0.0f;
+  for (int64_t p = 0; p < P; ++p) s += partial[p * N + col];
+  out[col] = s;
+}
+
+// RSUM axis attribute (reduce_sum/launcher.cu:75-85): default 0.
+int64_t read_rsum_axis(const void* attr) {
+  const AttrBlob& a = blob(attr);
+  if (!attr) return 0;
+  if (a.schema_id != 0 && a.schema_id != AICF_SCHEMA_RSUM) return 0;
+  if (!payload_ok(a, 8)) return 0;
+  return field<int64_t>(a, 0);
+}
+
+bool colsum_check(const TensorDesc* in, int ni, const TensorDesc* out, int no, const void* attr,
+                  DType din, DType dout, bool allow_partials) {
+  if (!in || !out || ni != 1) return false;
+  if (!(no == 1 || (allow_partials && no == 2))) return false;
+  const TensorDesc &X = in[0], &O = out[0];
+  if (dt(X) != din || !X.contiguous || X.rank < 2) return false;
+  if (read_rsum_axis(attr) != 0) return false;
+  int64_t M, N;
+  if (!rows_cols(X, &M, &N)) return false;
+  if (!(dt(O) == dout && O.contiguous && O.rank == 1 && O.shape[0] == N)) return false;
+  if (no == 2) {
+    const TensorDesc& W = out[1];
+    if (dt(W) != DType::kF32 || !W.contiguous || W.rank != 2 || W.shape[1] != N || W.shape[0] < 1)
+      return false;
+  }
+  return true;
+}
+
+template <typename TI, bool BF16IN, bool OUT_F16>
+Status colsum_run(const void* x, void* out, float* partial, int64_t P, int64_t M, int64_t N,
+                  void* stream, const char* what) {
+  hipStream_t s = as_stream(stream);
+  const unsigned gx = (unsigned)((N + 63) / 64);
+  if (partial && P > 1 && M >= 2 * P) {
+    const int64_t rpp = (M + P - 1) / P;
+    const int64_t parts = (M + rpp - 1) / rpp;
+    colsum_kernel<TI, BF16IN, OUT_F16><<<dim3(gx, (unsigned)parts), 256, 0, s>>>(
+        (const TI*)x, out, partial, M, N, rpp);
+    colsum_finish_kernel<<<(unsigned)((N + 255) / 256), 256, 0, s>>>(partial, (float*)out, parts, N);
+  } else {
+    colsum_kernel<TI, BF16IN, OUT_F16><<<dim3(gx, 1), 256, 0, s>>>((const TI*)x, out, nullptr, M, N,
+                                                                   M);
+  }
+  return launch_status(what);
+}
+
+#define COLSUM_VARIANT(NAME, DIN, DOUT, TI, BF16IN, OUTF16, PARTS)                                   \
+  bool NAME##_sup(const TensorDesc* i, int ni, const TensorDesc* o, int no, const void* a) {        \
+    return colsum_check(i, ni, o, no, a, DIN, DOUT, PARTS);                                          \
+  }                                                                                                  \
+  Status NAME##_launch(const TensorDesc* i, int ni, TensorDesc* o, int no, const void* a, void*,    \
+                       size_t, void* s) {                                                            \
+    if (!NAME##_sup(i, ni, o, no, a)) return Status::InvalidArgument;                               \
+    int64_t M, N;                                                                                    \
+    rows_cols(i[0], &M, &N);                                                                         \
+    float* part = no == 2 ? (float*)o[1].data : nullptr;                                            \
+    const int64_t P = no == 2 ? o[1].shape[0] : 1;                                                   \
+    return colsum_run<TI, BF16IN, OUTF16>(i[0].data, o[0].data, part, P, M, N, s, #NAME);           \
+  }
+
+COLSUM_VARIANT(colsum_f32, DType::kF32, DType::kF32, float, false, false, true)
+COLSUM_VARIANT(colsum_f16_f32, DType::kF16, DType::kF32, uint16_t, false, false, false)
+COLSUM_VARIANT(colsum_f16_f16, DType::kF16, DType::kF16, uint16_t, false, true, false)
+COLSUM_VARIANT(colsum_bf16_f32, DType::kBF16, DType::kF32, uint16_t, true, false, true)
+
+// ===========================================================================
+// Row kernels.
+// MODE_SOFTMAX: outputs y = softmax(x) per row, optional rowmax, rowsum(x).
+// MODE_SUM / MODE_MAX: one value per row.
+// MODE_XENT: logits + labels -> dlogits, argmax, row loss.
+// ===========================================================================
+enum RowMode { MODE_SOFTMAX = 0, MODE_SUM = 1, MODE_MAX = 2, MODE_XENT = 3 };
+
+struct RowArgs {
+  const float* x;
+  float* y;           // softmax / dlogits
+  float* rmax;        // row max (softmax, max)
+  float* rsum;        // row sum of x (softmax, sum)
+  const int32_t* labels;
+  int32_t* argmax;
+  float* row_loss;
+  int64_t R, C;
+  float inv_batch;    // 1/B for xent gradients
+};
+
+// Combine (value, index) pairs: larger value wins, ties go to smaller index.
+__device__ __forceinline__ void amax_combine(float& v, int& i, float v2, int i2) {
+  if (v2 > v || (v2 == v && i2 < i)) {
+    v = v2;
+    i = i2;
+  }
+}
+
+// Reduce over the LPR lanes that own one row.  LPR <= 64: butterfly within
+// the lane group.  LPR > 64: per-wave butterfly, then LDS across the
+// LPR/64 waves of the row (all waves of a workgroup belong to one row).
+template <int LPR>
+struct RowReducer {
+  static constexpr int NW = LPR > 64 ? LPR / 64 : 1;
+  float* lds;  // NW floats
+  __device__ float sum(float v) const {
+#pragma unroll
+    for (int off = (LPR < 64 ? LPR : 64) / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    if constexpr (NW > 1) {
+      const int w = threadIdx.x >> 6;
+      __syncthreads();
+      if ((threadIdx.x & 63) == 0) lds[w] = v;
+      __syncthreads();
+      v = 0.0f;
+#pragma unroll
+      for (int k = 0; k < NW; ++k) v += lds[k];
+    }
+    return v;
+  }
+  __device__ float max(float v) const {
+#pragma unroll
+    for (int off = (LPR < 64 ? LPR : 64) / 2; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    if constexpr (NW > 1) {
+      const int w = threadIdx.x >> 6;
+      __syncthreads();
+      if ((threadIdx.x & 63) == 0) lds[w] = v;
+      __syncthreads();
+      v = lds[0];
+#pragma unroll
+      for (int k = 1; k < NW; ++k) v = fmaxf(v, lds[k]);
+    }
+    return v;
+  }
+  __device__ void argmax(float& v, int& idx, int* ilds) const {
+#pragma unroll
+    for (int off = (LPR < 64 ? LPR : 64) / 2; off > 0; off >>= 1) {
+      const float v2 = __shfl_xor(v, off, 64);
+      const int i2 = __shfl_xor(idx, off, 64);
+      amax_combine(v, idx, v2, i2);
+    }
+    if constexpr (NW > 1) {
+      const int w = threadIdx.x >> 6;
+      __syncthreads();
+      if ((threadIdx.x & 63) == 0) {
+        lds[w] = v;
+        ilds[w] = idx;
+      }
+      __syncthreads();
+      v = lds[0];
+      idx = ilds[0];
+#pragma unroll
+      for (int k = 1; k < NW; ++k) amax_combine(v, idx, lds[k], ilds[k]);
+    }
+  }
+};
+
+// Register-resident row kernel: row = LPR lanes x VPT float4.  Element j of
+// lane l, vector k sits at column (k * LPR + l) * 4 + j, so every vector load
+// of a lane group is one contiguous, coalesced segment.
+template <int LPR, int VPT, int MODE>
+__global__ __launch_bounds__(LPR >= 256 ? LPR : 256) void row_reg_kernel(RowArgs a) {
+  constexpr int ROWS_PER_BLOCK = LPR >= 256 ? 1 : 256 / LPR;
+  constexpr int NW = LPR > 64 ? LPR / 64 : 1;
+  __shared__ float lds[NW > 1 ? NW : 1];
+  __shared__ int ilds[NW > 1 ? NW : 1];
+  const int sub = LPR >= 256 ? 0 : (int)threadIdx.x / LPR;
+  const int l = LPR >= 256 ? (int)threadIdx.x : (int)threadIdx.x % LPR;
+  const int64_t row = (int64_t)blockIdx.x * ROWS_PER_BLOCK + sub;
+  const bool active = row < a.R;  // uniform across the lanes of a row
+  const RowReducer<LPR> rr{lds};
+  const int64_t C = a.C;
+  const f32x4* xr = reinterpret_cast<const f32x4*>(a.x + (active ? row : 0) * C);
+
+  f32x4 v[VPT];
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) {
+    if (active)
+      v[k] = __builtin_nontemporal_load(xr + k * LPR + l);
+    else
+      v[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  if constexpr (MODE == MODE_SUM) {
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) s += (v[k][0] + v[k][1]) + (v[k][2] + v[k][3]);
+    s = rr.sum(s);
+    if (active && l == 0) a.rsum[row] = s;
+    return;
+  }
+
+  float mx = v[0][0];
+#pragma unroll
+  for (int k = 0; k < VPT; ++k)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) mx = fmaxf(mx, v[k][j]);
+
+  if constexpr (MODE == MODE_MAX) {
+    mx = rr.max(mx);
+    if (active && l == 0) a.rmax[row] = mx;
+    return;
+  }
+
+  int amx_idx = 0;
+  if constexpr (MODE == MODE_XENT) {
+    // first index of the lane's maximum, then a tie-aware reduction
+    float bv = v[0][0];
+    int bi = l * 4;
+#pragma unroll
+    for (int k = 0; k < VPT; ++k)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int col = (k * LPR + l) * 4 + j;
+        if (v[k][j] > bv) {
+          bv = v[k][j];
+          bi = col;
+        }
+      }
+    rr.argmax(bv, bi, ilds);
+    mx = bv;
+    amx_idx = bi;
+  } else {
+    mx = rr.max(mx);
+  }
+
+  float se = 0.0f, sx = 0.0f;
+#pragma unroll
+  for (int k = 0; k < VPT; ++k)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (MODE == MODE_SOFTMAX) sx += v[k][j];
+      const float e = __expf(v[k][j] - mx);
+      v[k][j] = e;
+      se += e;
+    }
+  se = rr.sum(se);
+  if constexpr (MODE == MODE_SOFTMAX) {
+    if (a.rsum) sx = rr.sum(sx);
+  }
+  const float inv = 1.0f / se;
+
+  f32x4* yr = reinterpret_cast<f32x4*>(a.y + (active ? row : 0) * C);
+  if constexpr (MODE == MODE_SOFTMAX) {
+    if (!active) return;
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+      f32x4 o;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[j] = v[k][j] * inv;
+      __builtin_nontemporal_store(o, yr + k * LPR + l);
+    }
+    if (l == 0) {
+      if (a.rmax) a.rmax[row] = mx;
+      if (a.rsum) a.rsum[row] = sx;
+    }
+  } else {  // MODE_XENT
+    if (!active) return;
+    const int lab = a.labels[row];
+    const bool valid = lab >= 0 && (int64_t)lab < C;
+    const float s = a.inv_batch;
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+      f32x4 o;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int col = (k * LPR + l) * 4 + j;
+        const float p = v[k][j] * inv;
+        o[j] = (p - (col == lab ? 1.0f : 0.0f)) * s;
+      }
+      yr[k * LPR + l] = o;
+    }
+    if (l == 0) {
+      a.argmax[row] = amx_idx;
+      // loss_i = log(sum exp(z - m)) + m - z[label]
+      a.row_loss[row] = valid ? (logf(se) + mx - a.x[row * C + lab]) : __builtin_nanf("");
+    }
+  }
+}
+
+// Looping row kernel for any C (one workgroup of 256 lanes per row).
+// Pass 1 computes max (and argmax / sum), pass 2 the exp-sum, pass 3 writes.
+template <int MODE>
+__global__ __launch_bounds__(256) void row_loop_kernel(RowArgs a) {
+  __shared__ float lds[4];
+  __shared__ int ilds[4];
+  const RowReducer<256> rr{lds};
+  const int64_t row = blockIdx.x;
+  const int64_t C = a.C;
+  const float* xr = a.x + row * C;
+  const int t = threadIdx.x;
+
+  if constexpr (MODE == MODE_SUM) {
+    float s = 0.0f;
+    for (int64_t c = t; c < C; c += 256) s += xr[c];
+    s = rr.sum(s);
+    if (t == 0) a.rsum[row] = s;
+    return;
+  }
+  float mx = -INFINITY;
+  int bi = INT32_MAX;
+  float sx = 0.0f;
+  for (int64_t c = t; c < C; c += 256) {
+    const float x = xr[c];
+    if (MODE == MODE_SOFTMAX) sx += x;
+    if (MODE == MODE_XENT) {
+      if (x > mx || bi == INT32_MAX) {
+        mx = x;
+        bi = (int)c;
+      }
+    } else {
+      mx = fmaxf(mx, x);
+    }
+  }
+  if constexpr (MODE == MODE_XENT) {
+    if (bi == INT32_MAX) mx = -INFINITY;
+    rr.argmax(mx, bi, ilds);
+  } else {
+    mx = rr.max(mx);
+  }
+  if constexpr (MODE == MODE_MAX) {
+    if (t == 0) a.rmax[row] = mx;
+    return;
+  }
+  float se = 0.0f;
+  for (int64_t c = t; c < C; c += 256) se += __expf(xr[c] - mx);
+  se = rr.sum(se);
+  if constexpr (MODE == MODE_SOFTMAX) {
+    if (a.rsum) sx = rr.sum(sx);
+  }
+  const float inv = 1.0f / se;
+  float* yr = a.y + row * C;
+  if constexpr (MODE == MODE_SOFTMAX) {
+    for (int64_t c = t; c < C; c += 256) yr[c] = __expf(xr[c] - mx) * inv;
+    if (t == 0) {
+      if (a.rmax) a.rmax[row] = mx;
+      if (a.rsum) a.rsum[row] = sx;
+    }
+  } else {
+    const int lab = a.labels[row];
+    const bool valid = lab >= 0 && (int64_t)lab < C;
+    for (int64_t c = t; c < C; c += 256)
+      yr[c] = (__expf(xr[c] - mx) * inv - (c == lab ? 1.0f : 0.0f)) * a.inv_batch;
+    if (t == 0) {
+      a.argmax[row] = bi;
+      a.row_loss[row] = valid ? (logf(se) + mx - xr[lab]) : __builtin_nanf("");
+    }
+  }
+}
+
+// Mean of the per-row losses in a fixed order (one workgroup, fp64 accumulate).
+__global__ __launch_bounds__(256) void mean_kernel(const float* __restrict__ v, int64_t n,
+                                                   float* __restrict__ out) {
+  __shared__ double red[4];
+  double acc = 0.0;
+  for (int64_t i = threadIdx.x; i < n; i += 256) acc += (double)v[i];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) out[0] = (float)(((red[0] + red[1]) + (red[2] + red[3])) / (double)n);
+}
+
+// Picks a register-resident configuration when C is one of the row widths
+// it covers, else the looping kernel.
+template <int MODE>
+Status launch_rows(const RowArgs& a, void* stream) {
+  hipStream_t s = as_stream(stream);
+  const int64_t R = a.R, C = a.C;
+  const bool al = aligned(a.x, 16) && (a.y == nullptr || aligned(a.y, 16));
+#define ROW_CASE(LPR, VPT)                                                                  \
+  if (al && C == (int64_t)(LPR) * (VPT) * 4) {                                               \
+    constexpr int RPB = (LPR) >= 256 ? 1 : 256 / (LPR);                                       \
+    constexpr int THREADS = (LPR) >= 256 ? (LPR) : 256;                                       \
+    static_assert(THREADS <= 1024, "row too wide");                                          \
+    row_reg_kernel<LPR, VPT, MODE><<<(unsigned)((R + RPB - 1) / RPB), THREADS, 0, s>>>(a);  \
+    return launch_status("row_kernel");                                                      \
+  }
+  ROW_CASE(16, 1)     // C = 64
+  ROW_CASE(32, 1)     // C = 128
+  ROW_CASE(32, 2)     // C = 256
+  ROW_CASE(64, 2)     // C = 512
+  ROW_CASE(64, 4)     // C = 1024
+  ROW_CASE(64, 8)     // C = 2048
+  ROW_CASE(256, 4)    // C = 4096
+  ROW_CASE(256, 8)    // C = 8192
+  ROW_CASE(512, 8)    // C = 16384
+  ROW_CASE(1024, 8)   // C = 32768
+#undef ROW_CASE
+  row_loop_kernel<MODE><<<(unsigned)R, 256, 0, s>>>(a);
+  return launch_status("row_loop_kernel");
+}
+
+bool rows_f32(const TensorDesc& X, int64_t* R, int64_t* C) {
+  if (dt(X) != DType::kF32 || !X.contiguous) return false;
+  if (X.rank == 1) {
+    *R = 1;
+    *C = X.shape[0];
+    return *C > 0;
+  }
+  return rows_cols(X, R, C);
+}
+bool vec_f32(const TensorDesc& t, int64_t n) {
+  return dt(t) == DType::kF32 && t.contiguous && numel_of(t) == n && t.rank >= 1;
+}
+
+// ---- RowSoftmax: X -> Y [, rowmax [, rowsum]] -----------------------------
+bool softmax_sup(const TensorDesc* in, int ni, const TensorDesc* out, int no, const void*) {
+  if (!in || !out || ni != 1 || no < 1 || no > 3) return false;
+  int64_t R, C;
+  if (!rows_f32(in[0], &R, &C)) return false;
+  if (dt(out[0]) != DType::kF32 || !out[0].contiguous || !same_shape(in[0], out[0])) return false;
+  for (int k = 1; k < no; ++k)
+    if (!vec_f32(out[k], R)) return false;
+  return true;
+}
+Status softmax_launch(const TensorDesc* in, int ni, TensorDesc* out, int no, const void* at, void*,
+                      size_t, void* s) {
+  if (!softmax_sup(in, ni, out, no, at)) return Status::InvalidArgument;
+  RowArgs a{};
+  rows_f32(in[0], &a.R, &a.C);
+  a.x = (const float*)in[0].data;
+  a.y = (float*)out[0].data;
+  a.rmax = no >= 2 ? (float*)out[1].data : nullptr;
+  a.rsum = no >= 3 ? (float*)out[2].data : nullptr;
+  return launch_rows<MODE_SOFTMAX>(a, s);
+}
+
+// ---- RowReduce: X -> out[R], schema RRED <i> (0 = sum, 1 = max) ------------
+int read_rred(const void* attr) {
+  const AttrBlob& a = blob(attr);
+  if (a.schema_id != AICF_SCHEMA_RRED || !payload_ok(a, 4)) return 0;
+  return field<int32_t>(a, 0);
+}
+bool row_reduce_sup(const TensorDesc* in, int ni, const TensorDesc* out, int no, const void* attr) {
+  if (!in || !out || ni != 1 || no != 1) return false;
+  const int op = read_rred(attr);
+  if (op != 0 && op != 1) return false;
+  int64_t R, C;
+  return rows_f32(in[0], &R, &C) && vec_f32(out[0], R);
+}
+Status row_reduce_launch(const TensorDesc* in, int ni, TensorDesc* out, int no, const void* at,
+                         void*, size_t, void* s) {
+  if (!row_reduce_sup(in, ni, out, no, at)) return Status::InvalidArgument;
+  RowArgs a{};
+  rows_f32(in[0], &a.R, &a.C);
+  a.x = (const float*)in[0].data;
+  if (read_rred(at) == 0) {
+    a.rsum = (float*)out[0].data;
+    return launch_rows<MODE_SUM>(a, s);
+  }
+  a.rmax = (float*)out[0].data;
+  return launch_rows<MODE_MAX>(a, s);
+}
+
+// ---- SoftmaxXent: (logits [B,C] f32, labels [B] i32) ->
+//      (loss f32 scalar, dlogits [B,C] f32, argmax [B] i32, row_loss [B] f32)
+bool xent_sup(const TensorDesc* in, int ni, const TensorDesc* out, int no, const void*) {
+  if (!in || !out || ni != 2 || no != 4) return false;
+  int64_t B, C;
+  if (!rows_f32(in[0], &B, &C) || in[0].rank != 2) return false;
+  const TensorDesc& L = in[1];
+  if (dt(L) != DType::kI32 || !L.contiguous || L.rank != 1 || L.shape[0] != B) return false;
+  if (dt(out[0]) != DType::kF32 || numel_of(out[0]) != 1) return false;
+  if (dt(out[1]) != DType::kF32 || !out[1].contiguous || !same_shape(out[1], in[0])) return false;
+  const TensorDesc& A = out[2];
+  if (dt(A) != DType::kI32 || !A.contiguous || numel_of(A) != B) return false;
+  if (C > INT32_MAX) return false;
+  return vec_f32(out[3], B);
+}
+Status xent_launch(const TensorDesc* in, int ni, TensorDesc* out, int no, const void* at, void*,
+                   size_t, void* s) {
+  if (!xent_sup(in, ni, out, no, at)) return Status::InvalidArgument;
+  RowArgs a{};
+  rows_f32(in[0], &a.R, &a.C);
+  a.x = (const float*)in[0].data;
+  a.labels = (const int32_t*)in[1].data;
+  a.y = (float*)out[1].data;
+  a.argmax = (int32_t*)out[2].data;
+  a.row_loss = (float*)out[3].data;
+  a.inv_batch = 1.0f / (float)a.R;
+  Status st = launch_rows<MODE_XENT>(a, s);
+  if (st != Status::Ok) return st;
+  mean_kernel<<<1, 256, 0, as_stream(s)>>>(a.row_loss, a.R, (float*)out[0].data);
+  return launch_status("softmax_xent_mean");
+}
+
+}  // namespace
+
+// Direct C++ API counterpart of reduce_sum/api.hpp:6.
+Status reduce_sum_lastdim_f32(const float* dY, float* dB, int M, int N, void* stream) {
+  if (!dY || !dB || M <= 0 || N <= 0) return Status::InvalidArgument;
+  return colsum_run<float, false, false>(dY, dB, nullptr, 1, M, N, stream,
+                                         "reduce_sum_lastdim_f32");
+}
+
+KernelVariant make_reduce_sum_lastdim_f32_variant() {
+  return make("reduce_sum_cols_f32", colsum_f32_launch, colsum_f32_sup);
+}
+KernelVariant make_reduce_sum_lastdim_f16_to_f32_variant() {
+  return make("reduce_sum_cols_f16_f32", colsum_f16_f32_launch, colsum_f16_f32_sup);
+}
+KernelVariant make_reduce_sum_lastdim_f16_variant() {
+  return make("reduce_sum_cols_f16", colsum_f16_f16_launch, colsum_f16_f16_sup);
+}
+KernelVariant make_reduce_sum_lastdim_bf16_to_f32_variant() {
+  return make("reduce_sum_cols_bf16_f32", colsum_bf16_f32_launch, colsum_bf16_f32_sup);
+}
+KernelVariant make_row_softmax_f32_variant() {
+  return make("row_softmax_f32", softmax_launch, softmax_sup);
+}
+KernelVariant make_row_reduce_f32_variant() {
+  return make("row_reduce_f32", row_reduce_launch, row_reduce_sup);
+}
+KernelVariant make_softmax_xent_f32_variant() {
+  return make("softmax_xent_f32", xent_launch, xent_sup);
+}
+
+}  // namespace aicf::hip
+
+extern "C" int32_t aicf_reduce_sum_lastdim_f32(const float* dY, float* dB, int32_t M, int32_t N,
+                                               void* stream) {
+  return static_cast<int32_t>(aicf::hip::reduce_sum_lastdim_f32(dY, dB, M, N, stream));
+}

@@ -1,0 +1,297 @@
+"""Lowering of the IR to the backend's primitive ops, plus the two
+compile-time rewrites of the reference pipeline:
+
+* StageA  lower_to_backend_ops  (reference core_v2/lower.py:24-147)
+    Linear    -> gemm(transB=True) + in-place bias_add
+    LinearBwd -> gemm dX = dY.W, gemm dW = dY^T.X, reduce_sum(axis 0) for db
+    Save      -> copy_saved;  other ops map one to one
+  and the ops this backend appends (GELU, softmax cross-entropy, fused MSE
+  loss, AdamW with in-kernel bias correction, row softmax / reduce).
+* StageC  fuse_gemm_epilogue    (reference rewrites/stageC_fuse_epilogue.py:5-76)
+    gemm [-> bias_add in place] -> relu  ==> gemm_epilogue (bias_relu/relu)
+  extended with gemm -> bias_add -> gelu (==> bias_gelu, keeping the
+  pre-activation when a later gelu_bwd needs it) and gemm -> gelu_bwd
+  (==> dgelu epilogue).
+* StageB  apply_kernel_selection (reference kernel_select.py:22-142 and the
+  vec2/half2 upgrades of plan.py:371-444): pins a kernel_id on every op.
+
+A lowered op is a dict {op, inputs, outputs, attrs[, kernel_id]} - the
+format the reference executor consumes (lower.py:9-21, exec.py:393-453).
+"""
+from __future__ import annotations
+
+from typing import Any, Dict, List, Optional
+
+from .ir import IRGraph
+
+Lowered = List[Dict[str, Any]]
+
+_PRIMITIVES = {
+    "gemm", "gemm_epilogue", "bias_add", "add", "relu", "reduce_sum", "mse_grad", "relu_bwd",
+    "copy", "copy_saved", "copy_aux", "grad_zero", "adam_step", "step_inc", "bias_corr",
+    "sgd_step", "gelu", "gelu_bwd", "softmax_xent", "row_softmax", "row_reduce", "mse_loss",
+    "adamw_step", "layernorm_fwd", "layernorm_bwd", "batchnorm_fwd", "batchnorm_bwd",
+}
+
+_ALIASES = {"adamstep": "adam_step", "stepinc": "step_inc", "biascorr": "bias_corr",
+            "msegrad": "mse_grad", "relubwd": "relu_bwd", "sgdstep": "sgd_step",
+            "linearbwd": "linear_bwd", "gelubwd": "gelu_bwd", "softmaxxent": "softmax_xent",
+            "mseloss": "mse_loss", "adamwstep": "adamw_step", "rowsoftmax": "row_softmax",
+            "rowreduce": "row_reduce"}
+
+
+def _item(op: str, inputs, outputs, attrs=None) -> Dict[str, Any]:
+    return {"op": str(op).strip().lower(), "inputs": [int(x) for x in inputs],
+            "outputs": [int(y) for y in outputs], "attrs": dict(attrs or {})}
+
+
+def lower_to_backend_ops(ir: IRGraph) -> Lowered:
+    """StageA: semantics-preserving lowering; no kernel ids yet."""
+    out: Lowered = []
+    for n in ir.nodes:
+        op = str(n.op).strip().lower()
+        op = _ALIASES.get(op, op)
+        ins, outs, attrs = list(n.inputs), list(n.outputs), dict(n.attrs)
+        if op == "linear":
+            x, w, y = ins[0], ins[1], outs[0]
+            out.append(_item("gemm", [x, w], [y], {"transB": True}))
+            if attrs.get("bias", False) and len(ins) >= 3:
+                out.append(_item("bias_add", [y, ins[2]], [y]))
+        elif op == "linear_bwd":
+            x, w, dy = ins[0], ins[1], ins[2]
+            dx, dw = outs[0], outs[1]
+            if attrs.get("need_dx", True):
+                out.append(_item("gemm", [dy, w], [dx], {"transA": False, "transB": False}))
+            out.append(_item("gemm", [dy, x], [dw], {"transA": True, "transB": False}))
+            if attrs.get("bias", False) and len(outs) >= 3:
+                rs_outs = [outs[2]] + ([int(attrs["db_workspace"])] if "db_workspace" in attrs else [])
+                out.append(_item("reduce_sum", [dy], rs_outs, {"axis": 0, "keepdim": False}))
+        elif op == "save":
+            out.append(_item("copy_saved", [ins[0]], [outs[0]]))
+        elif op in ("relu", "mse_grad", "relu_bwd", "sgd_step") or op in _PRIMITIVES:
+            out.append(_item(op, ins, outs, attrs))
+        else:
+            raise RuntimeError(f"[lower] unsupported IR op '{n.op}' (normalized='{op}')")
+    return out
+
+
+def _refs(it: Dict[str, Any], vid: int) -> bool:
+    return vid in it.get("inputs", []) or vid in it.get("outputs", [])
+
+
+def fuse_gemm_epilogue(ir: IRGraph, lowered: Lowered, *, fuse_bias: bool = False) -> Lowered:
+    """StageC: fold the activation (and an in-place bias add) that consumes a
+    GEMM output into the GEMM.  As in the reference rewrite, the bias add and
+    relu must follow the GEMM directly; a gelu_bwd may come later as long as
+    nothing in between touches the GEMM output."""
+    out: Lowered = []
+    lowered = list(lowered)
+    consumed = set()
+    i = 0
+    kind = lambda it: str(it.get("op", "")).strip().lower()  # noqa: E731
+    while i < len(lowered):
+        if i in consumed:
+            i += 1
+            continue
+        g = lowered[i]
+        if kind(g) != "gemm" or len(g["outputs"]) != 1:
+            out.append(g)
+            i += 1
+            continue
+        y = int(g["outputs"][0])
+        j = i + 1
+        bias = None
+        if j < len(lowered) and kind(lowered[j]) == "bias_add":
+            b = lowered[j]
+            if len(b["inputs"]) == 2 and int(b["inputs"][0]) == y and b["outputs"] == [y]:
+                bias = b
+                j += 1
+        act = lowered[j] if j < len(lowered) else None
+        if bias is None and act is not None and not _refs(act, y):
+            # first later op touching y may be a gelu_bwd(y, z)
+            k = j
+            while k < len(lowered) and not _refs(lowered[k], y):
+                k += 1
+            if k < len(lowered) and kind(lowered[k]) == "gelu_bwd" and lowered[k]["inputs"][0] == y \
+                    and not any(_refs(lowered[q], y) for q in range(k + 1, len(lowered))):
+                attrs = dict(g.get("attrs", {}))
+                attrs["epilogue_act"] = "dgelu"
+                attrs["epilogue_bias"] = False
+                out.append({"op": "gemm_epilogue", "inputs": list(g["inputs"]) + [int(lowered[k]["inputs"][1])],
+                            "outputs": list(lowered[k]["outputs"]), "attrs": attrs})
+                consumed.add(k)
+                i += 1
+                continue
+        attrs = dict(g.get("attrs", {}))
+        if act is not None and kind(act) == "relu" and act["inputs"] == [y]:
+            attrs["epilogue_act"] = "relu"
+            attrs["epilogue_bias"] = bias is not None
+            ins = list(g["inputs"]) + ([int(bias["inputs"][1])] if bias else [])
+            out.append({"op": "gemm_epilogue", "inputs": ins, "outputs": list(act["outputs"]),
+                        "attrs": attrs})
+            i = j + 1
+        elif act is not None and kind(act) == "gelu" and act["inputs"] == [y]:
+            attrs["epilogue_act"] = "gelu"
+            attrs["epilogue_bias"] = bias is not None
+            ins = list(g["inputs"]) + ([int(bias["inputs"][1])] if bias else [])
+            outs = list(act["outputs"])
+            if act.get("attrs", {}).get("save_preact", False):
+                outs.append(y)  # keep the pre-activation for gelu_bwd
+            out.append({"op": "gemm_epilogue", "inputs": ins, "outputs": outs, "attrs": attrs})
+            i = j + 1
+        elif (bias is None and act is not None and kind(act) == "gelu_bwd"
+              and act["inputs"][0] == y):
+            attrs["epilogue_act"] = "dgelu"
+            attrs["epilogue_bias"] = False
+            ins = list(g["inputs"]) + [int(act["inputs"][1])]
+            out.append({"op": "gemm_epilogue", "inputs": ins, "outputs": list(act["outputs"]),
+                        "attrs": attrs})
+            i = j + 1
+        elif bias is not None and fuse_bias:
+            # bias only (off by default: the reference fuses only with relu)
+            attrs["epilogue_act"] = "none"
+            attrs["epilogue_bias"] = True
+            out.append({"op": "gemm_epilogue", "inputs": list(g["inputs"]) + [int(bias["inputs"][1])],
+                        "outputs": [y], "attrs": attrs})
+            i = j
+        else:
+            out.append(g)
+            i += 1
+    return out
+
+
+# ---------------------------------------------------------------- StageB
+def _dt(ir: IRGraph, vid: int) -> str:
+    return str(ir.values[int(vid)].dtype)
+
+
+def _is(ds: str, kind: str) -> bool:
+    if kind == "f16":
+        return "float16" in ds and "bfloat16" not in ds
+    return kind in ds
+
+
+def _numel(ir: IRGraph, vid: int) -> int:
+    n = 1
+    for d in ir.values[int(vid)].shape:
+        n *= int(d)
+    return n
+
+
+def pick_kernel_id(ir: IRGraph, it: Dict[str, Any]) -> Optional[str]:
+    op = str(it["op"]).strip().lower()
+    ins, outs = it.get("inputs", []), it.get("outputs", [])
+    attrs = it.get("attrs", {}) or {}
+    in0 = _dt(ir, ins[0]) if ins else ""
+    out0 = _dt(ir, outs[0]) if outs else ""
+    f16 = _is(in0, "f16") or _is(out0, "f16")
+    bf16 = _is(in0, "bfloat16") or _is(out0, "bfloat16")
+    last = ir.values[int(outs[0])].shape[-1] if outs and ir.values[int(outs[0])].shape else 1
+    even_last = int(last) % 2 == 0
+    if op == "gemm_epilogue":
+        if f16:
+            return "gemm_bias_relu_f16_tc_wmma_out_f16_v0"
+        if bf16:
+            return "gemm_epilogue_bf16_mfma_f32out_v0" if _is(out0, "float32") else \
+                "gemm_epilogue_bf16_mfma_v0"
+        act = str(attrs.get("epilogue_act", "relu"))
+        return "gemm_bias_relu_f32_naive_v0" if act == "relu" else "gemm_epilogue_f32_mfma_v0"
+    if op == "gemm":
+        if f16:
+            return "gemm_f16_tc_wmma_out_f16_v0"
+        if bf16:
+            return "gemm_bf16_mfma_f32out_v0" if _is(out0, "float32") else "gemm_bf16_mfma_v0"
+        return "gemm_f32_naive_v0"
+    if op == "bias_add":
+        return ("bias_add_f16_vec2_v0" if even_last else "bias_add_f16_v0") if f16 else "bias_add_f32_v0"
+    if op == "add":
+        return ("add_f16_vec2_v0" if even_last else "add_f16_v0") if f16 else "add_f32_v0"
+    if op == "relu":
+        return ("relu_f16_vec2_v0" if even_last else "relu_f16_v0") if f16 else "relu_f32_v0"
+    if op == "relu_bwd":
+        return ("relu_bwd_f16_vec2_v0" if even_last else "relu_bwd_f16_v0") if f16 else "relu_bwd_f32_v0"
+    if op == "mse_grad":
+        return "mse_grad_f16_v0" if f16 else "mse_grad_f32_v0"
+    if op == "mse_loss":
+        return "mse_loss_grad_v0"
+    if op == "reduce_sum":
+        if _is(out0, "f16"):
+            return "reduce_sum_keep_lastdim_f16_v0"
+        if _is(in0, "f16"):
+            return "reduce_sum_keep_lastdim_f16_to_f32_v0"
+        if _is(in0, "bfloat16"):
+            return "reduce_sum_keep_lastdim_bf16_to_f32_v0"
+        return "reduce_sum_keep_lastdim_f32_v0"
+    if op == "sgd_step":
+        if f16:
+            return "sgd_step_f16_half2_v0" if _numel(ir, outs[0]) % 2 == 0 else "sgd_step_f16_v0"
+        return "sgd_step_f32_v0"
+    if op in ("copy", "copy_saved", "copy_aux"):
+        return "copy_f16_v0" if f16 else ("copy_bf16_v0" if bf16 else "copy_f32_v0")
+    if op == "grad_zero":
+        return "grad_zero_v0"
+    if op == "adam_step":
+        return "adam_step_f32_v0"
+    if op == "adamw_step":
+        return "adamw_step_f32_v1"
+    if op == "step_inc":
+        return "step_inc_v0"
+    if op == "bias_corr":
+        return "bias_corr_v0"
+    if op == "gelu":
+        return "gelu_bf16_v0" if bf16 else "gelu_f32_v0"
+    if op == "gelu_bwd":
+        return "gelu_bwd_bf16_v0" if bf16 else "gelu_bwd_f32_v0"
+    if op == "softmax_xent":
+        return "softmax_xent_f32_v0"
+    if op == "row_softmax":
+        return "row_softmax_f32_v0"
+    if op == "row_reduce":
+        return "row_reduce_f32_v0"
+    if op in ("layernorm_fwd", "layernorm_bwd"):
+        return f"{op}_{'f16' if f16 else 'f32'}_v0"
+    if op in ("batchnorm_fwd", "batchnorm_bwd"):
+        return f"{op}_f16_v0"
+    return None
+
+
+def apply_kernel_selection(ir: IRGraph, lowered: Lowered) -> Lowered:
+    """StageB: attach a kernel_id to every op that lacks one."""
+    out: Lowered = []
+    for it in lowered:
+        it = dict(it)
+        if it.get("kernel_id") is None:
+            kid = pick_kernel_id(ir, it)
+            if kid is not None:
+                it["kernel_id"] = kid
+        out.append(it)
+    return out
+
+
+def compile_lowered(ir: IRGraph, *, fuse: bool = True, fuse_bias: bool = False) -> Lowered:
+    """StageA -> StageC -> StageB."""
+    low = lower_to_backend_ops(ir)
+    if fuse:
+        low = fuse_gemm_epilogue(ir, low, fuse_bias=fuse_bias)
+    return apply_kernel_selection(ir, low)
+
+
+def _fmt_attr(v: Any) -> str:
+    return str(v)
+
+
+def lowered_to_text(lowered: Lowered, name: str) -> str:
+    """Text dump in the layout of the reference's 30_lowered.txt artifact."""
+    lines = [f"=== LoweredOps({name}) ===", f"ops: {len(lowered)}", ""]
+    for i, it in enumerate(lowered):
+        ins = ", ".join(str(x) for x in it["inputs"])
+        outs = ", ".join(str(y) for y in it["outputs"])
+        ins = f"({ins})" if len(it["inputs"]) != 1 else f"({ins})"
+        s = f"  #{i:03d} {it['op']:<10} {ins} -> ({outs})"
+        attrs = it.get("attrs") or {}
+        if attrs:
+            s += "  {" + ", ".join(f"{k}={_fmt_attr(attrs[k])}" for k in sorted(attrs)) + "}"
+        if it.get("kernel_id"):
+            s += f"  kid={it['kernel_id']}"
+        lines.append(s)
+    return "\n".join(lines)

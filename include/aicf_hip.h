@@ -1,0 +1,207 @@
+/*
+ * aicf_hip.h — C-ABI of the MI355X (gfx950) op backend and plan runtime.
+ *
+ * This is the drop-in boundary that replaces the reference's CUDA backend
+ * behind its unchanged kernel-registry / op-dispatch API and its
+ * `aicf_cuda._C` Python bindings.  Only plain C types cross it: POD structs,
+ * pointers, sizes and int32 status codes.  No torch or HIP types appear in
+ * any signature; streams are passed as opaque `void*` (a `hipStream_t`).
+ *
+ * Reference paths below are relative to ai-compiler-framework/ in the
+ * reference tree.
+ */
+#ifndef AICF_HIP_H
+#define AICF_HIP_H
+
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------------ */
+/* Value types                                                               */
+/* ------------------------------------------------------------------------ */
+
+/* Replaces include/aicf/backends/cuda/registry/tensor_desc.hpp:8 (kMaxRank). */
+#define AICF_MAX_RANK 4
+
+/* Replaces tensor_desc.hpp:13-27 (enum class DType : uint8_t); same values. */
+#define AICF_DTYPE_UNKNOWN 0
+#define AICF_DTYPE_F32 1
+#define AICF_DTYPE_F16 2
+#define AICF_DTYPE_BF16 3
+#define AICF_DTYPE_I32 4
+
+/* Replaces registry/status.hpp:6-11 (enum class Status : int32_t); same values. */
+#define AICF_STATUS_OK 0
+#define AICF_STATUS_INVALID_ARGUMENT 1
+#define AICF_STATUS_NOT_IMPLEMENTED 2
+#define AICF_STATUS_INTERNAL 3
+
+/*
+ * Replaces registry/op_kind.hpp:5-31 (enum class OpKind : int).  Values 0..17
+ * are identical; 18.. are appended kinds for ops the reference lacks.
+ */
+#define AICF_OP_ELTWISE_ADD 0
+#define AICF_OP_ELTWISE_RELU 1
+#define AICF_OP_GEMM 2
+#define AICF_OP_BIAS_ADD 3
+#define AICF_OP_REDUCE_SUM 4
+#define AICF_OP_MSE_GRAD 5
+#define AICF_OP_RELU_BWD 6
+#define AICF_OP_SGD_STEP 7
+#define AICF_OP_COPY 8
+#define AICF_OP_GRAD_ZERO 9
+#define AICF_OP_ADAM_STEP 10
+#define AICF_OP_STEP_INC 11
+#define AICF_OP_BIAS_CORR 12
+#define AICF_OP_LAYERNORM_FWD 13 /* reserved: no variant registered */
+#define AICF_OP_LAYERNORM_BWD 14 /* reserved: no variant registered */
+#define AICF_OP_BATCHNORM_FWD 15 /* reserved: no variant registered */
+#define AICF_OP_BATCHNORM_BWD 16 /* reserved: no variant registered */
+#define AICF_OP_GEMM_EPILOGUE 17
+/* appended kinds (no counterpart in the reference) */
+#define AICF_OP_ROW_SOFTMAX 18  /* X[R,C] -> softmax Y (+ row max, row sum of X) */
+#define AICF_OP_ROW_REDUCE 19   /* X[R,C] -> per-row sum or max (schema RRED) */
+#define AICF_OP_SOFTMAX_XENT 20 /* logits, labels -> loss, dlogits, argmax, row loss */
+#define AICF_OP_GELU_BWD 21     /* dOut, Z -> dOut * gelu_tanh'(Z) */
+#define AICF_OP_ELTWISE_GELU 22 /* X -> gelu_tanh(X) */
+#define AICF_OP_COUNT 23
+
+/*
+ * Attribute schema ids (numeric ABI).  The reference mixes big-endian fourccs
+ * (GEMM, GPEL, RSUM) with little-endian ones (the rest); the numbers are kept.
+ */
+#define AICF_SCHEMA_GEMM 0x47454D4Du /* gemm/launcher.cu:41          <ii>  transA, transB */
+#define AICF_SCHEMA_GPEL 0x4750454Cu /* gemm_epilogue/launcher.cu:49 <iii> transA, transB, relu */
+#define AICF_SCHEMA_GEPI 0x49504547u /* core_v2/exec.py:215-217      <iii> transA, transB, epilogue kind */
+#define AICF_SCHEMA_RSUM 0x5253554Du /* reduce_sum/launcher.cu:75    <q>   axis */
+#define AICF_SCHEMA_MSEG 0x4745534Du /* mse_grad/launcher.cu:36      <f>   scale */
+#define AICF_SCHEMA_BADD 0x44444142u /* bias_add/launcher.cu:97      <q>   axis */
+#define AICF_SCHEMA_ADAM 0x4D414441u /* adam_step/launcher.cu:32     <ffff> lr,b1,b2,eps (+<f> wd) */
+#define AICF_SCHEMA_BCOR 0x524F4342u /* biascorr/launcher.cu:31      <ff>  beta1, beta2 */
+#define AICF_SCHEMA_SGDS 0x53444753u /* sgd_step/launcher.cu:31      <f>   lr */
+#define AICF_SCHEMA_RRED 0x44455252u /* appended: b"RRED" little-endian, <i> 0=sum 1=max */
+
+/* GEPI epilogue kinds.  0..2 are the values core_v2/exec.py:223-252 packs;
+ * 3..5 are appended. */
+#define AICF_EPI_BIAS_RELU 0
+#define AICF_EPI_BIAS 1
+#define AICF_EPI_RELU 2
+#define AICF_EPI_BIAS_GELU 3  /* bias then gelu_tanh; optional 2nd output keeps the pre-activation */
+#define AICF_EPI_GELU 4       /* gelu_tanh, input 2 ignored */
+#define AICF_EPI_DGELU 5      /* out = acc * gelu_tanh'(Z), input 2 is Z[M,N] */
+
+/*
+ * Replaces tensor_desc.hpp:88-158 (struct TensorDesc).  Field order, types
+ * and therefore layout are identical (96 bytes on LP64): `rank` stands for
+ * the reference's one-member union RankND.  shape/stride are in elements.
+ */
+typedef struct aicf_tensor_desc {
+  void* data;
+  uint8_t dtype; /* AICF_DTYPE_* */
+  int32_t rank;
+  int64_t shape[AICF_MAX_RANK];
+  int64_t stride[AICF_MAX_RANK];
+  bool contiguous;
+  int32_t alignment; /* bytes; 0 = unknown */
+  int32_t device;
+} aicf_tensor_desc;
+
+/* Replaces registry/attr_blob.hpp:13-17 (struct AttrBlob); same layout. */
+typedef struct aicf_attr_blob {
+  uint32_t schema_id;
+  uint32_t bytes;
+  const void* data;
+} aicf_attr_blob;
+
+/* ------------------------------------------------------------------------ */
+/* Dispatch                                                                  */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * Replaces aicf::cuda::dispatch_v0 (registry/dispatch.hpp:12-17,
+ * src/backends/cuda/registry/registry.cpp:144-215): priority-ordered variant
+ * selection, first supported() wins.  `attrs` may be NULL (empty blob).
+ * Returns AICF_STATUS_*: NOT_IMPLEMENTED when no variant accepts the call.
+ */
+int32_t aicf_dispatch_v0(int32_t kind, const aicf_tensor_desc* inputs, int32_t num_inputs,
+                         aicf_tensor_desc* outputs, int32_t num_outputs,
+                         const aicf_attr_blob* attrs, void* stream);
+
+/*
+ * Replaces aicf::cuda::dispatch_by_id_v0 (dispatch.hpp:20-26,
+ * registry.cpp:16-64,218-236): run exactly the variant registered under
+ * `kernel_id`.  INVALID_ARGUMENT for an empty id, a schema mismatch or an
+ * unsupported call; NOT_IMPLEMENTED for an unknown id.
+ */
+int32_t aicf_dispatch_by_id_v0(int32_t kind, const char* kernel_id,
+                               const aicf_tensor_desc* inputs, int32_t num_inputs,
+                               aicf_tensor_desc* outputs, int32_t num_outputs,
+                               const aicf_attr_blob* attrs, void* stream);
+
+/* Replaces registry/register_all.hpp:8 (aicf_cuda_register_all_kernels).
+ * Idempotent: registration happens once per process. */
+void aicf_cuda_register_all_kernels(void);
+
+/* Replaces include/aicf/backends/cuda/ops/reduce_sum/api.hpp:6
+ * (reduce_sum_lastdim_f32, implemented at reduce_sum/launcher.cu:494-503):
+ * dB[n] = sum_m dY[m, n] over a row-major [M, N] fp32 matrix. */
+int32_t aicf_reduce_sum_lastdim_f32(const float* dY, float* dB, int32_t M, int32_t N, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Registry introspection (replaces KernelRegistry::variants_snapshot and    */
+/* find_by_id, registry/registry.hpp:39-42)                                  */
+/* ------------------------------------------------------------------------ */
+
+/* Number of variants registered for `kind` (in selection order). */
+int32_t aicf_registry_count(int32_t kind);
+/* kernel_id / priority / expected schema of the idx-th variant, or NULL / -1. */
+const char* aicf_registry_kernel_id(int32_t kind, int32_t idx);
+int32_t aicf_registry_priority(int32_t kind, int32_t idx);
+uint32_t aicf_registry_schema(int32_t kind, int32_t idx);
+/* 1 if `kernel_id` is registered under `kind`, else 0. */
+int32_t aicf_registry_has(int32_t kind, const char* kernel_id);
+
+/* Replaces registry/status.hpp:15-23 (status_to_string) and the OpKind name
+ * table of src/python_bindings/bindings.cpp:196-219. */
+const char* aicf_status_name(int32_t status);
+const char* aicf_opkind_name(int32_t kind);
+
+/* ------------------------------------------------------------------------ */
+/* Graph capture / replay (replaces the CudaGraphState singleton and the     */
+/* graph_* entry points of src/python_bindings/bindings.cpp:137-187,475-547) */
+/* ------------------------------------------------------------------------ */
+
+/* Ends any dangling capture, drops the previous graph, lazily creates the
+ * dedicated non-blocking stream and begins a global-mode capture on it.
+ * The stream handle is written to *out_stream.  Returns AICF_STATUS_*. */
+int32_t aicf_graph_begin(uint64_t* out_stream);
+/* Ends the capture and instantiates the executable graph.  INVALID_ARGUMENT
+ * when no capture is in progress. */
+int32_t aicf_graph_end(void);
+/* Launches the instantiated graph on the dedicated stream.  When
+ * `caller_stream` is non-NULL, the launch first waits on an event recorded
+ * on it, so work queued on the caller's stream (e.g. host-side updates of
+ * device scalars) is ordered before the replay.  INVALID_ARGUMENT when no
+ * graph was captured. */
+int32_t aicf_graph_launch(void* caller_stream);
+/* Ends a dangling capture and destroys the graph objects. */
+int32_t aicf_graph_reset(void);
+/* The dedicated stream (0 before the first aicf_graph_begin). */
+uint64_t aicf_graph_stream(void);
+/* 1 while capturing, 2 when a graph is instantiated, 0 otherwise. */
+int32_t aicf_graph_state(void);
+
+/* Message of the last failing HIP runtime call made by this library on the
+ * calling thread ("" if none). */
+const char* aicf_last_error(void);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* AICF_HIP_H */

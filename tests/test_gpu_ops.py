@@ -1,0 +1,550 @@
+"""GPU parity of every op family against the CPU oracle.
+
+Calls go through aicf_cuda._C (op_call / launch_by_id), which calls the
+C-ABI of libaicf_hip.  Inputs are seeded numpy arrays; expected values come
+from oracle/ (reference-exact fp32 restatements, or fp64 with the
+tolerances of the north star: bit-exact for integer/index work and
+order-free ops, rel-err <= 1e-5 for fp32 softmax/reduce/Adam, <= 1e-4 for
+fp32 GEMM, <= 1e-2 for bf16 GEMM).  Shapes follow the reference probes
+(python/cuda_binding_test/*.py) plus edge cases.
+"""
+from __future__ import annotations
+
+import struct
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+ADAM = int.from_bytes(b"ADAM", "little")
+BCOR = int.from_bytes(b"BCOR", "little")
+SGDS = int.from_bytes(b"SGDS", "little")
+MSEG = int.from_bytes(b"MSEG", "little")
+RSUM = int.from_bytes(b"RSUM", "big")
+BADD = int.from_bytes(b"BADD", "little")
+GEMM = int.from_bytes(b"GEMM", "big")
+GPEL = int.from_bytes(b"GPEL", "big")
+GEPI = int.from_bytes(b"GEPI", "little")
+RRED = int.from_bytes(b"RRED", "little")
+
+
+def g(a, dtype=None):
+    """numpy -> cuda tensor (uint16 arrays are reinterpreted as `dtype`)."""
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        t = torch.from_numpy(a.view(np.int16)).view(dtype or torch.float16)
+    else:
+        t = torch.from_numpy(a)
+    return t.cuda()
+
+
+def h(t):
+    """cuda tensor -> numpy (16-bit floats come back as raw uint16 bits)."""
+    t = t.detach().cpu().contiguous()
+    if t.dtype in (torch.float16, torch.bfloat16):
+        return t.view(torch.int16).numpy().view(np.uint16)
+    return t.numpy()
+
+
+def rng(seed):
+    return np.random.default_rng(seed)
+
+
+# ============================================================== optimizer
+@pytest.mark.parametrize("shape,inplace", [((1024,), False), ((64, 256), False),
+                                           ((8, 32, 128), False), ((64, 256), True),
+                                           ((1001,), False), ((3,), True)])
+def test_adam_reference_contract_bit_exact(C, shape, inplace):
+    # v2_adam_step_probe.py:41-92 shapes; bc = 1 - beta^3 (:53-54)
+    r = rng(1)
+    P, G, M = (r.standard_normal(shape).astype(np.float32) for _ in range(3))
+    V = np.abs(r.standard_normal(shape)).astype(np.float32)
+    lr, b1, b2, eps = 1e-3, 0.9, 0.999, 1e-8
+    bc1, bc2 = np.float32(1 - b1 ** 3), np.float32(1 - b2 ** 3)
+    tP, tG, tM, tV = g(P), g(G), g(M), g(V)
+    outs = [tP, tM, tV] if inplace else [torch.empty_like(tP) for _ in range(3)]
+    C.op_call(int(C.OpKind.AdamStep),
+              [tP, tG, tM, tV, g(np.array(bc1)), g(np.array(bc2))], outs, ADAM,
+              struct.pack("<ffff", lr, b1, b2, eps), 0)
+    Pr, Mr, Vr = orc.adam_ref(P, G, M, V, bc1, bc2, lr, b1, b2, eps)
+    assert np.array_equal(h(outs[0]).ravel(), Pr)
+    assert np.array_equal(h(outs[1]).ravel(), Mr)
+    assert np.array_equal(h(outs[2]).ravel(), Vr)
+    if not inplace:
+        assert np.array_equal(h(tP), P)  # inputs untouched
+
+
+@pytest.mark.parametrize("n,shadow", [(4096, False), (4099, True), (1 << 20, True)])
+def test_adamw_in_kernel_bias_correction(C, n, shadow):
+    r = rng(2)
+    P = (0.02 * r.standard_normal(n)).astype(np.float32)
+    G = (1e-3 * r.standard_normal(n)).astype(np.float32)
+    M = np.zeros(n, np.float32)
+    V = np.zeros(n, np.float32)
+    tP, tG, tM, tV = g(P), g(G), g(M), g(V)
+    step = torch.zeros((), dtype=torch.int32, device="cuda")
+    outs = [tP, tM, tV] + ([torch.empty(n, dtype=torch.bfloat16, device="cuda")] if shadow else [])
+    pay = struct.pack("<fffff", 1e-3, 0.9, 0.999, 1e-8, 0.01)
+    Pc, Mc, Vc = P.copy(), M.copy(), V.copy()
+    for t in range(1, 4):
+        C.launch_by_id("step_inc_v0", C.OpKind.StepInc, [step], [step])
+        C.launch_by_id("adamw_step_f32_v1", C.OpKind.AdamStep, [tP, tG, tM, tV, step], outs,
+                       ADAM, pay)
+        res = orc.adamw(Pc, G, Mc, Vc, t, 1e-3, 0.9, 0.999, 1e-8, 0.01, shadow=shadow)
+        Pc, Mc, Vc = res[0], res[1], res[2]
+    assert int(step.item()) == 3
+    assert np.array_equal(h(tP), Pc)
+    assert np.array_equal(h(tM), Mc)
+    assert np.array_equal(h(tV), Vc)
+    if shadow:
+        assert np.array_equal(h(outs[3]), res[3])
+
+
+@pytest.mark.parametrize("step", [1, 10, 0])
+@pytest.mark.parametrize("rank1", [False, True])
+def test_bias_corr(C, step, rank1):
+    s = torch.tensor([step] if rank1 else step, dtype=torch.int32, device="cuda")
+    shp = (1,) if rank1 else ()
+    o1, o2 = torch.empty(shp, device="cuda"), torch.empty(shp, device="cuda")
+    C.op_call(int(C.OpKind.BiasCorr), [s], [o1, o2], BCOR, struct.pack("<ff", 0.9, 0.999), 0)
+    r1, r2 = orc.bias_corr(step, 0.9, 0.999)
+    # device powf vs host powf: within 2 ulp
+    assert abs(float(o1.item()) - r1) <= 2 * np.spacing(np.float32(r1))
+    assert abs(float(o2.item()) - r2) <= 2 * np.spacing(np.float32(r2))
+
+
+@pytest.mark.parametrize("shape", [(1,), (1024,), (64, 256), ()])
+def test_step_inc(C, shape):
+    s = torch.arange(int(np.prod(shape)) if shape else 1, dtype=torch.int32, device="cuda").reshape(shape)
+    ref = s.clone()
+    C.op_call(int(C.OpKind.StepInc), [s], [s], 0, b"", 0)
+    assert torch.equal(s, ref + 1)
+    # out-of-place increments the output buffer (step_inc/launcher.cu:140-141)
+    o = torch.full_like(s, 7)
+    C.op_call(int(C.OpKind.StepInc), [s], [o], 0, b"", 0)
+    assert torch.equal(o, torch.full_like(s, 8))
+
+
+def test_sgd(C):
+    r = rng(3)
+    for n in (1024, 1023):
+        P = r.standard_normal(n).astype(np.float32)
+        G = r.standard_normal(n).astype(np.float32)
+        tP, tG = g(P), g(G)
+        C.op_call(int(C.OpKind.SgdStep), [tP, tG], [tP], SGDS, struct.pack("<f", 0.01), 0)
+        assert np.array_equal(h(tP), orc.sgd_f32(P, G, 0.01))
+        Ph = P.astype(np.float16).view(np.uint16)
+        Gh = G.astype(np.float16).view(np.uint16)
+        tPh, tGh = g(Ph), g(Gh)
+        C.op_call(int(C.OpKind.SgdStep), [tPh, tGh], [tPh], 0, b"", 0)  # default lr 1e-3
+        assert np.array_equal(h(tPh), orc.sgd_f16(Ph, Gh, 1e-3))
+    with pytest.raises(RuntimeError):
+        C.op_call(int(C.OpKind.SgdStep), [tP, tG], [tG], 0, b"", 0)  # O aliases G
+
+
+# ============================================================== elementwise
+SHAPES = [(1024,), (64, 256), (8, 32, 128), (7, 33, 127)]
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+def test_add_relu_relu_bwd_copy_zero(C, shape):
+    r = rng(4)
+    a = r.standard_normal(shape).astype(np.float32)
+    b = r.standard_normal(shape).astype(np.float32)
+    ta, tb = g(a), g(b)
+    o = torch.empty_like(ta)
+    C.op_call(int(C.OpKind.EltwiseAdd), [ta, tb], [o], 0, b"", 0)
+    assert np.array_equal(h(o).ravel(), orc.add_f32(a, b))
+    C.op_call(int(C.OpKind.EltwiseRelu), [ta], [o], 0, b"", 0)
+    assert np.array_equal(h(o).ravel(), orc.relu_f32(a))
+    C.op_call(int(C.OpKind.ReluBwd), [tb, ta], [o], 0, b"", 0)
+    assert np.array_equal(h(o).ravel(), orc.relu_bwd_f32(b, a))
+    C.op_call(int(C.OpKind.Copy), [ta], [o], 0, b"", 0)
+    assert np.array_equal(h(o), a)
+    C.op_call(int(C.OpKind.GradZero), [o], [o], 0, b"", 0)
+    assert not h(o).any()
+    ah = a.astype(np.float16).view(np.uint16)
+    bh = b.astype(np.float16).view(np.uint16)
+    tah, tbh = g(ah), g(bh)
+    oh = torch.empty_like(tah)
+    C.op_call(int(C.OpKind.EltwiseAdd), [tah, tbh], [oh], 0, b"", 0)
+    assert np.array_equal(h(oh).ravel(), orc.add_f16(ah, bh))
+    C.op_call(int(C.OpKind.EltwiseRelu), [tah], [oh], 0, b"", 0)
+    assert np.array_equal(h(oh).ravel(), orc.relu_f16(ah))
+    C.op_call(int(C.OpKind.ReluBwd), [tbh, tah], [oh], 0, b"", 0)
+    assert np.array_equal(h(oh).ravel(), orc.relu_bwd_f16(bh, ah))
+    C.op_call(int(C.OpKind.Copy), [tah], [oh], 0, b"", 0)
+    assert np.array_equal(h(oh), ah)
+
+
+def test_relu_special_values(C):
+    x = np.array([1.5, -2.0, 0.0, -0.0, np.nan, np.inf, -np.inf, 1e-40], np.float32)
+    tx = g(x)
+    o = torch.empty_like(tx)
+    C.op_call(int(C.OpKind.EltwiseRelu), [tx], [o], 0, b"", 0)
+    assert np.array_equal(h(o).view(np.uint32), orc.relu_f32(x).view(np.uint32))
+
+
+@pytest.mark.parametrize("shape", [(64, 256), (8, 32, 128), (7, 33, 127), (3, 5)])
+def test_bias_add(C, shape):
+    r = rng(5)
+    y = r.standard_normal(shape).astype(np.float32)
+    b = r.standard_normal(shape[-1]).astype(np.float32)
+    ty = g(y)
+    C.op_call(int(C.OpKind.BiasAdd), [ty, g(b)], [ty], BADD, struct.pack("<q", -1), 0)
+    assert np.array_equal(h(ty).ravel(), orc.bias_add_f32(y, b))
+    yh = y.astype(np.float16).view(np.uint16)
+    bh = b.astype(np.float16).view(np.uint16)
+    tyh = g(yh)
+    C.op_call(int(C.OpKind.BiasAdd), [tyh, g(bh)], [tyh], 0, b"", 0)
+    assert np.array_equal(h(tyh).ravel(), orc.bias_add_f16(yh, bh))
+
+
+@pytest.mark.parametrize("shape", [(64, 256), (8, 32, 128), (7, 33, 127)])
+def test_mse_grad(C, shape):
+    r = rng(6)
+    p = r.standard_normal(shape).astype(np.float32)
+    t = r.standard_normal(shape).astype(np.float32)
+    o = torch.empty(shape, device="cuda")
+    C.op_call(int(C.OpKind.MseGrad), [g(p), g(t)], [o], 0, b"", 0)
+    assert np.array_equal(h(o).ravel(), orc.mse_grad_f32(p, t))
+    C.op_call(int(C.OpKind.MseGrad), [g(p), g(t)], [o], MSEG, struct.pack("<f", 0.125), 0)
+    assert np.array_equal(h(o).ravel(), orc.mse_grad_f32(p, t, 0.125))
+    ph = p.astype(np.float16).view(np.uint16)
+    th = t.astype(np.float16).view(np.uint16)
+    oh = torch.empty(shape, dtype=torch.float16, device="cuda")
+    C.op_call(int(C.OpKind.MseGrad), [g(ph), g(th)], [oh], MSEG, struct.pack("<f", 0.125), 0)
+    half = int(np.prod(shape)) % 2 == 0  # the f16 variant's half2 path (mse_grad/launcher.cu:272)
+    assert np.array_equal(h(oh).ravel(), orc.mse_grad_f16(ph, th, 0.125, half_math=half))
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("shape", [(64, 256), (513, 1000), (2048, 4096)])
+def test_mse_loss_grad_fused(C, dtype, shape):
+    r = rng(7)
+    p = r.standard_normal(shape).astype(np.float32)
+    t = r.standard_normal(shape).astype(np.float32)
+    if dtype == "bf16":
+        pb = orc.bf16_bits_from_f32(p)
+        tp = g(pb, torch.bfloat16)
+        p = orc.bf16_bits_to_f32(pb).reshape(shape)
+    else:
+        tp = g(p)
+    d = torch.empty_like(tp)
+    loss = torch.empty((), device="cuda")
+    part = torch.empty(1024, device="cuda")
+    C.launch_by_id("mse_loss_grad_v0", C.OpKind.MseGrad, [tp, g(t)], [d, loss, part])
+    ref = orc.mse_grad_f32(p, t)
+    if dtype == "bf16":
+        assert np.array_equal(h(d).ravel(), orc.bf16_bits_from_f32(ref))
+    else:
+        assert np.array_equal(h(d).ravel(), ref)
+    assert abs(loss.item() - orc.mse_loss_f64(p, t)) / orc.mse_loss_f64(p, t) < 1e-5
+
+
+def test_gelu_and_gelu_bwd(C):
+    r = rng(8)
+    x = (3 * r.standard_normal(100003)).astype(np.float32)
+    d = r.standard_normal(100003).astype(np.float32)
+    o = torch.empty(100003, device="cuda")
+    C.op_call(int(C.OpKind.EltwiseGelu), [g(x)], [o], 0, b"", 0)
+    assert orc.rel_err(h(o), orc.gelu_f64(x.astype(np.float64))) < 1e-5
+    C.op_call(int(C.OpKind.GeluBwd), [g(d), g(x)], [o], 0, b"", 0)
+    assert orc.rel_err(h(o), d * orc.gelu_grad_f64(x.astype(np.float64))) < 1e-5
+    xb = orc.bf16_bits_from_f32(x)
+    ob = torch.empty(100003, dtype=torch.bfloat16, device="cuda")
+    C.op_call(int(C.OpKind.EltwiseGelu), [g(xb, torch.bfloat16)], [ob], 0, b"", 0)
+    ref = orc.gelu_f64(orc.bf16_bits_to_f32(xb).astype(np.float64))
+    assert orc.rel_err(orc.bf16_bits_to_f32(h(ob)), ref) < 8e-3
+
+
+# ============================================================== reductions
+def test_reduce_sum_columns(C):
+    # v2_reduce_sum_probe.py:24-75: f32 128x64 (seed 0), f16->f32 257x64 (seed 1)
+    x = rng(0).standard_normal((128, 64)).astype(np.float32)
+    o = torch.empty(64, device="cuda")
+    C.op_call(int(C.OpKind.ReduceSum), [g(x)], [o], RSUM, struct.pack("<q", 0), 0)
+    assert orc.rel_err(h(o), orc.colsum_f64(x)) < 1e-5
+    xh = rng(1).standard_normal((257, 64)).astype(np.float16)
+    o = torch.empty(64, device="cuda")
+    C.op_call(int(C.OpKind.ReduceSum), [g(xh.view(np.uint16))], [o], 0, b"", 0)
+    assert orc.rel_err(h(o), orc.colsum_f64(xh.astype(np.float32))) < 1e-5
+    oh = torch.empty(64, dtype=torch.float16, device="cuda")
+    C.op_call(int(C.OpKind.ReduceSum), [g(xh.view(np.uint16))], [oh], 0, b"", 0)
+    assert orc.rel_err(orc.f16_bits_to_f64(h(oh)), orc.colsum_f64(xh.astype(np.float32))) < 1e-3
+    # bf16 -> f32 with a partials buffer (two-pass, 8192 x 4096 like the MLP bias grads)
+    xb = orc.bf16_bits_from_f32(rng(2).standard_normal((8192, 4096)).astype(np.float32))
+    o = torch.empty(4096, device="cuda")
+    part = torch.empty((64, 4096), device="cuda")
+    C.launch_by_id("reduce_sum_keep_lastdim_bf16_to_f32_v0", C.OpKind.ReduceSum,
+                   [g(xb, torch.bfloat16)], [o, part])
+    ref = orc.colsum_f64(orc.bf16_bits_to_f32(xb).reshape(8192, 4096))
+    assert orc.rel_err(h(o), ref) < 1e-5
+    o1 = torch.empty(4096, device="cuda")
+    C.launch_by_id("reduce_sum_keep_lastdim_bf16_to_f32_v0", C.OpKind.ReduceSum,
+                   [g(xb, torch.bfloat16)], [o1])
+    assert orc.rel_err(h(o1), ref) < 1e-5
+
+
+@pytest.mark.parametrize("cols", [128, 1024, 8192, 32768, 1000, 64, 2048, 4096])
+def test_row_softmax_and_stats(C, cols):
+    rows = 64 if cols <= 8192 else 16
+    x = (2.0 * rng(cols).standard_normal((rows, cols))).astype(np.float32)  # N(0, 4)
+    x[-1, :] = -1e4
+    y = torch.empty((rows, cols), device="cuda")
+    mx = torch.empty(rows, device="cuda")
+    sx = torch.empty(rows, device="cuda")
+    C.op_call(int(C.OpKind.RowSoftmax), [g(x)], [y, mx, sx], 0, b"", 0)
+    ry, rmx, rsx = orc.softmax_rows_f64(x)
+    yy = h(y)
+    assert orc.rel_err(yy, ry) < 1e-5
+    assert np.array_equal(h(mx), rmx.astype(np.float32))  # max is order-free: bit-exact
+    assert orc.rel_err(h(sx)[:-1], rsx[:-1]) < 1e-5
+    assert orc.rel_err(h(sx), rsx) < 1e-5
+    assert np.all(yy[-1] == np.float32(1.0 / cols))  # stable row: exactly 1/C
+    # RowReduce sum / max
+    o = torch.empty(rows, device="cuda")
+    C.op_call(int(C.OpKind.RowReduce), [g(x)], [o], RRED, struct.pack("<i", 1), 0)
+    assert np.array_equal(h(o), rmx.astype(np.float32))
+    C.op_call(int(C.OpKind.RowReduce), [g(x)], [o], RRED, struct.pack("<i", 0), 0)
+    assert orc.rel_err(h(o), rsx) < 1e-5
+    # softmax only
+    C.op_call(int(C.OpKind.RowSoftmax), [g(x)], [y], 0, b"", 0)
+    assert orc.rel_err(h(y), ry) < 1e-5
+
+
+@pytest.mark.parametrize("B,Ccls", [(64, 10), (64, 1024), (37, 1000), (256, 128)])
+def test_softmax_xent(C, B, Ccls):
+    r = rng(B * Ccls)
+    z = (3 * r.standard_normal((B, Ccls))).astype(np.float32)
+    z[1, 3] = z[1, 5] = z[1].max() + 2.0  # tie -> first index
+    lab = r.integers(0, Ccls, B).astype(np.int32)
+    loss = torch.empty((), device="cuda")
+    dz = torch.empty((B, Ccls), device="cuda")
+    am = torch.empty(B, dtype=torch.int32, device="cuda")
+    rl = torch.empty(B, device="cuda")
+    C.op_call(int(C.OpKind.SoftmaxXent), [g(z), g(lab)], [loss, dz, am, rl], 0, b"", 0)
+    rloss, rdz, ram, rrl = orc.softmax_xent_f64(z, lab)
+    assert np.array_equal(h(am), ram)
+    assert h(am)[1] == 3
+    assert abs(loss.item() - rloss) / abs(rloss) < 1e-5
+    assert orc.rel_err(h(dz), rdz) < 1e-5
+    assert orc.rel_err(h(rl), rrl) < 1e-5
+
+
+# ============================================================== GEMM
+def _gemm_ref(A, B, ta, tb):
+    return orc.gemm_f64(A, B, ta, tb)
+
+
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+def test_gemm_f32_probe_shapes(C, ta, tb):
+    # v2_gemm_probe.py:92-119: M,K,N = 64,48,80, all trans combos
+    r = rng(10)
+    M, K, N = 64, 48, 80
+    A = r.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
+    B = r.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
+    o = torch.empty((M, N), device="cuda")
+    C.op_call(int(C.OpKind.Gemm), [g(A), g(B)], [o], 0, struct.pack("<ii", ta, tb), 0)
+    assert orc.rel_err(h(o), _gemm_ref(A, B, ta, tb)) < 1e-4
+    C.launch_by_id("gemm_f32_naive_v0", C.OpKind.Gemm, [g(A), g(B)], [o], GEMM,
+                   struct.pack("<ii", ta, tb))
+    assert orc.rel_err(h(o), _gemm_ref(A, B, ta, tb)) < 1e-4
+
+
+def test_gemm_f32_strided_views(C):
+    r = rng(11)
+    A = r.standard_normal((96, 70)).astype(np.float32)
+    B = r.standard_normal((90, 50)).astype(np.float32)
+    tA, tB = g(A), g(B)
+    a_view = tA[:64:1, 3:51]     # [64, 48], row stride 70
+    b_view = tB[5:53, 10:40:1]   # [48, 30], row stride 50
+    o_full = torch.zeros((64, 61), device="cuda")
+    o = o_full[:, 1:31]          # non-contiguous output
+    C.op_call(int(C.OpKind.Gemm), [a_view, b_view], [o], 0, b"", 0)
+    ref = A[:64, 3:51].astype(np.float64) @ B[5:53, 10:40].astype(np.float64)
+    assert orc.rel_err(h(o), ref) < 1e-4
+    assert not h(o_full)[:, 0].any() and not h(o_full)[:, 31:].any()
+    # column-strided (gather) operand: every other column
+    a2 = tA[:, ::2][:64, :32]
+    o2 = torch.empty((64, 30), device="cuda")
+    C.op_call(int(C.OpKind.Gemm), [a2, tB[:32, :30]], [o2], 0, b"", 0)
+    ref2 = A[:64, ::2][:, :32].astype(np.float64) @ B[:32, :30].astype(np.float64)
+    assert orc.rel_err(h(o2), ref2) < 1e-4
+
+
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+def test_gemm_f16_probe_shapes(C, ta, tb):
+    r = rng(12)
+    M = K = N = 64
+    A = r.standard_normal((M, K)).astype(np.float16)
+    B = r.standard_normal((K, N)).astype(np.float16)
+    o = torch.empty((M, N), dtype=torch.float16, device="cuda")
+    C.op_call(int(C.OpKind.Gemm), [g(A.view(np.uint16)), g(B.view(np.uint16))], [o], 0,
+              struct.pack("<ii", ta, tb), 0)
+    ref = _gemm_ref(A.astype(np.float32), B.astype(np.float32), ta, tb)
+    assert orc.rel_err(orc.f16_bits_to_f64(h(o)), ref) < 2e-3
+
+
+@pytest.mark.parametrize("M,N,K,ta,tb", [
+    (1024, 1024, 1024, False, True),
+    (100, 72, 784, False, True),
+    (64, 256, 784, False, True),
+    (256, 4096, 256, False, True),
+    (512, 384, 640, False, False),
+    (384, 512, 1024, True, False),
+    (200, 136, 96, True, True),
+])
+def test_gemm_bf16(C, M, N, K, ta, tb):
+    r = rng(M + N + K)
+    s = 1.0 / np.sqrt(K)
+    A = r.uniform(-s, s, (K, M) if ta else (M, K)).astype(np.float32)
+    B = r.uniform(-s, s, (N, K) if tb else (K, N)).astype(np.float32)
+    Ab, Bb = orc.bf16_bits_from_f32(A), orc.bf16_bits_from_f32(B)
+    ref = _gemm_ref(orc.bf16_bits_to_f32(Ab).reshape(A.shape), orc.bf16_bits_to_f32(Bb).reshape(B.shape), ta, tb)
+    o = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    C.op_call(int(C.OpKind.Gemm), [g(Ab, torch.bfloat16), g(Bb, torch.bfloat16)], [o], 0,
+              struct.pack("<ii", ta, tb), 0)
+    assert orc.rel_err(orc.bf16_bits_to_f32(h(o)), ref) < 1e-2
+    of = torch.empty((M, N), device="cuda")
+    C.launch_by_id("gemm_bf16_mfma_f32out_v0", C.OpKind.Gemm,
+                   [g(Ab, torch.bfloat16), g(Bb, torch.bfloat16)], [of], 0, struct.pack("<ii", ta, tb))
+    assert orc.rel_err(h(of), ref) < 1e-5  # fp32 out: only accumulation-order error
+
+
+@pytest.mark.parametrize("relu", [1, 0])
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, True)])
+def test_gemm_epilogue_f32_gpel(C, relu, ta, tb):
+    # v2_gemm_epilogue_probe.py:108-158: f32 64,48,80 x trans x relu
+    r = rng(13)
+    M, K, N = 64, 48, 80
+    A = r.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
+    B = r.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
+    bias = r.standard_normal(N).astype(np.float32)
+    o = torch.empty((M, N), device="cuda")
+    C.op_call(int(C.OpKind.GemmEpilogue), [g(A), g(B), g(bias)], [o], GPEL,
+              struct.pack("<iii", ta, tb, relu), 0)
+    ref = _gemm_ref(A, B, ta, tb) + bias[None, :]
+    if relu:
+        ref = np.maximum(ref, 0)
+    assert orc.rel_err(h(o), ref) < 1e-4
+    if relu:
+        assert np.all(h(o)[ref < -1e-3] == 0)
+
+
+def test_gemm_epilogue_default_is_bias_relu_and_gepi_kinds(C):
+    r = rng(14)
+    M, K, N = 64, 64, 64
+    A = r.standard_normal((M, K)).astype(np.float32)
+    B = r.standard_normal((K, N)).astype(np.float32)
+    bias = r.standard_normal(N).astype(np.float32)
+    base = _gemm_ref(A, B, False, False)
+    o = torch.empty((M, N), device="cuda")
+    C.op_call(int(C.OpKind.GemmEpilogue), [g(A), g(B), g(bias)], [o], 0, b"", 0)
+    assert orc.rel_err(h(o), np.maximum(base + bias, 0)) < 1e-4
+    for kind, fn in [(0, lambda x: np.maximum(x + bias, 0)), (1, lambda x: x + bias),
+                     (2, lambda x: np.maximum(x, 0)),
+                     (3, lambda x: orc.gelu_f64(x + bias)), (4, lambda x: orc.gelu_f64(x))]:
+        C.op_call(int(C.OpKind.GemmEpilogue), [g(A), g(B), g(bias)], [o], GEPI,
+                  struct.pack("<iii", 0, 0, kind), 0)
+        assert orc.rel_err(h(o), fn(base)) < 1e-4, kind
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 512, 384), (1024, 1024, 1024), (100, 200, 64)])
+def test_gemm_epilogue_bf16_gelu_aux_and_dgelu(C, M, N, K):
+    r = rng(15)
+    s = 1.0 / np.sqrt(K)
+    X = orc.bf16_bits_from_f32(r.uniform(-1, 1, (M, K)).astype(np.float32))
+    W = orc.bf16_bits_from_f32(r.uniform(-s, s, (N, K)).astype(np.float32))
+    bias = r.uniform(-s, s, N).astype(np.float32)
+    Xf = orc.bf16_bits_to_f32(X).reshape(M, K)
+    Wf = orc.bf16_bits_to_f32(W).reshape(N, K)
+    z_ref = _gemm_ref(Xf, Wf, False, True) + bias[None, :]
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    z = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    C.launch_by_id("gemm_epilogue_bf16_mfma_v0", C.OpKind.GemmEpilogue,
+                   [g(X, torch.bfloat16), g(W, torch.bfloat16), g(bias)], [y, z], GEPI,
+                   struct.pack("<iii", 0, 1, 3))
+    zz = orc.bf16_bits_to_f32(h(z)).reshape(M, N)
+    assert orc.rel_err(zz, z_ref) < 1e-2
+    assert orc.rel_err(orc.bf16_bits_to_f32(h(y)).reshape(M, N), orc.gelu_f64(z_ref)) < 1e-2
+    # dgelu epilogue: dZ = (dY . W) * gelu'(Z), dY [M,N] . W [N,K] -> [M,K]
+    dY = orc.bf16_bits_from_f32(r.standard_normal((M, N)).astype(np.float32))
+    Zk = orc.bf16_bits_from_f32(r.standard_normal((M, K)).astype(np.float32))
+    dz = torch.empty((M, K), dtype=torch.bfloat16, device="cuda")
+    C.launch_by_id("gemm_epilogue_bf16_mfma_v0", C.OpKind.GemmEpilogue,
+                   [g(dY, torch.bfloat16), g(W, torch.bfloat16), g(Zk, torch.bfloat16)], [dz], GEPI,
+                   struct.pack("<iii", 0, 0, 5))
+    ref = _gemm_ref(orc.bf16_bits_to_f32(dY).reshape(M, N), Wf, False, False) * \
+        orc.gelu_grad_f64(orc.bf16_bits_to_f32(Zk).reshape(M, K).astype(np.float64))
+    assert orc.rel_err(orc.bf16_bits_to_f32(h(dz)).reshape(M, K), ref) < 1e-2
+
+
+def test_gemm_neg_cases_raise(C):
+    A = torch.zeros((64, 48), device="cuda")
+    B = torch.zeros((48, 80), device="cuda")
+    with pytest.raises(RuntimeError, match="status=NotImplemented"):
+        C.op_call(int(C.OpKind.Gemm), [A, B], [torch.empty((64, 81), device="cuda")], 0, b"", 0)
+    with pytest.raises(RuntimeError, match="kernel_id=gemm_f32_naive_v0"):
+        C.launch_by_id("gemm_f32_naive_v0", C.OpKind.Gemm, [A, B],
+                       [torch.empty((64, 81), device="cuda")])
+    with pytest.raises(RuntimeError):
+        C.op_call(int(C.OpKind.Gemm), [A.cpu(), B], [torch.empty((64, 80), device="cuda")])
+
+
+# ============================================================== graph
+def test_graph_capture_replay_matches_eager(C):
+    """Captured elementwise + Adam sequence, replayed 3x with eager work and
+    host-side scalar updates between replays; each replay checked."""
+    r = rng(16)
+    n = 1 << 16
+    P = r.standard_normal(n).astype(np.float32)
+    G = r.standard_normal(n).astype(np.float32)
+    tP, tG = g(P), g(G)
+    tM, tV = torch.zeros_like(tP), torch.zeros_like(tP)
+    bc1 = torch.tensor(1.0, device="cuda")
+    bc2 = torch.tensor(1.0, device="cuda")
+    pay = struct.pack("<ffff", 1e-3, 0.9, 0.999, 1e-8)
+    C.graph_reset()
+    s = C.graph_begin()
+    assert s != 0 and C.graph_stream() == s
+    C.launch_by_id("adam_step_f32_v0", C.OpKind.AdamStep, [tP, tG, tM, tV, bc1, bc2],
+                   [tP, tM, tV], ADAM, pay, s)
+    C.graph_end()
+    trace = C.trace_get()
+    assert trace == ["kid:adam_step_f32_v0 kind:adam_step"]
+    Pc, Mc, Vc = P.copy(), np.zeros(n, np.float32), np.zeros(n, np.float32)
+    for t in range(1, 4):
+        b1, b2 = np.float32(1 - 0.9 ** t), np.float32(1 - 0.999 ** t)
+        bc1.fill_(float(b1))
+        bc2.fill_(float(b2))
+        _ = (tG * 2).sum()  # unrelated eager work on torch's stream
+        C.graph_launch()
+        torch.cuda.synchronize()
+        Pc, Mc, Vc = orc.adam_ref(Pc, G, Mc, Vc, b1, b2)
+        assert np.array_equal(h(tP), Pc), f"replay {t}"
+        assert np.array_equal(h(tV), Vc), f"replay {t}"
+    C.graph_reset()
+    with pytest.raises(RuntimeError, match="no captured graph"):
+        C.graph_launch()
+    with pytest.raises(RuntimeError, match="not capturing"):
+        C.graph_end()
+
+
+def test_trace_api(C):
+    C.trace_reset()
+    C.trace_enable(True)
+    x = torch.ones(16, device="cuda")
+    C.op_call(int(C.OpKind.EltwiseRelu), [x], [x])
+    C.launch_by_id("relu_f32_v0", C.OpKind.EltwiseRelu, [x], [x])
+    assert C.trace_get() == ["relu", "kid:relu_f32_v0 kind:relu"]
+    C.trace_enable(False)
+    C.op_call(int(C.OpKind.EltwiseRelu), [x], [x])
+    assert len(C.trace_get()) == 2
+    C.trace_enable(True)
+    C.trace_reset()
+    assert C.trace_get() == []
