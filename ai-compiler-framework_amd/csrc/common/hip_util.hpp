@@ -50,16 +50,36 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
   u += 0x7fffu + ((u >> 16) & 1u);
   return static_cast<uint16_t>(u >> 16);
 }
+// binary16 <-> fp32 with integer operations only.  The reference converts
+// with __half2float (exact) and __float2half_rn (one RNE rounding of the
+// fp32 value); doing the same here keeps hipcc from fusing a convert-fma-
+// convert chain into v_fma_mix*, which rounds the exact result straight to
+// f16 and can differ from the reference in the last bit.
 __device__ __forceinline__ float f16_to_f32(uint16_t h) {
-  _Float16 x;
-  __builtin_memcpy(&x, &h, 2);
-  return static_cast<float>(x);
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  const uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+  if (e == 0) {
+    // zero / subnormal: m * 2^-24 is exact in fp32
+    const float v = (float)m * 5.9604644775390625e-8f;
+    return __uint_as_float(__float_as_uint(v) | sign);
+  }
+  if (e == 31) return __uint_as_float(sign | 0x7f800000u | (m << 13));
+  return __uint_as_float(sign | ((e + 112u) << 23) | (m << 13));
 }
 __device__ __forceinline__ uint16_t f32_to_f16(float f) {
-  _Float16 x = static_cast<_Float16>(f);  // round-to-nearest-even
-  uint16_t h;
-  __builtin_memcpy(&h, &x, 2);
-  return h;
+  uint32_t x = __float_as_uint(f);
+  const uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+  x &= 0x7fffffffu;
+  if (x >= 0x7f800000u) return sign | (x > 0x7f800000u ? 0x7e00u : 0x7c00u);  // NaN / inf
+  if (x >= 0x477ff000u) return sign | 0x7c00u;  // >= 65520 rounds to inf
+  if (x >= 0x38800000u) {                       // normal binary16 range
+    x += 0xc8000fffu + ((x >> 13) & 1u);        // rebias exponent, round half to even
+    return sign | (uint16_t)(x >> 13);
+  }
+  // subnormal / zero: adding 0.5 aligns the 2^-24 quantum to the fp32 ulp,
+  // so the fp32 addition performs the RNE rounding
+  const float r = __uint_as_float(x) + 0.5f;
+  return sign | (uint16_t)(__float_as_uint(r) - 0x3f000000u);
 }
 
 // ---- wave64 reductions (butterfly over all 64 lanes) ----------------------

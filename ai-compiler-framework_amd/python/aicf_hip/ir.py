@@ -63,10 +63,9 @@ class IRGraph:
         """Text dump in the layout of the reference's 20_ir.txt artifact."""
         lines = [f"=== IRGraph: {self.name} ===",
                  f"values: {len(self.values)}, nodes: {len(self.nodes)}", "", "[values]"]
-        w = max([len(v.name) for v in self.values.values()] + [1])
         for vid in sorted(self.values):
             v = self.values[vid]
-            lines.append(f"  v{vid:03d}  {v.name:<{w}}  shape={v.shape} dtype={v.dtype} device={v.device}")
+            lines.append(f"  v{vid:03d}  {v.name:<12} shape={v.shape} dtype={v.dtype} device={v.device}")
         lines += ["", "[nodes]"]
         for i, n in enumerate(self.nodes):
             ins = ", ".join(f"v{x:03d}" for x in n.inputs)

@@ -270,3 +270,82 @@ def check_mlp_small(device: str = "cuda:0", verbose: bool = False, B=64, din=784
     if verbose:
         print("[mlp] check", res)
     return res
+
+
+def check_mlp_mse_small(B: int = 256, D: int = 256, L: int = 4, device: str = "cuda:0",
+                        steps: int = 3) -> Dict[str, object]:
+    """Runs the bf16 MSE MLP (same graph and kernels as the benchmark, smaller
+    shape) eagerly for one step and as a captured graph for `steps`-1 more,
+    and checks each step against the CPU oracle: an fp64 chain that rounds
+    every stored bf16 tensor as the kernels do (loss, all dW / db, rel-err
+    <= 1e-2), and the reference-exact AdamW restatement applied to the GPU's
+    own gradients (updated parameters, moments and bf16 shadow bit-exact)."""
+    import oracle as orc  # test infrastructure
+
+    ir, lowered, plan = build_mlp_mse(B, D, L, device=device)
+    lay = FlatLayout(D, L)
+    ex = make_executor(ir, lowered, plan, device)
+    inputs, params = init_mlp_mse(B, D, L, seed=1, device=device)
+    ex.build_env(inputs=inputs, params=params, reuse_static=False)
+    refresh_shadow(ex)
+    torch.cuda.synchronize()
+    X = _np(inputs["x"]).astype(np.float64)
+    T = _np(inputs["t"]).astype(np.float64)
+    q = lambda a: orc.bf16_round(np.asarray(a, np.float32)).astype(np.float64)  # noqa: E731
+    res: Dict[str, object] = {"ok": True}
+    Pm = _np(params["flat.params"]).copy()
+    Mm = np.zeros_like(Pm)
+    Vm = np.zeros_like(Pm)
+
+    def expect(P):
+        Wb = [q(P[lay.w_off(i):lay.w_off(i) + D * D].reshape(D, D)) for i in range(1, L + 1)]
+        bs = [P[lay.b_off(i):lay.b_off(i) + D].astype(np.float64) for i in range(1, L + 1)]
+        hs, zs = [X], []
+        for i in range(L - 1):
+            v = hs[-1] @ Wb[i].T + bs[i]
+            zs.append(q(v))
+            hs.append(q(orc.gelu_f64(v)))
+        y = q(hs[-1] @ Wb[L - 1].T + bs[L - 1])
+        n = B * D
+        loss = float(np.mean((y - T) ** 2))
+        dy = q((y - T) * np.float32(2.0 / n))
+        grads = {}
+        for i in range(L - 1, -1, -1):
+            grads[f"{i + 1}.W"] = dy.T @ hs[i]
+            grads[f"{i + 1}.b"] = dy.sum(0)
+            if i > 0:
+                dy = q((dy @ Wb[i]) * orc.gelu_grad_f64(zs[i - 1]))
+        return loss, grads
+
+    def check(tag, t):
+        nonlocal Pm, Mm, Vm
+        loss, grads = expect(Pm)
+        gl = float(ex.value("loss").item())
+        res[f"{tag}_loss_rel"] = abs(gl - loss) / loss
+        ok = res[f"{tag}_loss_rel"] < 1e-2
+        G = _np(ex.value("grad.flat"))
+        for i in range(1, L + 1):
+            for k, off, n in ((f"{i}.W", lay.w_off(i), D * D), (f"{i}.b", lay.b_off(i), D)):
+                e = orc.rel_err(G[off:off + n], grads[k].ravel())
+                res[f"{tag}_grad_{k}"] = e
+                ok &= e < 1e-2
+        Pr, Mr, Vr, Wr = orc.adamw(Pm, G, Mm, Vm, t, 1e-3, 0.9, 0.999, 1e-8, 0.0, shadow=True)
+        exact = (np.array_equal(_np(ex.value("flat.params")), Pr)
+                 and np.array_equal(_np(ex.value("opt.m.flat")), Mr)
+                 and np.array_equal(_np(ex.value("opt.v.flat")), Vr)
+                 and np.array_equal(ex.value("wb.flat").view(torch.int16).cpu().numpy().view(np.uint16), Wr))
+        res[f"{tag}_adamw_exact"] = bool(exact)
+        ok &= exact
+        Pm, Mm, Vm = Pr, Mr, Vr
+        res["ok"] = bool(res["ok"] and ok)
+
+    ex.run(inputs=inputs, params=params, reuse_static=True)
+    torch.cuda.synchronize()
+    check("eager", 1)
+    ex.capture(inputs=inputs, params=params, reuse_static=True)
+    for t in range(2, steps + 1):
+        ex.replay(1)
+        torch.cuda.synchronize()
+        check(f"replay{t}", t)
+    ex.reset_graph()
+    return res

@@ -54,6 +54,22 @@ def rng(seed):
     return np.random.default_rng(seed)
 
 
+def scalar(v, dtype=torch.float32):
+    """0-d device tensor (np.ascontiguousarray would promote 0-d to 1-d)."""
+    return torch.tensor(v, dtype=dtype, device="cuda")
+
+
+def assert_bits_equal(got, ref, *inputs):
+    """Bit-exact check that reports the first mismatching elements."""
+    got = np.asarray(got).ravel()
+    ref = np.asarray(ref).ravel()
+    bad = np.nonzero(got != ref)[0]
+    if bad.size:
+        rows = [f"i={i} got={got[i]} ref={ref[i]} in={[np.asarray(a).ravel()[i] for a in inputs]}"
+                for i in bad[:8]]
+        raise AssertionError(f"{bad.size} mismatches\n" + "\n".join(rows))
+
+
 # ============================================================== optimizer
 @pytest.mark.parametrize("shape,inplace", [((1024,), False), ((64, 256), False),
                                            ((8, 32, 128), False), ((64, 256), True),
@@ -68,7 +84,7 @@ def test_adam_reference_contract_bit_exact(C, shape, inplace):
     tP, tG, tM, tV = g(P), g(G), g(M), g(V)
     outs = [tP, tM, tV] if inplace else [torch.empty_like(tP) for _ in range(3)]
     C.op_call(int(C.OpKind.AdamStep),
-              [tP, tG, tM, tV, g(np.array(bc1)), g(np.array(bc2))], outs, ADAM,
+              [tP, tG, tM, tV, scalar(float(bc1)), scalar(float(bc2))], outs, ADAM,
               struct.pack("<ffff", lr, b1, b2, eps), 0)
     Pr, Mr, Vr = orc.adam_ref(P, G, M, V, bc1, bc2, lr, b1, b2, eps)
     assert np.array_equal(h(outs[0]).ravel(), Pr)
@@ -141,7 +157,7 @@ def test_sgd(C):
         Gh = G.astype(np.float16).view(np.uint16)
         tPh, tGh = g(Ph), g(Gh)
         C.op_call(int(C.OpKind.SgdStep), [tPh, tGh], [tPh], 0, b"", 0)  # default lr 1e-3
-        assert np.array_equal(h(tPh), orc.sgd_f16(Ph, Gh, 1e-3))
+        assert_bits_equal(h(tPh), orc.sgd_f16(Ph, Gh, 1e-3), Ph, Gh)
     with pytest.raises(RuntimeError):
         C.op_call(int(C.OpKind.SgdStep), [tP, tG], [tG], 0, b"", 0)  # O aliases G
 
