@@ -53,6 +53,7 @@ enum class OpKind : int {
   SoftmaxXent = AICF_OP_SOFTMAX_XENT,
   GeluBwd = AICF_OP_GELU_BWD,
   EltwiseGelu = AICF_OP_ELTWISE_GELU,
+  Transpose = AICF_OP_TRANSPOSE,
 };
 
 std::string tensor_brief(const torch::Tensor& t) {
@@ -224,6 +225,7 @@ PYBIND11_MODULE(_C, m) {
       .value("SoftmaxXent", OpKind::SoftmaxXent)
       .value("GeluBwd", OpKind::GeluBwd)
       .value("EltwiseGelu", OpKind::EltwiseGelu)
+      .value("Transpose", OpKind::Transpose)
       .export_values();
 
   m.def(

@@ -97,15 +97,21 @@ __device__ __forceinline__ float wave_max(float v) {
 // ---- GELU (tanh approximation) ---------------------------------------------
 // gelu(x) = 0.5 x (1 + tanh(u)),  u = sqrt(2/pi) (x + 0.044715 x^3)
 // gelu'(x) = 0.5 (1 + t) + 0.5 x (1 - t^2) sqrt(2/pi) (1 + 3*0.044715 x^2)
+// tanh(u) = 1 - 2 / (1 + e^{2u}): exact limits +-1 when e^{2u} overflows or
+// underflows; its absolute error (a few 1e-8) enters gelu only through
+// (1 + t), i.e. as a relative error of the same size.
+__device__ __forceinline__ float tanh_fast(float u) {
+  return 1.0f - 2.0f / (1.0f + __expf(2.0f * u));
+}
 __device__ __forceinline__ float gelu_tanh_f(float x) {
   const float k0 = 0.7978845608028654f, k1 = 0.044715f;
   const float u = k0 * (x + k1 * x * x * x);
-  return 0.5f * x * (1.0f + tanhf(u));
+  return 0.5f * x * (1.0f + tanh_fast(u));
 }
 __device__ __forceinline__ float gelu_tanh_grad_f(float x) {
   const float k0 = 0.7978845608028654f, k1 = 0.044715f;
   const float x2 = x * x;
-  const float t = tanhf(k0 * (x + k1 * x2 * x));
+  const float t = tanh_fast(k0 * (x + k1 * x2 * x));
   return 0.5f * (1.0f + t) + 0.5f * x * (1.0f - t * t) * k0 * (1.0f + 3.0f * k1 * x2);
 }
 

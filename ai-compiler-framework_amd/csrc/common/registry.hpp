@@ -62,6 +62,7 @@ enum class OpKind : int {
   SoftmaxXent = AICF_OP_SOFTMAX_XENT,
   GeluBwd = AICF_OP_GELU_BWD,
   EltwiseGelu = AICF_OP_ELTWISE_GELU,
+  Transpose = AICF_OP_TRANSPOSE,
   _Count = AICF_OP_COUNT,
 };
 

@@ -675,6 +675,84 @@ Status gelu_bwd_bf16_launch(const TensorDesc* i, int ni, TensorDesc* o, int no, 
                                "gelu_bwd_bf16");
 }
 
+// ---------------------------------------------------------------------------
+// 2-D transpose (appended op): X [R, C] -> Y [C, R], both row-major with
+// arbitrary row strides, 2- or 4-byte elements.  64 x 64 tiles through LDS:
+// each thread reads two 16-byte chunks along a row of X and writes two
+// 16-byte chunks along a row of Y; the LDS row pitch is padded by 16 bytes.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void transpose_kernel(const T* __restrict__ X, T* __restrict__ Y,
+                                                        int64_t R, int64_t C, int64_t ldx,
+                                                        int64_t ldy) {
+  constexpr int TILE = 64;
+  constexpr int V = 16 / (int)sizeof(T);        // elements per 16-byte chunk
+  constexpr int CPR = TILE / V;                 // chunks per tile row
+  constexpr int PITCH = TILE + V;               // padded LDS row (elements)
+  __shared__ __attribute__((aligned(16))) T tile[TILE * PITCH];
+  typedef T vec __attribute__((ext_vector_type(V)));
+  const int64_t r0 = (int64_t)blockIdx.y * TILE, c0 = (int64_t)blockIdx.x * TILE;
+  const bool full = r0 + TILE <= R && c0 + TILE <= C;
+  const bool vx = full && ((uintptr_t)X % 16 == 0) && ((ldx * (int64_t)sizeof(T)) % 16 == 0);
+  const bool vy = full && ((uintptr_t)Y % 16 == 0) && ((ldy * (int64_t)sizeof(T)) % 16 == 0);
+  for (int q = threadIdx.x; q < TILE * CPR; q += 256) {
+    const int r = q / CPR, c = (q % CPR) * V;
+    vec v;
+    if (vx) {
+      v = *reinterpret_cast<const vec*>(X + (r0 + r) * ldx + c0 + c);
+    } else {
+#pragma unroll
+      for (int e = 0; e < V; ++e)
+        v[e] = (r0 + r < R && c0 + c + e < C) ? X[(r0 + r) * ldx + c0 + c + e] : T(0);
+    }
+    *reinterpret_cast<vec*>(tile + r * PITCH + c) = v;
+  }
+  __syncthreads();
+  for (int q = threadIdx.x; q < TILE * CPR; q += 256) {
+    const int c = q / CPR, r = (q % CPR) * V;  // output row c (= input column), columns r..r+V
+    vec v;
+#pragma unroll
+    for (int e = 0; e < V; ++e) v[e] = tile[(r + e) * PITCH + c];
+    if (vy) {
+      *reinterpret_cast<vec*>(Y + (c0 + c) * ldy + r0 + r) = v;
+    } else {
+#pragma unroll
+      for (int e = 0; e < V; ++e)
+        if (c0 + c < C && r0 + r + e < R) Y[(c0 + c) * ldy + r0 + r + e] = v[e];
+    }
+  }
+}
+
+bool transpose_sup(const TensorDesc* in, int ni, const TensorDesc* out, int no, const void*) {
+  if (!in || !out || ni != 1 || no != 1) return false;
+  const TensorDesc &X = in[0], &Y = out[0];
+  if (X.rank != 2 || Y.rank != 2 || dt(X) != dt(Y)) return false;
+  const DType d = dt(X);
+  if (d != DType::kF32 && d != DType::kF16 && d != DType::kBF16 && d != DType::kI32) return false;
+  if (Y.shape[0] != X.shape[1] || Y.shape[1] != X.shape[0]) return false;
+  if (X.shape[0] <= 0 || X.shape[1] <= 0) return false;
+  if (X.stride[1] != 1 || Y.stride[1] != 1 || X.stride[0] < X.shape[1] || Y.stride[0] < Y.shape[1])
+    return false;
+  return X.data != Y.data;
+}
+
+Status transpose_launch(const TensorDesc* in, int ni, TensorDesc* out, int no, const void* a, void*,
+                        size_t, void* stream) {
+  if (!transpose_sup(in, ni, out, no, a)) return Status::InvalidArgument;
+  const int64_t R = in[0].shape[0], C = in[0].shape[1];
+  if ((C + 63) / 64 > INT32_MAX || (R + 63) / 64 > 65535) return Status::InvalidArgument;
+  dim3 grid((unsigned)((C + 63) / 64), (unsigned)((R + 63) / 64));
+  hipStream_t s = as_stream(stream);
+  if (dt(in[0]) == DType::kF32 || dt(in[0]) == DType::kI32)
+    transpose_kernel<float><<<grid, 256, 0, s>>>((const float*)in[0].data, (float*)out[0].data, R, C,
+                                                 in[0].stride[0], out[0].stride[0]);
+  else
+    transpose_kernel<uint16_t><<<grid, 256, 0, s>>>((const uint16_t*)in[0].data,
+                                                    (uint16_t*)out[0].data, R, C, in[0].stride[0],
+                                                    out[0].stride[0]);
+  return launch_status("transpose2d_v0");
+}
+
 }  // namespace
 
 KernelVariant make_add_f32_variant() { return make("add_f32", add_f32_launch, add_f32_sup); }
@@ -729,6 +807,9 @@ KernelVariant make_gelu_bwd_f32_variant() {
 }
 KernelVariant make_gelu_bwd_bf16_variant() {
   return make("gelu_bwd_bf16", gelu_bwd_bf16_launch, gelu_bwd_bf16_sup);
+}
+KernelVariant make_transpose_variant() {
+  return make("transpose2d_lds64", transpose_launch, transpose_sup);
 }
 
 }  // namespace aicf::hip

@@ -366,6 +366,201 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_kernel(GemmParams p) {
 }
 
 // ---------------------------------------------------------------------------
+// Fast path for 16-bit inputs with both operands K-contiguous (X[M,K] and
+// W[N,K] row-major, the Linear layout) and tile-divisible shapes.
+//   * BM x BN x 64 workgroup tiles; WM x WN waves (two per SIMD for the
+//     256x256 tile), each wave owns (BM/WM) x (BN/WN) = TM x TN blocks of
+//     32x32 fp32 accumulators;
+//   * global -> LDS with gfx950's direct 16-byte LDS loads
+//     (global_load_lds_dwordx4): lane i of a wave fills bytes [16i, 16i+16)
+//     of a 1 KB LDS block = 8 rows of 64 K-elements, so there is no VGPR
+//     staging and no ds_write; the XOR swizzle (chunk ^ row%8) that keeps the
+//     fragment reads bank-conflict free is applied by choosing which global
+//     chunk each lane fetches;
+//   * two LDS stages: the loads of K-step k+1 are issued right after the
+//     barrier of step k and waited for once at its end;
+//   * inside a K-step the MFMA fragments of sub-step s+1 are read from LDS
+//     while the MFMAs of sub-step s run (two register sets), interleaved one
+//     ds_read per few MFMAs with sched_group_barrier;
+//   * MFMA operands swapped (A-operand = W rows, B-operand = X rows) so that
+//     each lane holds 4 consecutive output columns of one row and the
+//     epilogue stores 8 (bf16) or 16 (fp32) contiguous bytes per lane;
+//   * the activation is a template parameter; bias and the pre-activation
+//     output are uniform runtime flags.
+// ---------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void glb_void_t;
+
+struct NTParams {
+  const uint16_t* A;  // [M, K], row stride lda
+  const uint16_t* B;  // [N, K], row stride ldb
+  void* C;            // [M, N], row stride ldc
+  const void* bias;
+  void* aux;
+  int64_t lda, ldb, ldc, aux_ld;
+  int M, N, K;
+  int bias_f32;
+  int tiles_m, tiles_n;
+};
+
+template <int OUT, int ACT>
+__device__ __forceinline__ void nt_epilogue4(const NTParams& p, int m, int n, float* v) {
+  if constexpr (ACT == ACT_DGELU) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] *= gelu_tanh_grad_f(load_out<OUT>(p.aux, (int64_t)m * p.aux_ld + n + e));
+  } else {
+    if (p.bias) {
+      if (p.bias_f32) {
+        const f32x4 b = *reinterpret_cast<const f32x4*>((const float*)p.bias + n);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] += b[e];
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] += load_out<OUT>(p.bias, n + e);
+      }
+    }
+    if constexpr (ACT == ACT_RELU) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = v[e] > 0.0f ? v[e] : 0.0f;
+    } else if constexpr (ACT == ACT_GELU) {
+      if (p.aux) {
+        if constexpr (OUT == OUT_F32) {
+          *reinterpret_cast<f32x4*>((float*)p.aux + (int64_t)m * p.aux_ld + n) = f32x4{v[0], v[1], v[2], v[3]};
+        } else {
+          u16x4 z;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) z[e] = OUT == OUT_BF16 ? f32_to_bf16(v[e]) : f32_to_f16(v[e]);
+          *reinterpret_cast<u16x4*>((uint16_t*)p.aux + (int64_t)m * p.aux_ld + n) = z;
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = gelu_tanh_f(v[e]);
+    }
+  }
+  const int64_t idx = (int64_t)m * p.ldc + n;
+  if constexpr (OUT == OUT_F32) {
+    *reinterpret_cast<f32x4*>((float*)p.C + idx) = f32x4{v[0], v[1], v[2], v[3]};
+  } else {
+    u16x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = OUT == OUT_BF16 ? f32_to_bf16(v[e]) : f32_to_f16(v[e]);
+    *reinterpret_cast<u16x4*>((uint16_t*)p.C + idx) = o;
+  }
+}
+
+template <int IN, int OUT, int ACT, int BM, int BN, int WM, int WN>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_nt16_kernel(NTParams p) {
+  constexpr int BK = 64;
+  constexpr int KS = BK / 16;  // MFMA sub-steps per K-step
+  constexpr int NW = WM * WN;
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int TM = WTM / 32, TN = WTN / 32;
+  constexpr int A_BYTES = BM * BK * 2, B_BYTES = BN * BK * 2;
+  constexpr int STAGE = A_BYTES + B_BYTES;
+  static_assert((BM / 8 + BN / 8) % NW == 0, "load blocks must split evenly over waves");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE];
+
+  int tm_i, tn_i;
+  tile_coords(p.tiles_m, p.tiles_n, tm_i, tn_i);
+  const int m0 = tm_i * BM, n0 = tn_i * BN;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+
+  // slot `lane` of a 1 KB block holds row lane/8, physical chunk lane%8,
+  // i.e. logical chunk (lane%8) ^ (lane/8)
+  const int r_in = lane >> 3;
+  const int c_log = (lane & 7) ^ r_in;
+  const uint16_t* a_src = p.A + (int64_t)(m0 + r_in) * p.lda + c_log * 8;
+  const uint16_t* b_src = p.B + (int64_t)(n0 + r_in) * p.ldb + c_log * 8;
+
+  auto issue_loads = [&](int kt, int stage) {
+    uint8_t* base = smem + stage * STAGE;
+    const int64_t koff = (int64_t)kt * BK;
+#pragma unroll
+    for (int j = wave; j < BM / 8; j += NW)
+      __builtin_amdgcn_global_load_lds((glb_void_t*)(a_src + (int64_t)j * 8 * p.lda + koff),
+                                       (lds_void_t*)(base + j * 1024), 16, 0, 0);
+#pragma unroll
+    for (int j = wave; j < BN / 8; j += NW)
+      __builtin_amdgcn_global_load_lds((glb_void_t*)(b_src + (int64_t)j * 8 * p.ldb + koff),
+                                       (lds_void_t*)(base + A_BYTES + j * 1024), 16, 0, 0);
+  };
+
+  floatx16 acc[TN][TM];
+#pragma unroll
+  for (int i = 0; i < TN; ++i)
+#pragma unroll
+    for (int j = 0; j < TM; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  const int fr = lane & 31, fh = lane >> 5;
+  int a_off[TM], b_off[TN];
+#pragma unroll
+  for (int j = 0; j < TM; ++j) a_off[j] = (wm * WTM + j * 32 + fr) * 128;
+#pragma unroll
+  for (int i = 0; i < TN; ++i) b_off[i] = A_BYTES + (wn * WTN + i * 32 + fr) * 128;
+  const int rsw = fr & 7;
+
+  const int nk = p.K / BK;
+  issue_loads(0, 0);
+  for (int kt = 0; kt < nk; ++kt) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (kt + 1 < nk) issue_loads(kt + 1, (kt + 1) & 1);
+    const uint8_t* st = smem + (kt & 1) * STAGE;
+    u16x8 fa[2][TM], fb[2][TN];
+    {
+      const int chunk = (fh ^ rsw) * 16;
+#pragma unroll
+      for (int j = 0; j < TM; ++j) fa[0][j] = *reinterpret_cast<const u16x8*>(st + a_off[j] + chunk);
+#pragma unroll
+      for (int i = 0; i < TN; ++i) fb[0][i] = *reinterpret_cast<const u16x8*>(st + b_off[i] + chunk);
+    }
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+      const int cb = kk & 1, nb = cb ^ 1;
+      if (kk + 1 < KS) {
+        const int chunk = (((kk + 1) * 2 + fh) ^ rsw) * 16;
+#pragma unroll
+        for (int j = 0; j < TM; ++j) fa[nb][j] = *reinterpret_cast<const u16x8*>(st + a_off[j] + chunk);
+#pragma unroll
+        for (int i = 0; i < TN; ++i) fb[nb][i] = *reinterpret_cast<const u16x8*>(st + b_off[i] + chunk);
+      }
+#pragma unroll
+      for (int i = 0; i < TN; ++i)
+#pragma unroll
+        for (int j = 0; j < TM; ++j)
+          acc[i][j] = mfma32<IN>(reinterpret_cast<const uint16_t*>(&fb[cb][i]),
+                                 reinterpret_cast<const uint16_t*>(&fa[cb][j]), acc[i][j]);
+      if (kk + 1 < KS) {
+#pragma unroll
+        for (int t = 0; t < TM + TN; ++t) {
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                      // one ds_read
+          __builtin_amdgcn_sched_group_barrier(0x008, (TM * TN) / (TM + TN), 0);  // some MFMAs
+        }
+      }
+    }
+  }
+
+  // Epilogue: block (i, j) holds D[n][m]; this lane has m = .. + fr and
+  // n = .. + 8g + 4fh + {0..3} in acc[i][j][4g .. 4g+3].
+#pragma unroll
+  for (int j = 0; j < TM; ++j) {
+    const int m = m0 + wm * WTM + j * 32 + fr;
+#pragma unroll
+    for (int i = 0; i < TN; ++i)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * g + e];
+        nt_epilogue4<OUT, ACT>(p, m, n0 + wn * WTN + i * 32 + 8 * g + 4 * fh, v);
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
 struct View2D {
@@ -449,8 +644,64 @@ Status run_cfg(GemmParams& p, hipStream_t s) {
   return launch_status("gemm_mfma");
 }
 
+template <int IN, int OUT, int ACT, int BM, int BN, int WM, int WN>
+Status run_nt_act(const GemmParams& g, hipStream_t s) {
+  NTParams p{};
+  p.A = (const uint16_t*)g.A;
+  p.B = (const uint16_t*)g.B;
+  p.C = g.C;
+  p.bias = g.bias;
+  p.aux = g.aux;
+  p.lda = g.a_rs;
+  p.ldb = g.b_cs;
+  p.ldc = g.c_rs;
+  p.aux_ld = g.aux_rs;
+  p.M = (int)g.M;
+  p.N = (int)g.N;
+  p.K = (int)g.K;
+  p.bias_f32 = g.bias_f32;
+  p.tiles_m = p.M / BM;
+  p.tiles_n = p.N / BN;
+  gemm_nt16_kernel<IN, OUT, ACT, BM, BN, WM, WN>
+      <<<(unsigned)(p.tiles_m * p.tiles_n), 64 * WM * WN, 0, s>>>(p);
+  return launch_status("gemm_nt16");
+}
+
+template <int IN, int OUT, int BM, int BN, int WM, int WN>
+Status run_nt(const GemmParams& g, hipStream_t s) {
+  switch (g.act) {
+    case ACT_RELU: return run_nt_act<IN, OUT, ACT_RELU, BM, BN, WM, WN>(g, s);
+    case ACT_GELU: return run_nt_act<IN, OUT, ACT_GELU, BM, BN, WM, WN>(g, s);
+    case ACT_DGELU: return run_nt_act<IN, OUT, ACT_DGELU, BM, BN, WM, WN>(g, s);
+    default: return run_nt_act<IN, OUT, ACT_NONE, BM, BN, WM, WN>(g, s);
+  }
+}
+
+// The NT fast path applies when both operands are K-contiguous 16-bit
+// matrices with 16-byte aligned rows, C (and the aux matrix) have unit column
+// stride with 8/16-byte aligned rows, bias is contiguous, and the shape tiles
+// exactly.
+template <int IN, int OUT>
+bool nt_eligible(const GemmParams& p, int BM, int BN) {
+  if (IN == IN_F32) return false;
+  if (p.a_mode != LD_KCONTIG || p.b_mode != LD_KCONTIG) return false;
+  if (p.M % BM || p.N % BN || p.K % 64) return false;
+  if ((uintptr_t)p.A % 16 || (uintptr_t)p.B % 16 || (p.a_rs * 2) % 16 || (p.b_cs * 2) % 16) return false;
+  const int osz = OUT == OUT_F32 ? 4 : 2;
+  if (p.c_cs != 1 || (uintptr_t)p.C % (4 * osz) || (p.c_rs * osz) % (4 * osz)) return false;
+  if (p.aux && (((uintptr_t)p.aux % (4 * osz)) || p.aux_rs % 4)) return false;
+  if (p.bias && (p.bias_s != 1 || (uintptr_t)p.bias % 16)) return false;
+  if (p.M > INT32_MAX / 2 || p.N > INT32_MAX / 2 || p.K > INT32_MAX / 2) return false;
+  return true;
+}
+
 template <int IN, int OUT>
 Status run_gemm(GemmParams& p, hipStream_t s) {
+  if constexpr (IN != IN_F32) {
+    const int64_t tiles256 = (p.M / 256) * (p.N / 256);
+    if (tiles256 >= 128 && nt_eligible<IN, OUT>(p, 256, 256)) return run_nt<IN, OUT, 256, 256, 2, 4>(p, s);
+    if (nt_eligible<IN, OUT>(p, 128, 128)) return run_nt<IN, OUT, 128, 128, 2, 2>(p, s);
+  }
   // Large problems: 128x128 workgroup tiles (4 waves, 64x64 per wave).
   // Smaller ones: 64x64 tiles so that enough workgroups exist.
   const int64_t big_tiles = ((p.M + 127) / 128) * ((p.N + 127) / 128);

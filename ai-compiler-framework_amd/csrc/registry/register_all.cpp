@@ -42,6 +42,7 @@ KernelVariant make_gelu_f32_variant();
 KernelVariant make_gelu_bf16_variant();
 KernelVariant make_gelu_bwd_f32_variant();
 KernelVariant make_gelu_bwd_bf16_variant();
+KernelVariant make_transpose_variant();
 // reduce.hip
 KernelVariant make_reduce_sum_lastdim_f32_variant();
 KernelVariant make_reduce_sum_lastdim_f16_to_f32_variant();
@@ -146,6 +147,7 @@ void register_all_kernels_into(KernelRegistry& R) {
   reg(OpKind::GeluBwd, make_gelu_bwd_f32_variant(), 0, "gelu_bwd_f32_v0");
   reg(OpKind::EltwiseGelu, make_gelu_bf16_variant(), 10, "gelu_bf16_v0");
   reg(OpKind::EltwiseGelu, make_gelu_f32_variant(), 0, "gelu_f32_v0");
+  reg(OpKind::Transpose, make_transpose_variant(), 0, "transpose2d_v0");
 }
 
 }  // namespace aicf::hip

@@ -156,6 +156,7 @@ const char* opkind_name(OpKind k) {
     case OpKind::SoftmaxXent: return "softmax_xent";
     case OpKind::GeluBwd: return "gelu_bwd";
     case OpKind::EltwiseGelu: return "gelu";
+    case OpKind::Transpose: return "transpose";
     case OpKind::_Count: break;
   }
   return "unknown";

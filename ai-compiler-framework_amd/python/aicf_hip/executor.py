@@ -55,7 +55,7 @@ OPNAME_TO_KIND: Dict[str, int] = {
     "batchnorm_bwd": int(_C.OpKind.BatchNormBwd), "gemm_epilogue": int(_C.OpKind.GemmEpilogue),
     "row_softmax": int(_C.OpKind.RowSoftmax), "row_reduce": int(_C.OpKind.RowReduce),
     "softmax_xent": int(_C.OpKind.SoftmaxXent), "gelu_bwd": int(_C.OpKind.GeluBwd),
-    "gelu": int(_C.OpKind.EltwiseGelu),
+    "gelu": int(_C.OpKind.EltwiseGelu), "transpose": int(_C.OpKind.Transpose),
 }
 
 

@@ -31,6 +31,7 @@ _PRIMITIVES = {
     "copy", "copy_saved", "copy_aux", "grad_zero", "adam_step", "step_inc", "bias_corr",
     "sgd_step", "gelu", "gelu_bwd", "softmax_xent", "row_softmax", "row_reduce", "mse_loss",
     "adamw_step", "layernorm_fwd", "layernorm_bwd", "batchnorm_fwd", "batchnorm_bwd",
+    "transpose",
 }
 
 _ALIASES = {"adamstep": "adam_step", "stepinc": "step_inc", "biascorr": "bias_corr",
@@ -160,6 +161,61 @@ def fuse_gemm_epilogue(ir: IRGraph, lowered: Lowered, *, fuse_bias: bool = False
     return out
 
 
+# ---------------------------------------------------------------- StageD
+def _writes(it: Dict[str, Any], vid: int) -> bool:
+    return vid in it.get("outputs", [])
+
+
+def normalize_gemm_layout(ir: IRGraph, lowered: Lowered, *, min_flops: float = 2.0 ** 30) -> Lowered:
+    """StageD (not in the reference): rewrite 16-bit GEMMs whose operands are
+    M/N-contiguous (transA=True on A, transB=False on B) into explicit 2-D
+    transposes plus the K-contiguous "NT" form (transA=False, transB=True)
+    that the fast MFMA kernel takes.  The transposed copies become new IR
+    values; a copy is reused while its source is not written in between.
+    Small GEMMs (< min_flops) are left to the general kernel."""
+    out: Lowered = []
+    cache: Dict[int, int] = {}  # source vid -> transposed vid (valid until the source is written)
+    kind = lambda it: str(it.get("op", "")).strip().lower()  # noqa: E731
+
+    def transposed(src: int) -> int:
+        if src in cache:
+            return cache[src]
+        v = ir.values[src]
+        tv = ir.new_value(name=f"{v.name}^T", shape=(v.shape[1], v.shape[0]), dtype=v.dtype,
+                          device=v.device)
+        out.append(_item("transpose", [src], [tv.id]))
+        cache[src] = tv.id
+        return tv.id
+
+    for it in lowered:
+        op = kind(it)
+        if op in ("gemm", "gemm_epilogue"):
+            a, b = int(it["inputs"][0]), int(it["inputs"][1])
+            attrs = dict(it.get("attrs", {}) or {})
+            ta, tb = bool(attrs.get("transA", False)), bool(attrs.get("transB", False))
+            dts = str(ir.values[a].dtype)
+            sa, sb = ir.values[a].shape, ir.values[b].shape
+            M = sa[1] if ta else sa[0]
+            K = sa[0] if ta else sa[1]
+            N = sb[0] if tb else sb[1]
+            big = 2.0 * M * N * K >= min_flops
+            if ("float16" in dts or "bfloat16" in dts) and big and (ta or not tb):
+                it = dict(it)
+                ins = list(it["inputs"])
+                if ta:
+                    ins[0] = transposed(a)
+                if not tb:
+                    ins[1] = transposed(b)
+                attrs["transA"], attrs["transB"] = False, True
+                it["inputs"], it["attrs"] = ins, attrs
+                it.pop("kernel_id", None)
+        for o in it.get("outputs", []):
+            for src in [s for s in cache if s == int(o)]:
+                del cache[src]
+        out.append(it)
+    return out
+
+
 # ---------------------------------------------------------------- StageB
 def _dt(ir: IRGraph, vid: int) -> str:
     return str(ir.values[int(vid)].dtype)
@@ -248,6 +304,8 @@ def pick_kernel_id(ir: IRGraph, it: Dict[str, Any]) -> Optional[str]:
         return "row_softmax_f32_v0"
     if op == "row_reduce":
         return "row_reduce_f32_v0"
+    if op == "transpose":
+        return "transpose2d_v0"
     if op in ("layernorm_fwd", "layernorm_bwd"):
         return f"{op}_{'f16' if f16 else 'f32'}_v0"
     if op in ("batchnorm_fwd", "batchnorm_bwd"):
@@ -268,11 +326,14 @@ def apply_kernel_selection(ir: IRGraph, lowered: Lowered) -> Lowered:
     return out
 
 
-def compile_lowered(ir: IRGraph, *, fuse: bool = True, fuse_bias: bool = False) -> Lowered:
-    """StageA -> StageC -> StageB."""
+def compile_lowered(ir: IRGraph, *, fuse: bool = True, fuse_bias: bool = False,
+                    nt_layout: bool = False, nt_min_flops: float = 2.0 ** 30) -> Lowered:
+    """StageA -> StageC -> (StageD) -> StageB."""
     low = lower_to_backend_ops(ir)
     if fuse:
         low = fuse_gemm_epilogue(ir, low, fuse_bias=fuse_bias)
+    if nt_layout:
+        low = normalize_gemm_layout(ir, low, min_flops=nt_min_flops)
     return apply_kernel_selection(ir, low)
 
 

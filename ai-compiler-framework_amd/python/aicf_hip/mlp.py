@@ -112,7 +112,8 @@ class FlatLayout:
 
 def build_mlp_mse(B: int = 8192, D: int = 4096, L: int = 4, *, lr: float = 1e-3,
                   beta1: float = 0.9, beta2: float = 0.999, eps: float = 1e-8,
-                  weight_decay: float = 0.0, dead_dx: bool = True, device: str = "cuda:0"):
+                  weight_decay: float = 0.0, dead_dx: bool = True, nt_layout: bool = True,
+                  nt_min_flops: float = 2.0 ** 30, device: str = "cuda:0"):
     """bf16 activations/weights, fp32 master parameters in one flat buffer."""
     ir = IRGraph(name=f"mlp_mse_{B}x{D}x{L}")
     lay = FlatLayout(D, L)
@@ -162,7 +163,7 @@ def build_mlp_mse(B: int = 8192, D: int = 4096, L: int = 4, *, lr: float = 1e-3,
     ir.emit(op="AdamWStep", inputs=[P, Gf, Mf, Vf, step], outputs=[P, Mf, Vf, Wb],
             attrs={"lr": lr, "beta1": beta1, "beta2": beta2, "eps": eps,
                    "weight_decay": weight_decay})
-    lowered = compile_lowered(ir, fuse_bias=True)
+    lowered = compile_lowered(ir, fuse_bias=True, nt_layout=nt_layout, nt_min_flops=nt_min_flops)
     plan = build_binding_plan(ir, opts=PlanOptions(param_names={"flat.params"}))
     return ir, lowered, plan
 
@@ -273,7 +274,7 @@ def check_mlp_small(device: str = "cuda:0", verbose: bool = False, B=64, din=784
 
 
 def check_mlp_mse_small(B: int = 256, D: int = 256, L: int = 4, device: str = "cuda:0",
-                        steps: int = 3) -> Dict[str, object]:
+                        steps: int = 3, nt_layout: bool = True) -> Dict[str, object]:
     """Runs the bf16 MSE MLP (same graph and kernels as the benchmark, smaller
     shape) eagerly for one step and as a captured graph for `steps`-1 more,
     and checks each step against the CPU oracle: an fp64 chain that rounds
@@ -282,7 +283,9 @@ def check_mlp_mse_small(B: int = 256, D: int = 256, L: int = 4, device: str = "c
     own gradients (updated parameters, moments and bf16 shadow bit-exact)."""
     import oracle as orc  # test infrastructure
 
-    ir, lowered, plan = build_mlp_mse(B, D, L, device=device)
+    # nt_min_flops=0: take the transpose + NT-kernel route at every size, as
+    # the benchmark shape does
+    ir, lowered, plan = build_mlp_mse(B, D, L, device=device, nt_layout=nt_layout, nt_min_flops=0)
     lay = FlatLayout(D, L)
     ex = make_executor(ir, lowered, plan, device)
     inputs, params = init_mlp_mse(B, D, L, seed=1, device=device)

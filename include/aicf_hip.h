@@ -69,7 +69,8 @@ extern "C" {
 #define AICF_OP_SOFTMAX_XENT 20 /* logits, labels -> loss, dlogits, argmax, row loss */
 #define AICF_OP_GELU_BWD 21     /* dOut, Z -> dOut * gelu_tanh'(Z) */
 #define AICF_OP_ELTWISE_GELU 22 /* X -> gelu_tanh(X) */
-#define AICF_OP_COUNT 23
+#define AICF_OP_TRANSPOSE 23    /* X[R,C] -> X^T[C,R] (2-D, row-major) */
+#define AICF_OP_COUNT 24
 
 /*
  * Attribute schema ids (numeric ABI).  The reference mixes big-endian fourccs

@@ -101,3 +101,26 @@ def test_runtime_trace_and_numerics(C, graph):
         # within an f16 ulp or two of the emulated chain
         assert orc.rel_err(got, want) < 4e-3, k
         assert not np.array_equal(got, p), k  # the step did update
+
+
+def test_stage_d_rewrites_backward_gemms_to_nt():
+    """StageD turns every bf16 backward GEMM into transposes + the
+    K-contiguous form and reuses a transposed copy until its source changes."""
+    from aicf_hip import mlp
+
+    ir, lowered, _ = mlp.build_mlp_mse(8192, 4096, 4)
+    gemms = [it for it in lowered if it["op"] in ("gemm", "gemm_epilogue")]
+    assert len(gemms) == 12
+    for it in gemms:
+        assert not it["attrs"].get("transA", False) and it["attrs"].get("transB", False)
+    tr = [it for it in lowered if it["op"] == "transpose"]
+    assert len(tr) == 12  # 4 weights, 4 output grads, 4 layer inputs
+    srcs = [it["inputs"][0] for it in tr]
+    assert len(set(srcs)) == len(srcs)
+    # every transposed value is produced before it is consumed
+    made = set()
+    for it in lowered:
+        for v in it["inputs"]:
+            if ir.values[v].name.endswith("^T"):
+                assert v in made
+        made.update(it["outputs"])

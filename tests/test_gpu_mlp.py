@@ -17,12 +17,13 @@ def test_mlp_xent_fp32_reference_config(C):
     assert res["ok"], res
 
 
-@pytest.mark.parametrize("B,D,L", [(256, 256, 4), (512, 384, 3)])
-def test_mlp_mse_bf16_graph(C, B, D, L):
-    """The benchmark's bf16 GELU/MSE/AdamW graph at a reduced shape."""
+@pytest.mark.parametrize("B,D,L,nt", [(256, 256, 4, True), (512, 384, 3, True), (256, 256, 2, False)])
+def test_mlp_mse_bf16_graph(C, B, D, L, nt):
+    """The benchmark's bf16 GELU/MSE/AdamW graph at a reduced shape, with the
+    transpose + NT-GEMM lowering (nt) and with the general GEMM kernel."""
     from aicf_hip import mlp
 
-    res = mlp.check_mlp_mse_small(B, D, L)
+    res = mlp.check_mlp_mse_small(B, D, L, nt_layout=nt)
     assert res["ok"], res
 
 

@@ -407,6 +407,7 @@ def test_gemm_f16_probe_shapes(C, ta, tb):
 
 
 @pytest.mark.parametrize("M,N,K,ta,tb", [
+    (4096, 4096, 128, False, True),   # 256x256-tile fast path
     (1024, 1024, 1024, False, True),
     (100, 72, 784, False, True),
     (64, 256, 784, False, True),
@@ -470,7 +471,8 @@ def test_gemm_epilogue_default_is_bias_relu_and_gepi_kinds(C):
         assert orc.rel_err(h(o), fn(base)) < 1e-4, kind
 
 
-@pytest.mark.parametrize("M,N,K", [(256, 512, 384), (1024, 1024, 1024), (100, 200, 64)])
+@pytest.mark.parametrize("M,N,K", [(256, 512, 384), (1024, 1024, 1024), (100, 200, 64),
+                                   (4096, 4096, 64)])
 def test_gemm_epilogue_bf16_gelu_aux_and_dgelu(C, M, N, K):
     r = rng(15)
     s = 1.0 / np.sqrt(K)
@@ -510,6 +512,21 @@ def test_gemm_neg_cases_raise(C):
                        [torch.empty((64, 81), device="cuda")])
     with pytest.raises(RuntimeError):
         C.op_call(int(C.OpKind.Gemm), [A.cpu(), B], [torch.empty((64, 80), device="cuda")])
+
+
+@pytest.mark.parametrize("R,Ccols,dtype", [(64, 64, "bf16"), (4096, 8192, "bf16"), (100, 37, "f32"),
+                                           (300, 129, "bf16"), (8192, 256, "f32")])
+def test_transpose(C, R, Ccols, dtype):
+    r = rng(R * Ccols)
+    x = r.standard_normal((R, Ccols)).astype(np.float32)
+    if dtype == "bf16":
+        xb = orc.bf16_bits_from_f32(x)
+        tx, want = g(xb, torch.bfloat16), np.ascontiguousarray(xb.reshape(R, Ccols).T)
+    else:
+        tx, want = g(x), np.ascontiguousarray(x.T)
+    y = torch.empty((Ccols, R), dtype=tx.dtype, device="cuda")
+    C.op_call(int(C.OpKind.Transpose), [tx], [y], 0, b"", 0)
+    assert np.array_equal(h(y), want)  # pure data movement: bit-exact
 
 
 # ============================================================== graph
