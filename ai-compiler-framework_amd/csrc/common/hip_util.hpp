@@ -96,23 +96,24 @@ __device__ __forceinline__ float wave_max(float v) {
 
 // ---- GELU (tanh approximation) ---------------------------------------------
 // gelu(x) = 0.5 x (1 + tanh(u)),  u = sqrt(2/pi) (x + 0.044715 x^3)
-// gelu'(x) = 0.5 (1 + t) + 0.5 x (1 - t^2) sqrt(2/pi) (1 + 3*0.044715 x^2)
-// tanh(u) = 1 - 2 / (1 + e^{2u}): exact limits +-1 when e^{2u} overflows or
-// underflows; its absolute error (a few 1e-8) enters gelu only through
-// (1 + t), i.e. as a relative error of the same size.
-__device__ __forceinline__ float tanh_fast(float u) {
-  return 1.0f - 2.0f / (1.0f + __expf(2.0f * u));
+// Since 0.5 (1 + tanh(u)) = sigmoid(2u) = s:
+//   gelu(x)  = x s,            s = 1 / (1 + 2^{x (a + b x^2)})
+//   gelu'(x) = s + s (1 - s) x (2 k0 + 6 k0 k1 x^2)
+// with a = -2 k0 log2(e), b = -2 k0 k1 log2(e).  One v_exp_f32 and one
+// v_rcp_f32 (each ~1 ulp), no IEEE divide: relative error a few 1e-7.
+// Limits: 2^(..) overflowing to +inf gives s = 0 (gelu -> -0, gelu' -> 0);
+// underflowing to 0 gives s = 1 (gelu -> x, gelu' -> 1).
+__device__ __forceinline__ float gelu_sigmoid_arg(float x) {
+  const float a = -2.302208198144325f, b = -0.1029432395800235f;  // -2k0/ln2, -2k0k1/ln2
+  return 1.0f + __builtin_amdgcn_exp2f(x * fmaf(b, x * x, a));
 }
 __device__ __forceinline__ float gelu_tanh_f(float x) {
-  const float k0 = 0.7978845608028654f, k1 = 0.044715f;
-  const float u = k0 * (x + k1 * x * x * x);
-  return 0.5f * x * (1.0f + tanh_fast(u));
+  return x * __builtin_amdgcn_rcpf(gelu_sigmoid_arg(x));
 }
 __device__ __forceinline__ float gelu_tanh_grad_f(float x) {
-  const float k0 = 0.7978845608028654f, k1 = 0.044715f;
-  const float x2 = x * x;
-  const float t = tanh_fast(k0 * (x + k1 * x2 * x));
-  return 0.5f * (1.0f + t) + 0.5f * x * (1.0f - t * t) * k0 * (1.0f + 3.0f * k1 * x2);
+  const float c2 = 1.5957691216057308f, c3 = 0.21406444881780076f;  // 2k0, 6k0k1
+  const float s = __builtin_amdgcn_rcpf(gelu_sigmoid_arg(x));
+  return fmaf(s * (1.0f - s), x * fmaf(c3, x * x, c2), s);
 }
 
 }  // namespace aicf::hip

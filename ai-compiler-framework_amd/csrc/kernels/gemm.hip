@@ -374,17 +374,17 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_kernel(GemmParams p) {
 //   * global -> LDS with gfx950's direct 16-byte LDS loads
 //     (global_load_lds_dwordx4): lane i of a wave fills bytes [16i, 16i+16)
 //     of a 1 KB LDS block = 8 rows of 64 K-elements, so there is no VGPR
-//     staging and no ds_write; the XOR swizzle (chunk ^ row%8) that keeps the
-//     fragment reads bank-conflict free is applied by choosing which global
-//     chunk each lane fetches;
-//   * two LDS stages: the loads of K-step k+1 are issued right after the
-//     barrier of step k and waited for once at its end;
-//   * inside a K-step the MFMA fragments of sub-step s+1 are read from LDS
-//     while the MFMAs of sub-step s run (two register sets), interleaved one
-//     ds_read per few MFMAs with sched_group_barrier;
+//     staging and no ds_write; the XOR swizzle that keeps the fragment reads
+//     bank-conflict free is applied by choosing which global chunk each lane
+//     fetches;
+//   * two LDS stages and one barrier per K-step, placed before the last
+//     sub-step so that no wave waits on LDS after it;
+//   * the MFMA fragments of sub-step s+1 are read from LDS while the MFMAs of
+//     sub-step s run (two register sets), interleaved one ds_read per few
+//     MFMAs with sched_group_barrier;
 //   * MFMA operands swapped (A-operand = W rows, B-operand = X rows) so that
-//     each lane holds 4 consecutive output columns of one row and the
-//     epilogue stores 8 (bf16) or 16 (fp32) contiguous bytes per lane;
+//     each lane holds 4 consecutive output columns of one row;
+//   * the epilogue stages the output tile through LDS and stores whole rows;
 //   * the activation is a template parameter; bias and the pre-activation
 //     output are uniform runtime flags.
 // ---------------------------------------------------------------------------
@@ -403,48 +403,178 @@ struct NTParams {
   int tiles_m, tiles_n;
 };
 
-template <int OUT, int ACT>
-__device__ __forceinline__ void nt_epilogue4(const NTParams& p, int m, int n, float* v) {
-  if constexpr (ACT == ACT_DGELU) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] *= gelu_tanh_grad_f(load_out<OUT>(p.aux, (int64_t)m * p.aux_ld + n + e));
-  } else {
+// Epilogue of the NT kernels.  Block (i, j) of the accumulators holds D[n][m];
+// this lane has m = .. + fr and n = .. + 8g + 4fh + {0..3} in
+// acc[i][j][4g .. 4g+3].  The fragments go through LDS (`smem`, at least
+// STAGE_BYTES, free when this is called) so that every global store, and the
+// load of the dGELU pre-activation, moves whole 512-1024 byte rows.  LDS rows
+// hold 16-byte chunks XOR-swizzled by row, which keeps both the fragment
+// writes (32 rows, one chunk each) and the row reads bank-balanced.  A tile
+// that does not fit (fp32 256x256) is done in passes over the wave's 32-row
+// fragment groups.
+template <int OUT, int ACT, int BM, int BN, int WM, int WN, int STAGE_BYTES>
+__device__ __forceinline__ void nt_epilogue_staged(const NTParams& p,
+                                                   floatx16 (&acc)[BN / WN / 32][BM / WM / 32],
+                                                   uint8_t* smem, int m0, int n0) {
+  constexpr int NW = WM * WN;
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int TM = WTM / 32, TN = WTN / 32;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int fr = lane & 31, fh = lane >> 5;
+  constexpr int NT = 64 * NW;
+  constexpr int OB = OUT == OUT_F32 ? 4 : 2;
+  constexpr int ROWB = BN * OB;    // bytes per staged row
+  constexpr int CPR = ROWB / 16;   // 16-byte chunks per row
+  constexpr int ROWS_PASS = STAGE_BYTES / ROWB < BM ? STAGE_BYTES / ROWB : BM;
+  constexpr int NPASS = BM / ROWS_PASS;
+  constexpr int JP = TM / NPASS;   // 32-row fragment groups per wave per pass
+  constexpr int WROWS = JP * 32;   // rows per wave per pass
+  static_assert(NPASS * ROWS_PASS == BM && JP * NPASS == TM, "pass split");
+  static_assert((CPR & (CPR - 1)) == 0 && (ROWS_PASS * CPR) % NT == 0, "chunk split");
+  uint8_t* const tile = smem;
+
+  if constexpr (ACT != ACT_DGELU) {
     if (p.bias) {
-      if (p.bias_f32) {
-        const f32x4 b = *reinterpret_cast<const f32x4*>((const float*)p.bias + n);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] += b[e];
-      } else {
+      for (int i = 0; i < TN; ++i)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] += load_out<OUT>(p.bias, n + e);
-      }
-    }
-    if constexpr (ACT == ACT_RELU) {
+        for (int g = 0; g < 4; ++g) {
+          const int n = n0 + wn * WTN + i * 32 + 8 * g + 4 * fh;
+          float b[4];
+          if (p.bias_f32) {
+            const f32x4 bv = *reinterpret_cast<const f32x4*>((const float*)p.bias + n);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = v[e] > 0.0f ? v[e] : 0.0f;
-    } else if constexpr (ACT == ACT_GELU) {
-      if (p.aux) {
-        if constexpr (OUT == OUT_F32) {
-          *reinterpret_cast<f32x4*>((float*)p.aux + (int64_t)m * p.aux_ld + n) = f32x4{v[0], v[1], v[2], v[3]};
-        } else {
-          u16x4 z;
+            for (int e = 0; e < 4; ++e) b[e] = bv[e];
+          } else {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) z[e] = OUT == OUT_BF16 ? f32_to_bf16(v[e]) : f32_to_f16(v[e]);
-          *reinterpret_cast<u16x4*>((uint16_t*)p.aux + (int64_t)m * p.aux_ld + n) = z;
+            for (int e = 0; e < 4; ++e) b[e] = load_out<OUT>(p.bias, n + e);
+          }
+#pragma unroll
+          for (int j = 0; j < TM; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[i][j][4 * g + e] += b[e];
         }
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = gelu_tanh_f(v[e]);
     }
   }
-  const int64_t idx = (int64_t)m * p.ldc + n;
-  if constexpr (OUT == OUT_F32) {
-    *reinterpret_cast<f32x4*>((float*)p.C + idx) = f32x4{v[0], v[1], v[2], v[3]};
-  } else {
-    u16x4 o;
+
+  // byte offset of this lane's 4 outputs of fragment (jj, i, g) in the tile
+  auto slot = [&](int jj, int i, int g) -> int {
+    const int pr = wm * WROWS + jj * 32 + fr;
+    int c, half;
+    if constexpr (OB == 2) {
+      c = (wn * WTN + i * 32) / 8 + g;
+      half = fh * 8;
+    } else {
+      c = (wn * WTN + i * 32) / 4 + 2 * g + fh;
+      half = 0;
+    }
+    return pr * ROWB + ((c ^ (pr & (CPR - 1))) * 16) + half;
+  };
+  auto put4 = [&](int off, const float* v) {
+    if constexpr (OB == 4) {
+      *reinterpret_cast<f32x4*>(tile + off) = f32x4{v[0], v[1], v[2], v[3]};
+    } else {
+      u16x4 o;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) o[e] = OUT == OUT_BF16 ? f32_to_bf16(v[e]) : f32_to_f16(v[e]);
-    *reinterpret_cast<u16x4*>((uint16_t*)p.C + idx) = o;
+      for (int e = 0; e < 4; ++e) o[e] = OUT == OUT_BF16 ? f32_to_bf16(v[e]) : f32_to_f16(v[e]);
+      *reinterpret_cast<u16x4*>(tile + off) = o;
+    }
+  };
+  auto get4 = [&](int off, float* v) {
+    if constexpr (OB == 4) {
+      const f32x4 x = *reinterpret_cast<const f32x4*>(tile + off);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = x[e];
+    } else {
+      const u16x4 x = *reinterpret_cast<const u16x4*>(tile + off);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = OUT == OUT_BF16 ? bf16_to_f32(x[e]) : f16_to_f32(x[e]);
+    }
+  };
+  // global row of staged row pr in pass `pass`
+  auto grow = [&](int pass, int pr) -> int64_t {
+    return (int64_t)m0 + (pr / WROWS) * WTM + pass * WROWS + (pr % WROWS);
+  };
+  // tile rows of this pass -> global matrix (row stride ld elements)
+  auto copy_out = [&](int pass, void* dst, int64_t ld) {
+#pragma unroll
+    for (int k = 0; k < ROWS_PASS * CPR / NT; ++k) {
+      const int idx = threadIdx.x + k * NT;
+      const int pr = idx / CPR, c = idx % CPR;
+      const u16x8 x = *reinterpret_cast<const u16x8*>(tile + pr * ROWB + ((c ^ (pr & (CPR - 1))) * 16));
+      *reinterpret_cast<u16x8*>((uint8_t*)dst + (grow(pass, pr) * ld + n0) * OB + c * 16) = x;
+    }
+  };
+  // global matrix -> tile rows of this pass, straight into LDS (no VGPRs:
+  // the accumulators are live).  Wave instruction q fills the 1 KB at
+  // tile + 1024 q, i.e. physical chunks idx = 64 q + lane; the lane fetches
+  // the logical chunk stored there.
+  auto copy_in = [&](int pass, const void* src, int64_t ld) {
+    const int wave_id = threadIdx.x >> 6;
+#pragma unroll
+    for (int k = 0; k < ROWS_PASS * CPR / NT; ++k) {
+      const int q = wave_id + k * NW;
+      const int idx = q * 64 + lane;
+      const int pr = idx / CPR, c = (idx % CPR) ^ (pr & (CPR - 1));
+      __builtin_amdgcn_global_load_lds(
+          (glb_void_t*)((const uint8_t*)src + (grow(pass, pr) * ld + n0) * OB + c * 16),
+          (lds_void_t*)(tile + q * 1024), 16, 0, 0);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+  };
+
+#pragma unroll
+  for (int pass = 0; pass < NPASS; ++pass) {
+    if constexpr (ACT == ACT_DGELU) {
+      copy_in(pass, p.aux, p.aux_ld);
+      __syncthreads();
+    }
+    if constexpr (ACT == ACT_GELU) {
+      if (p.aux) {  // pre-activation z
+#pragma unroll
+        for (int jj = 0; jj < JP; ++jj)
+#pragma unroll
+          for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+              float v[4];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) v[e] = acc[i][pass * JP + jj][4 * g + e];
+              put4(slot(jj, i, g), v);
+            }
+        __syncthreads();
+        copy_out(pass, p.aux, p.aux_ld);
+        __syncthreads();
+      }
+    }
+#pragma unroll
+    for (int jj = 0; jj < JP; ++jj)
+#pragma unroll
+      for (int i = 0; i < TN; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int off = slot(jj, i, g);
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = acc[i][pass * JP + jj][4 * g + e];
+          if constexpr (ACT == ACT_DGELU) {
+            float z[4];
+            get4(off, z);  // this lane's own slot: no barrier between read and write
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] *= gelu_tanh_grad_f(z[e]);
+          } else if constexpr (ACT == ACT_RELU) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = v[e] > 0.0f ? v[e] : 0.0f;
+          } else if constexpr (ACT == ACT_GELU) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = gelu_tanh_f(v[e]);
+          }
+          put4(off, v);
+        }
+    __syncthreads();
+    copy_out(pass, p.C, p.ldc);
+    if (pass + 1 < NPASS) __syncthreads();
   }
 }
 
@@ -466,24 +596,32 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt16_kernel(NTParams p) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / WN, wn = wave % WN;
 
-  // slot `lane` of a 1 KB block holds row lane/8, physical chunk lane%8,
-  // i.e. logical chunk (lane%8) ^ (lane/8)
+  // LDS layout of a stage: 1 KB blocks of 8 rows x 64 K-elements (128 B per
+  // row = 8 chunks of 16 B); row r stores logical chunk c at physical chunk
+  // c ^ ((r >> 1) & 7).  Any 16 consecutive rows of one logical chunk then
+  // cover all 64 banks, so the fragment reads (ds_read_b128, 32 rows) are
+  // conflict-free.  Slot `lane` of block j is row 8j + lane/8, physical chunk
+  // lane%8; the loader picks the matching global chunk, which depends on the
+  // parity of j.
   const int r_in = lane >> 3;
-  const int c_log = (lane & 7) ^ r_in;
-  const uint16_t* a_src = p.A + (int64_t)(m0 + r_in) * p.lda + c_log * 8;
-  const uint16_t* b_src = p.B + (int64_t)(n0 + r_in) * p.ldb + c_log * 8;
+  const int cl_even = (lane & 7) ^ (r_in >> 1);
+  const int cl_odd = (lane & 7) ^ ((4 + (r_in >> 1)) & 7);
+  const uint16_t* a_row = p.A + (int64_t)(m0 + r_in) * p.lda;
+  const uint16_t* b_row = p.B + (int64_t)(n0 + r_in) * p.ldb;
 
   auto issue_loads = [&](int kt, int stage) {
     uint8_t* base = smem + stage * STAGE;
     const int64_t koff = (int64_t)kt * BK;
 #pragma unroll
     for (int j = wave; j < BM / 8; j += NW)
-      __builtin_amdgcn_global_load_lds((glb_void_t*)(a_src + (int64_t)j * 8 * p.lda + koff),
-                                       (lds_void_t*)(base + j * 1024), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(
+          (glb_void_t*)(a_row + (int64_t)j * 8 * p.lda + koff + ((j & 1) ? cl_odd : cl_even) * 8),
+          (lds_void_t*)(base + j * 1024), 16, 0, 0);
 #pragma unroll
     for (int j = wave; j < BN / 8; j += NW)
-      __builtin_amdgcn_global_load_lds((glb_void_t*)(b_src + (int64_t)j * 8 * p.ldb + koff),
-                                       (lds_void_t*)(base + A_BYTES + j * 1024), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(
+          (glb_void_t*)(b_row + (int64_t)j * 8 * p.ldb + koff + ((j & 1) ? cl_odd : cl_even) * 8),
+          (lds_void_t*)(base + A_BYTES + j * 1024), 16, 0, 0);
   };
 
   floatx16 acc[TN][TM];
@@ -500,64 +638,74 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt16_kernel(NTParams p) {
   for (int j = 0; j < TM; ++j) a_off[j] = (wm * WTM + j * 32 + fr) * 128;
 #pragma unroll
   for (int i = 0; i < TN; ++i) b_off[i] = A_BYTES + (wn * WTN + i * 32 + fr) * 128;
-  const int rsw = fr & 7;
+  const int rsw = (fr >> 1) & 7;  // fragment rows start at multiples of 32
 
-  const int nk = p.K / BK;
-  issue_loads(0, 0);
-  for (int kt = 0; kt < nk; ++kt) {
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (kt + 1 < nk) issue_loads(kt + 1, (kt + 1) & 1);
-    const uint8_t* st = smem + (kt & 1) * STAGE;
-    u16x8 fa[2][TM], fb[2][TN];
-    {
-      const int chunk = (fh ^ rsw) * 16;
+  u16x8 fa[2][TM], fb[2][TN];
+  auto read_frags = [&](const uint8_t* st, int kk, int buf) {
+    const int chunk = ((kk * 2 + fh) ^ rsw) * 16;
 #pragma unroll
-      for (int j = 0; j < TM; ++j) fa[0][j] = *reinterpret_cast<const u16x8*>(st + a_off[j] + chunk);
+    for (int j = 0; j < TM; ++j) fa[buf][j] = *reinterpret_cast<const u16x8*>(st + a_off[j] + chunk);
 #pragma unroll
-      for (int i = 0; i < TN; ++i) fb[0][i] = *reinterpret_cast<const u16x8*>(st + b_off[i] + chunk);
-    }
-#pragma unroll
-    for (int kk = 0; kk < KS; ++kk) {
-      const int cb = kk & 1, nb = cb ^ 1;
-      if (kk + 1 < KS) {
-        const int chunk = (((kk + 1) * 2 + fh) ^ rsw) * 16;
-#pragma unroll
-        for (int j = 0; j < TM; ++j) fa[nb][j] = *reinterpret_cast<const u16x8*>(st + a_off[j] + chunk);
-#pragma unroll
-        for (int i = 0; i < TN; ++i) fb[nb][i] = *reinterpret_cast<const u16x8*>(st + b_off[i] + chunk);
-      }
-#pragma unroll
-      for (int i = 0; i < TN; ++i)
-#pragma unroll
-        for (int j = 0; j < TM; ++j)
-          acc[i][j] = mfma32<IN>(reinterpret_cast<const uint16_t*>(&fb[cb][i]),
-                                 reinterpret_cast<const uint16_t*>(&fa[cb][j]), acc[i][j]);
-      if (kk + 1 < KS) {
-#pragma unroll
-        for (int t = 0; t < TM + TN; ++t) {
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                      // one ds_read
-          __builtin_amdgcn_sched_group_barrier(0x008, (TM * TN) / (TM + TN), 0);  // some MFMAs
-        }
-      }
-    }
-  }
-
-  // Epilogue: block (i, j) holds D[n][m]; this lane has m = .. + fr and
-  // n = .. + 8g + 4fh + {0..3} in acc[i][j][4g .. 4g+3].
-#pragma unroll
-  for (int j = 0; j < TM; ++j) {
-    const int m = m0 + wm * WTM + j * 32 + fr;
+    for (int i = 0; i < TN; ++i) fb[buf][i] = *reinterpret_cast<const u16x8*>(st + b_off[i] + chunk);
+  };
+  auto mfmas = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < TN; ++i)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        float v[4];
+      for (int j = 0; j < TM; ++j)
+        acc[i][j] = mfma32<IN>(reinterpret_cast<const uint16_t*>(&fb[buf][i]),
+                               reinterpret_cast<const uint16_t*>(&fa[buf][j]), acc[i][j]);
+  };
+  // one ds_read per few MFMAs
+  auto interleave = [&]() {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * g + e];
-        nt_epilogue4<OUT, ACT>(p, m, n0 + wn * WTN + i * 32 + 8 * g + 4 * fh, v);
-      }
+    for (int t = 0; t < TM + TN; ++t) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, (TM * TN) / (TM + TN), 0);
+    }
+  };
+
+  // Pipeline: a K-step has KS sub-steps; the fragments of sub-step s+1 are
+  // read while the MFMAs of sub-step s run.  The only barrier of a K-step
+  // sits before its last sub-step (whose fragments are already in
+  // registers): after it the next stage is visible to every wave (so its
+  // first fragments are read during the last MFMAs) and the current stage
+  // is no longer read by anyone (so the loads of K-step kt+2 refill it).
+  const int nk = p.K / BK;
+  constexpr int LAST = (KS - 1) & 1;  // fragment buffer of the last sub-step
+  issue_loads(0, 0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (nk > 1) issue_loads(1, 1);
+  read_frags(smem, 0, 0);
+  for (int kt = 0; kt + 1 < nk; ++kt) {
+    const uint8_t* st = smem + (kt & 1) * STAGE;
+#pragma unroll
+    for (int kk = 0; kk < KS - 1; ++kk) {
+      read_frags(st, kk + 1, (kk & 1) ^ 1);
+      mfmas(kk & 1);
+      interleave();
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // own loads of K-step kt+1 and fragment reads done
+    __syncthreads();
+    if (kt + 2 < nk) issue_loads(kt + 2, kt & 1);
+    read_frags(smem + ((kt + 1) & 1) * STAGE, 0, LAST ^ 1);
+    mfmas(LAST);
+    interleave();
   }
+  {
+    const uint8_t* st = smem + ((nk - 1) & 1) * STAGE;
+#pragma unroll
+    for (int kk = 0; kk < KS - 1; ++kk) {
+      read_frags(st, kk + 1, (kk & 1) ^ 1);
+      mfmas(kk & 1);
+      interleave();
+    }
+    mfmas(LAST);
+  }
+
+  __syncthreads();  // every wave is done reading the last stage
+  nt_epilogue_staged<OUT, ACT, BM, BN, WM, WN, 2 * STAGE>(p, acc, smem, m0, n0);
 }
 
 // ---------------------------------------------------------------------------
@@ -679,7 +827,7 @@ Status run_nt(const GemmParams& g, hipStream_t s) {
 
 // The NT fast path applies when both operands are K-contiguous 16-bit
 // matrices with 16-byte aligned rows, C (and the aux matrix) have unit column
-// stride with 8/16-byte aligned rows, bias is contiguous, and the shape tiles
+// stride with 16-byte aligned rows, bias is contiguous, and the shape tiles
 // exactly.
 template <int IN, int OUT>
 bool nt_eligible(const GemmParams& p, int BM, int BN) {
@@ -688,8 +836,8 @@ bool nt_eligible(const GemmParams& p, int BM, int BN) {
   if (p.M % BM || p.N % BN || p.K % 64) return false;
   if ((uintptr_t)p.A % 16 || (uintptr_t)p.B % 16 || (p.a_rs * 2) % 16 || (p.b_cs * 2) % 16) return false;
   const int osz = OUT == OUT_F32 ? 4 : 2;
-  if (p.c_cs != 1 || (uintptr_t)p.C % (4 * osz) || (p.c_rs * osz) % (4 * osz)) return false;
-  if (p.aux && (((uintptr_t)p.aux % (4 * osz)) || p.aux_rs % 4)) return false;
+  if (p.c_cs != 1 || (uintptr_t)p.C % 16 || (p.c_rs * osz) % 16) return false;
+  if (p.aux && (((uintptr_t)p.aux % 16) || (p.aux_rs * osz) % 16)) return false;
   if (p.bias && (p.bias_s != 1 || (uintptr_t)p.bias % 16)) return false;
   if (p.M > INT32_MAX / 2 || p.N > INT32_MAX / 2 || p.K > INT32_MAX / 2) return false;
   return true;

@@ -139,7 +139,17 @@ __global__ __launch_bounds__(256) void adamw_vec4_kernel(
     const float* __restrict__ V, float* __restrict__ Pout, float* __restrict__ Mout,
     float* __restrict__ Vout, uint16_t* __restrict__ Wb, int64_t n4, AdamWArgs a,
     const int32_t* __restrict__ stepp) {
-  const AdamWScalars s = adamw_scalars(stepp, a);
+  // the bias corrections (two fp64 pow) are computed by one wave per block
+  __shared__ float sh[2];
+  if (threadIdx.x < 64) {
+    const AdamWScalars t = adamw_scalars(stepp, a);
+    if (threadIdx.x == 0) {
+      sh[0] = t.step;
+      sh[1] = t.ibc2;
+    }
+  }
+  __syncthreads();
+  const AdamWScalars s{sh[0], sh[1]};
   const int64_t base = (int64_t)blockIdx.x * (256 * UNROLL) + threadIdx.x;
   f32x4 p[UNROLL], g[UNROLL], m[UNROLL], v[UNROLL];
 #pragma unroll
@@ -190,7 +200,7 @@ __global__ __launch_bounds__(256) void adamw_scalar_kernel(
   if (Wb) Wb[i] = f32_to_bf16(p);
 }
 
-constexpr int kAdamUnroll = 2;
+constexpr int kAdamUnroll = 1;  // measured best on MI355X (more blocks in flight)
 
 // ---------------------------------------------------------------------------
 // Host glue: Adam

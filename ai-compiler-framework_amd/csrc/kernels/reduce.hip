@@ -32,10 +32,12 @@ KernelVariant make(const char* name, LaunchFn l, SupportedFn s, uint32_t schema 
 
 // ===========================================================================
 // Column sum: dY [M, N] (leading dims flattened) -> out [N].
-// Each lane owns one column (waves read 64 consecutive columns per row);
-// the RS row-slices of a workgroup are combined in LDS in a fixed order.
+// Vector kernel (N a multiple of the 16-byte vector): each lane owns 16
+// bytes of columns, so a wave reads 1 KB of one row per load and keeps 8
+// such loads in flight; scalar kernel otherwise (one column per lane).  The
+// RS row-slices (waves) of a workgroup are combined in LDS in a fixed order.
 // With a partials buffer [P, N] the rows are also split over P workgroup
-// rows and a second pass adds the P partials in order.
+// rows and a second pass adds the P partials in a fixed order.
 // ===========================================================================
 template <typename TI, bool BF16IN>
 __device__ __forceinline__ float load_elem(const TI* p, int64_t i) {
@@ -86,14 +88,89 @@ __global__ __launch_bounds__(256) void colsum_kernel(const TI* __restrict__ x, v
   }
 }
 
+template <typename TI, bool BF16IN>
+__device__ __forceinline__ void add_vec16(float* acc, const uint4& v) {
+  if constexpr (sizeof(TI) == 4) {
+    acc[0] += __uint_as_float(v.x);
+    acc[1] += __uint_as_float(v.y);
+    acc[2] += __uint_as_float(v.z);
+    acc[3] += __uint_as_float(v.w);
+  } else {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint16_t lo = (uint16_t)(w[k] & 0xffffu), hi = (uint16_t)(w[k] >> 16);
+      acc[2 * k] += BF16IN ? bf16_to_f32(lo) : f16_to_f32(lo);
+      acc[2 * k + 1] += BF16IN ? bf16_to_f32(hi) : f16_to_f32(hi);
+    }
+  }
+}
+
+template <typename TI, bool BF16IN, bool OUT_F16>
+__global__ __launch_bounds__(256) void colsum_vec_kernel(const TI* __restrict__ x, void* __restrict__ out,
+                                                         float* __restrict__ partial, int64_t M,
+                                                         int64_t N, int64_t rows_per_part) {
+  constexpr int VEC = 16 / sizeof(TI);
+  constexpr int CB = 64 * VEC;  // columns per workgroup
+  constexpr int UNROLL = 8;
+  __shared__ float red[kColRS][CB];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t c0 = (int64_t)blockIdx.x * CB + lane * VEC;
+  const int64_t r0 = (int64_t)blockIdx.y * rows_per_part;
+  const int64_t r1 = r0 + rows_per_part < M ? r0 + rows_per_part : M;
+  float acc[VEC];
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) acc[e] = 0.0f;
+  if (c0 < N) {  // N % VEC == 0: the whole vector is in range
+    int64_t r = r0 + w;
+    for (; r + (UNROLL - 1) * kColRS < r1; r += UNROLL * kColRS) {
+      uint4 v[UNROLL];
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u)
+        v[u] = *reinterpret_cast<const uint4*>(x + (r + u * kColRS) * N + c0);
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) add_vec16<TI, BF16IN>(acc, v[u]);
+    }
+    for (; r < r1; r += kColRS) add_vec16<TI, BF16IN>(acc, *reinterpret_cast<const uint4*>(x + r * N + c0));
+  }
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) red[w][lane * VEC + e] = acc[e];
+  __syncthreads();
+  for (int cc = threadIdx.x; cc < CB; cc += 256) {
+    const int64_t col = (int64_t)blockIdx.x * CB + cc;
+    if (col >= N) break;
+    const float s = (red[0][cc] + red[1][cc]) + (red[2][cc] + red[3][cc]);
+    if (partial) {
+      partial[(int64_t)blockIdx.y * N + col] = s;
+    } else if constexpr (OUT_F16) {
+      ((uint16_t*)out)[col] = f32_to_f16(s);
+    } else {
+      ((float*)out)[col] = s;
+    }
+  }
+}
+
+// out[col] = sum over p of partial[p][col]: 64 columns per workgroup, the
+// four waves take every fourth partial row, combined in LDS in fixed order.
 __global__ __launch_bounds__(256) void colsum_finish_kernel(const float* __restrict__ partial,
                                                             float* __restrict__ out, int64_t P,
                                                             int64_t N) {
-  const int64_t col = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (col >= N) return;
+  __shared__ float red[4][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t col = (int64_t)blockIdx.x * 64 + lane;
   float s = 0.0f;
-  for (int64_t p = 0; p < P; ++p) s += partial[p * N + col];
-  out[col] = s;
+  if (col < N) {
+    int64_t p = w;
+    for (; p + 12 < P; p += 16) {
+      const float a0 = partial[p * N + col], a1 = partial[(p + 4) * N + col];
+      const float a2 = partial[(p + 8) * N + col], a3 = partial[(p + 12) * N + col];
+      s += (a0 + a1) + (a2 + a3);
+    }
+    for (; p < P; p += 4) s += partial[p * N + col];
+  }
+  red[w][lane] = s;
+  __syncthreads();
+  if (w == 0 && col < N) out[col] = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
 }
 
 // RSUM axis attribute (reduce_sum/launcher.cu:75-85): default 0.
@@ -127,17 +204,24 @@ template <typename TI, bool BF16IN, bool OUT_F16>
 Status colsum_run(const void* x, void* out, float* partial, int64_t P, int64_t M, int64_t N,
                   void* stream, const char* what) {
   hipStream_t s = as_stream(stream);
-  const unsigned gx = (unsigned)((N + 63) / 64);
+  constexpr int VEC = 16 / sizeof(TI);
+  const bool vec = N % VEC == 0 && (uintptr_t)x % 16 == 0;
+  const unsigned gx = (unsigned)(vec ? (N + 64 * VEC - 1) / (64 * VEC) : (N + 63) / 64);
+  int64_t rpp = M, parts = 1;
   if (partial && P > 1 && M >= 2 * P) {
-    const int64_t rpp = (M + P - 1) / P;
-    const int64_t parts = (M + rpp - 1) / rpp;
+    rpp = (M + P - 1) / P;
+    parts = (M + rpp - 1) / rpp;
+  } else {
+    partial = nullptr;
+  }
+  if (vec)
+    colsum_vec_kernel<TI, BF16IN, OUT_F16><<<dim3(gx, (unsigned)parts), 256, 0, s>>>(
+        (const TI*)x, out, partial, M, N, rpp);
+  else
     colsum_kernel<TI, BF16IN, OUT_F16><<<dim3(gx, (unsigned)parts), 256, 0, s>>>(
         (const TI*)x, out, partial, M, N, rpp);
-    colsum_finish_kernel<<<(unsigned)((N + 255) / 256), 256, 0, s>>>(partial, (float*)out, parts, N);
-  } else {
-    colsum_kernel<TI, BF16IN, OUT_F16><<<dim3(gx, 1), 256, 0, s>>>((const TI*)x, out, nullptr, M, N,
-                                                                   M);
-  }
+  if (partial)
+    colsum_finish_kernel<<<(unsigned)((N + 63) / 64), 256, 0, s>>>(partial, (float*)out, parts, N);
   return launch_status(what);
 }
 

@@ -59,8 +59,10 @@ def time_launches(fn, iters: int, warmup: int, stream=None) -> float:
 
 
 # ------------------------------------------------------------------ GEMM
-def bench_gemm(C, M, N, K, act_kind=None, iters=20, warmup=5):
-    """bf16 X[M,K] . W[N,K]^T (+bias, act) -> bf16, fp32 accumulate."""
+def bench_gemm(C, M, N, K, act_kind=None, iters=20, warmup=5, save_preact=False):
+    """bf16 X[M,K] . W[N,K]^T (+bias, act) -> bf16, fp32 accumulate.  With
+    save_preact the bias+GELU epilogue also writes the pre-activation Z, as
+    the forward GEMMs of the train step do."""
     import torch
 
     g = torch.Generator(device="cuda")
@@ -74,8 +76,9 @@ def bench_gemm(C, M, N, K, act_kind=None, iters=20, warmup=5):
         fn = lambda: C.launch_by_id("gemm_bf16_mfma_v0", C.OpKind.Gemm, [X, W], [Y], 0,  # noqa: E731
                                     struct.pack("<ii", 0, 1))
     else:
+        outs = [Y, torch.empty_like(Y)] if save_preact else [Y]
         fn = lambda: C.launch_by_id("gemm_epilogue_bf16_mfma_v0", C.OpKind.GemmEpilogue,  # noqa: E731
-                                    [X, W, b], [Y], GEPI, struct.pack("<iii", 0, 1, act_kind))
+                                    [X, W, b], outs, GEPI, struct.pack("<iii", 0, 1, act_kind))
     ms = time_launches(fn, iters, warmup)
     return {"ms": ms, "tflops": 2.0 * M * N * K / (ms * 1e-3) / 1e12}
 
@@ -217,6 +220,88 @@ def cpu_baseline_mlp(B, D, L, sample_rows):
 
 
 # ------------------------------------------------------------------ main
+# ------------------------------------------------------------------ HBM traffic (rocprofv3 --pmc)
+TRAFFIC_FILE = REPO / "profiles" / "gemm_bias_gelu_8192x4096x4096_traffic.md"
+CALIB_ELEMS = 1 << 27          # calibration copy: 2^27 bf16 = 256 MiB read + 256 MiB written
+CALIB_KIB = CALIB_ELEMS * 2 / 1024
+
+
+def roofline_only(C, B, D, launches):
+    """The roofline kernel alone (launches x the step's bias+GELU GEMM with
+    saved pre-activation), then 3 calibration copies of known size; the
+    program profiled by the FETCH_SIZE / WRITE_SIZE passes."""
+    import torch
+
+    g = bench_gemm(C, B, D, D, act_kind=3, iters=launches, warmup=1, save_preact=True)
+    x = torch.ones(CALIB_ELEMS, device="cuda", dtype=torch.bfloat16)
+    y = torch.empty_like(x)
+    for _ in range(3):
+        C.launch_by_id("copy_bf16_v0", C.OpKind.Copy, [x], [y], 0, b"")
+    torch.cuda.synchronize()
+    log(f"[bench] roofline-only: {launches + 1} gemm launches, 3 calibration copies; {g}")
+
+
+def pmc_report(fetch_csv, write_csv):
+    """Markdown summary of two rocprofv3 --pmc runs of --roofline-only
+    (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch).  Each counter is scaled
+    by calibration copy's expected/measured ratio."""
+    import csv
+    from statistics import mean
+
+    def per_kernel(path, counter):
+        vals = {"gemm": [], "copy": []}
+        with open(path, newline="") as f:
+            for row in csv.DictReader(f):
+                if row.get("Counter_Name") != counter:
+                    continue
+                name = row.get("Kernel_Name", "")
+                key = "gemm" if "gemm_nt16" in name else "copy" if "map1" in name else None
+                if key:
+                    vals[key].append(float(row["Counter_Value"]))
+        return vals
+
+    fe, wr = per_kernel(fetch_csv, "FETCH_SIZE"), per_kernel(write_csv, "WRITE_SIZE")
+    f_r = CALIB_KIB / mean(fe["copy"])
+    f_w = CALIB_KIB / mean(wr["copy"])
+    fetch_b = mean(fe["gemm"]) * f_r * 1024
+    write_b = mean(wr["gemm"]) * f_w * 1024
+    lines = [
+        "# HBM traffic of the step's bias+GELU GEMM (8192x4096x4096, bf16, Z saved)",
+        "",
+        "Commands (GPU box, repo root):",
+        "```",
+        "rocprofv3 --pmc FETCH_SIZE --output-format csv -d gpurun_out/pmc_fetch -o run -- "
+        "python3 bench.py --roofline-only",
+        "rocprofv3 --pmc WRITE_SIZE --output-format csv -d gpurun_out/pmc_write -o run -- "
+        "python3 bench.py --roofline-only",
+        "python3 bench.py --pmc-report <fetch counter_collection.csv> <write counter_collection.csv>",
+        "```",
+        "",
+        f"calibration copy (copy_bf16_v0, {CALIB_KIB:.0f} KiB read + written): "
+        f"FETCH_SIZE {mean(fe['copy']):.0f} KiB -> factor {f_r:.4f}; "
+        f"WRITE_SIZE {mean(wr['copy']):.0f} KiB -> factor {f_w:.4f}",
+        f"gemm dispatches: {len(fe['gemm'])} (fetch run), {len(wr['gemm'])} (write run)",
+        f"gemm FETCH_SIZE {mean(fe['gemm']):.0f} KiB/dispatch -> {fetch_b / 1e6:.1f} MB",
+        f"gemm WRITE_SIZE {mean(wr['gemm']):.0f} KiB/dispatch -> {write_b / 1e6:.1f} MB",
+        "algorithmic bytes: X 64 MiB + W 32 MiB read, Y 64 MiB + Z 64 MiB written = 224 MiB",
+        "",
+        f"traffic_bytes_per_launch: {int(round(fetch_b + write_b))}",
+        "",
+    ]
+    print("\n".join(lines))
+
+
+def read_traffic():
+    """HBM bytes per launch of the roofline kernel from the committed PMC summary."""
+    try:
+        for line in TRAFFIC_FILE.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -228,7 +313,14 @@ def main():
     ap.add_argument("--no-components", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=8)
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="run only the roofline GEMM and a calibration copy (for rocprofv3 --pmc)")
+    ap.add_argument("--pmc-report", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="summarise two rocprofv3 --pmc CSVs of --roofline-only and exit")
     args = ap.parse_args()
+    if args.pmc_report:
+        pmc_report(*args.pmc_report)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); multi-GPU runs are not "
               f"part of this build", file=sys.stderr)
@@ -241,16 +333,21 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     B, D, L = args.batch, args.hidden, args.layers
     log(f"[bench] device={torch.cuda.get_device_name(0)} mlp B={B} D={D} L={L}")
+    if args.roofline_only:
+        roofline_only(C, B, D, 5)
+        return
 
     res = bench_mlp(B, D, L, args.steps, args.warmup)
     log(f"[bench] mlp {res}")
 
     # dominant kernel: forward GEMM of the step (bias + GELU epilogue)
-    g = bench_gemm(C, B, D, D, act_kind=3, iters=20, warmup=3)
+    g = bench_gemm(C, B, D, D, act_kind=3, iters=20, warmup=3, save_preact=True)
     flops = 2.0 * B * D * D
+    traffic = read_traffic() if (B, D) == (8192, 4096) else None
     roofline = {"bound": "mfma", "achieved": round(g["tflops"], 2), "peak": PEAK_BF16_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(g["tflops"] / PEAK_BF16_TFLOPS, 4),
-                "traffic": None, "kernel": "gemm_epilogue_bf16_mfma (bias+gelu)",
+                "traffic": traffic, "traffic_unit": "bytes/launch",
+                "kernel": "gemm_epilogue_bf16_mfma_v0 (bias+gelu, pre-activation saved)",
                 "shape": [B, D, D], "flops_per_launch": flops, "avg_ms": round(g["ms"], 4)}
     log(f"[bench] roofline gemm {g}")
 
