@@ -380,8 +380,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_kernel(GemmParams p) {
 //   * two LDS stages and one barrier per K-step, placed before the last
 //     sub-step so that no wave waits on LDS after it;
 //   * the MFMA fragments of sub-step s+1 are read from LDS while the MFMAs of
-//     sub-step s run (two register sets), interleaved one ds_read per few
-//     MFMAs with sched_group_barrier;
+//     sub-step s run (two register sets), one ds_read after each MFMA
+//     (sched_group_barrier);
 //   * MFMA operands swapped (A-operand = W rows, B-operand = X rows) so that
 //     each lane holds 4 consecutive output columns of one row;
 //   * the epilogue stages the output tile through LDS and stores whole rows;
@@ -656,13 +656,16 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt16_kernel(NTParams p) {
         acc[i][j] = mfma32<IN>(reinterpret_cast<const uint16_t*>(&fb[buf][i]),
                                reinterpret_cast<const uint16_t*>(&fa[buf][j]), acc[i][j]);
   };
-  // one ds_read per few MFMAs
+  // One ds_read after each MFMA, MFMA first: the lgkmcnt wait in front of a
+  // sub-step's first MFMA then covers only reads issued during the previous
+  // sub-step, never one issued just before it.
   auto interleave = [&]() {
 #pragma unroll
     for (int t = 0; t < TM + TN; ++t) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, (TM * TN) / (TM + TN), 0);
     }
+    if constexpr (TM * TN > TM + TN) __builtin_amdgcn_sched_group_barrier(0x008, TM * TN - (TM + TN), 0);
   };
 
   // Pipeline: a K-step has KS sub-steps; the fragments of sub-step s+1 are
