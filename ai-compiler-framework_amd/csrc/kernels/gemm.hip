@@ -372,9 +372,9 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_kernel(GemmParams p) {
 //     256x256 tile), each wave owns (BM/WM) x (BN/WN) = TM x TN blocks of
 //     32x32 fp32 accumulators;
 //   * global -> LDS with gfx950's direct 16-byte LDS loads
-//     (global_load_lds_dwordx4): lane i of a wave fills bytes [16i, 16i+16)
-//     of a 1 KB LDS block = 8 rows of 64 K-elements, so there is no VGPR
-//     staging and no ds_write; the XOR swizzle that keeps the fragment reads
+//     (buffer_load_dwordx4 ... lds): lane i of a wave fills bytes
+//     [16i, 16i+16) of a 1 KB LDS block = 8 rows of 64 K-elements, so there
+//     is no VGPR staging and no ds_write; the XOR swizzle that keeps the fragment reads
 //     bank-conflict free is applied by choosing which global chunk each lane
 //     fetches;
 //   * two LDS stages and one barrier per K-step, placed before the last
@@ -390,6 +390,27 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_kernel(GemmParams p) {
 // ---------------------------------------------------------------------------
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) void glb_void_t;
+
+// Buffer load straight into LDS (buffer_load_dwordx4 ... lds): lane i's 16
+// bytes land at M0 + 16 i.  The LLVM intrinsic has no clang builtin; it is
+// bound by name.  A buffer resource = 48-bit base, byte range (loads past it
+// return zero), gfx9 format word.  Per-lane 32-bit offsets stay fixed for the
+// whole K loop; the K advance is the scalar offset.
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+__device__ void raw_buffer_load_lds(i32x4_t rsrc, __attribute__((address_space(3))) unsigned* lds,
+                                    int size, int voffset, int soffset, int offset,
+                                    int aux) __asm("llvm.amdgcn.raw.buffer.load.lds");
+__device__ __forceinline__ i32x4_t buffer_rsrc(const void* base, uint32_t bytes) {
+  struct __attribute__((packed)) Rsrc {
+    const void* ptr;
+    uint32_t range;
+    uint32_t config;
+  } r{base, bytes, 0x00020000u};
+  i32x4_t v = __builtin_bit_cast(i32x4_t, r);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = __builtin_amdgcn_readfirstlane(v[i]);
+  return v;
+}
 
 struct NTParams {
   const uint16_t* A;  // [M, K], row stride lda
@@ -587,7 +608,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt16_kernel(NTParams p) {
   constexpr int TM = WTM / 32, TN = WTN / 32;
   constexpr int A_BYTES = BM * BK * 2, B_BYTES = BN * BK * 2;
   constexpr int STAGE = A_BYTES + B_BYTES;
-  static_assert((BM / 8 + BN / 8) % NW == 0, "load blocks must split evenly over waves");
+  static_assert((BM / 8) % NW == 0 && (BN / 8) % NW == 0, "load blocks must split evenly over waves");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE];
 
   int tm_i, tn_i;
@@ -606,22 +627,36 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt16_kernel(NTParams p) {
   const int r_in = lane >> 3;
   const int cl_even = (lane & 7) ^ (r_in >> 1);
   const int cl_odd = (lane & 7) ^ ((4 + (r_in >> 1)) & 7);
-  const uint16_t* a_row = p.A + (int64_t)(m0 + r_in) * p.lda;
-  const uint16_t* b_row = p.B + (int64_t)(n0 + r_in) * p.ldb;
+  // Loads go through buffer resources over this tile's rows of A and B (the
+  // host checks that BM * lda * 2 bytes fit a signed 32-bit offset).
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  const i32x4_t rsrc_a = buffer_rsrc(p.A + (int64_t)m0 * p.lda, (uint32_t)((int64_t)BM * p.lda * 2));
+  const i32x4_t rsrc_b = buffer_rsrc(p.B + (int64_t)n0 * p.ldb, (uint32_t)((int64_t)BN * p.ldb * 2));
+  constexpr int LA = BM / 8 / NW, LB = BN / 8 / NW;  // 1 KB blocks per wave and operand
+  int voff_a[LA], voff_b[LB];
+#pragma unroll
+  for (int t = 0; t < LA; ++t) {
+    const int j = wave + t * NW;
+    voff_a[t] = ((j * 8 + r_in) * (int)p.lda + ((j & 1) ? cl_odd : cl_even) * 8) * 2;
+  }
+#pragma unroll
+  for (int t = 0; t < LB; ++t) {
+    const int j = wave + t * NW;
+    voff_b[t] = ((j * 8 + r_in) * (int)p.ldb + ((j & 1) ? cl_odd : cl_even) * 8) * 2;
+  }
 
   auto issue_loads = [&](int kt, int stage) {
     uint8_t* base = smem + stage * STAGE;
-    const int64_t koff = (int64_t)kt * BK;
+    const int soff = kt * BK * 2;
 #pragma unroll
-    for (int j = wave; j < BM / 8; j += NW)
-      __builtin_amdgcn_global_load_lds(
-          (glb_void_t*)(a_row + (int64_t)j * 8 * p.lda + koff + ((j & 1) ? cl_odd : cl_even) * 8),
-          (lds_void_t*)(base + j * 1024), 16, 0, 0);
+    for (int t = 0; t < LA; ++t)
+      raw_buffer_load_lds(rsrc_a, (__attribute__((address_space(3))) unsigned*)(base + (wave_s + t * NW) * 1024),
+                          16, voff_a[t], soff, 0, 0);
 #pragma unroll
-    for (int j = wave; j < BN / 8; j += NW)
-      __builtin_amdgcn_global_load_lds(
-          (glb_void_t*)(b_row + (int64_t)j * 8 * p.ldb + koff + ((j & 1) ? cl_odd : cl_even) * 8),
-          (lds_void_t*)(base + A_BYTES + j * 1024), 16, 0, 0);
+    for (int t = 0; t < LB; ++t)
+      raw_buffer_load_lds(rsrc_b,
+                          (__attribute__((address_space(3))) unsigned*)(base + A_BYTES + (wave_s + t * NW) * 1024),
+                          16, voff_b[t], soff, 0, 0);
   };
 
   floatx16 acc[TN][TM];
@@ -843,6 +878,8 @@ bool nt_eligible(const GemmParams& p, int BM, int BN) {
   if (p.aux && (((uintptr_t)p.aux % 16) || (p.aux_rs * osz) % 16)) return false;
   if (p.bias && (p.bias_s != 1 || (uintptr_t)p.bias % 16)) return false;
   if (p.M > INT32_MAX / 2 || p.N > INT32_MAX / 2 || p.K > INT32_MAX / 2) return false;
+  // buffer-load offsets: a tile's rows of A / B must span < 2^31 bytes
+  if ((int64_t)BM * p.a_rs * 2 >= INT32_MAX || (int64_t)BN * p.b_cs * 2 >= INT32_MAX) return false;
   return true;
 }
 
