@@ -28,6 +28,8 @@
 //     MFMAs of tile k run, with one barrier per K step;
 //   * workgroup ids are remapped so that consecutive tiles of one XCD share
 //     A rows (grouped column-major raster per XCD).
+#include <utility>
+
 #include "../common/hip_util.hpp"
 
 namespace aicf::hip {
@@ -599,7 +601,84 @@ __device__ __forceinline__ void nt_epilogue_staged(const NTParams& p,
   }
 }
 
-template <int IN, int OUT, int ACT, int BM, int BN, int WM, int WN>
+// Scheduling pattern of one MFMA sub-step: NMF MFMAs, each followed by its
+// front-loaded share of the NDS LDS reads (sched_group_barrier masks: 0x008
+// MFMA, 0x100 DS read).
+template <int NMF, int NDS, int T>
+__device__ __forceinline__ void sched_interleave_step() {
+  constexpr int PER = (NDS + NMF - 1) / NMF;
+  constexpr int lo = T * PER < NDS ? T * PER : NDS;
+  constexpr int hi = (T + 1) * PER < NDS ? (T + 1) * PER : NDS;
+  __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+  if constexpr (hi > lo) __builtin_amdgcn_sched_group_barrier(0x100, hi - lo, 0);
+}
+template <int NMF, int NDS, int... T>
+__device__ __forceinline__ void sched_interleave(std::integer_sequence<int, T...>) {
+  (sched_interleave_step<NMF, NDS, T>(), ...);
+}
+
+// One operand of the NT kernel: BMN rows (the M or N dimension) x BK = 64
+// K-elements per stage.
+//   KC (K-contiguous, memory [MN][K] with row stride ld): 1 KB LDS blocks of
+//     8 MN-rows x 64 K (128 B per row); row r keeps logical 16-byte chunk c
+//     at physical chunk c ^ ((r >> 1) & 7), so the 32-row ds_read_b128
+//     fragment reads hit all 64 banks.  Slot `lane` of block j is row
+//     8j + lane/8, physical chunk lane%8.
+//   MN-contiguous (memory [K][MN] with row stride ld): 64 K-rows of BMN
+//     elements; row k keeps logical chunk c (8 MN-elements) at physical chunk
+//     c ^ (4 (k & 3)).  A fragment (32 MN x 16 K) is two ds_read_b64_tr_b16:
+//     in each 16-lane group lane j points at row k0 + j/4, elements
+//     m + 4 (j%4) .. +3, and the transposing read hands lane i the four K
+//     values of element m + i; the swizzle keeps the 4-row x 32-byte pattern
+//     of a group conflict-free.
+// Loads are buffer loads straight into LDS with per-lane offsets fixed for
+// the whole K loop (the K advance is the scalar offset); the host checks that
+// the bytes a resource spans fit a signed 32-bit offset.
+template <bool KC, int BMN, int NW>
+struct NTOperand {
+  static constexpr int BK = 64;
+  static constexpr int BYTES = BMN * BK * 2;
+  static constexpr int BLOCKS = BYTES / 1024 / NW;  // 1 KB load blocks per wave
+  static constexpr int ROWB = BMN * 2;               // MN-contiguous row bytes
+  static constexpr int CPR = ROWB / 16;              // chunks per MN-contiguous row
+  static_assert(BYTES % (1024 * NW) == 0, "load blocks must split evenly over waves");
+  static_assert(KC || CPR >= 16, "MN-contiguous tiles need >= 16 chunks per row");
+
+  i32x4_t rsrc;
+  int voff[BLOCKS];
+  int soff_step;  // scalar byte offset per K-step
+};
+
+template <bool KC, int BMN, int NW>
+__device__ __forceinline__ void nt_operand_init(NTOperand<KC, BMN, NW>& o, const uint16_t* X, int64_t ld,
+                                                int mn0, int K, int lane, int wave) {
+  if constexpr (KC) {
+    o.rsrc = buffer_rsrc(X + (int64_t)mn0 * ld, (uint32_t)((int64_t)BMN * ld * 2));
+    const int r_in = lane >> 3;
+    const int cl_even = (lane & 7) ^ (r_in >> 1);
+    const int cl_odd = (lane & 7) ^ ((4 + (r_in >> 1)) & 7);
+#pragma unroll
+    for (int t = 0; t < o.BLOCKS; ++t) {
+      const int j = wave + t * NW;
+      o.voff[t] = ((j * 8 + r_in) * (int)ld + ((j & 1) ? cl_odd : cl_even) * 8) * 2;
+    }
+    o.soff_step = 64 * 2;
+  } else {
+    constexpr int CPR = NTOperand<KC, BMN, NW>::CPR;
+    constexpr int RPB = 64 / CPR;  // rows per 1 KB block
+    o.rsrc = buffer_rsrc(X + mn0, (uint32_t)((int64_t)K * ld * 2));
+#pragma unroll
+    for (int t = 0; t < o.BLOCKS; ++t) {
+      const int q = wave + t * NW;
+      const int k = q * RPB + lane / CPR;
+      const int c = (lane % CPR) ^ (4 * (k & 3));
+      o.voff[t] = (k * (int)ld + c * 8) * 2;
+    }
+    o.soff_step = 64 * (int)ld * 2;
+  }
+}
+
+template <int IN, int OUT, int ACT, int BM, int BN, int WM, int WN, bool AKC, bool BKC>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_nt16_kernel(NTParams p) {
   constexpr int BK = 64;
   constexpr int KS = BK / 16;  // MFMA sub-steps per K-step
@@ -608,7 +687,6 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt16_kernel(NTParams p) {
   constexpr int TM = WTM / 32, TN = WTN / 32;
   constexpr int A_BYTES = BM * BK * 2, B_BYTES = BN * BK * 2;
   constexpr int STAGE = A_BYTES + B_BYTES;
-  static_assert((BM / 8) % NW == 0 && (BN / 8) % NW == 0, "load blocks must split evenly over waves");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE];
 
   int tm_i, tn_i;
@@ -616,47 +694,24 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt16_kernel(NTParams p) {
   const int m0 = tm_i * BM, n0 = tn_i * BN;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / WN, wn = wave % WN;
-
-  // LDS layout of a stage: 1 KB blocks of 8 rows x 64 K-elements (128 B per
-  // row = 8 chunks of 16 B); row r stores logical chunk c at physical chunk
-  // c ^ ((r >> 1) & 7).  Any 16 consecutive rows of one logical chunk then
-  // cover all 64 banks, so the fragment reads (ds_read_b128, 32 rows) are
-  // conflict-free.  Slot `lane` of block j is row 8j + lane/8, physical chunk
-  // lane%8; the loader picks the matching global chunk, which depends on the
-  // parity of j.
-  const int r_in = lane >> 3;
-  const int cl_even = (lane & 7) ^ (r_in >> 1);
-  const int cl_odd = (lane & 7) ^ ((4 + (r_in >> 1)) & 7);
-  // Loads go through buffer resources over this tile's rows of A and B (the
-  // host checks that BM * lda * 2 bytes fit a signed 32-bit offset).
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
-  const i32x4_t rsrc_a = buffer_rsrc(p.A + (int64_t)m0 * p.lda, (uint32_t)((int64_t)BM * p.lda * 2));
-  const i32x4_t rsrc_b = buffer_rsrc(p.B + (int64_t)n0 * p.ldb, (uint32_t)((int64_t)BN * p.ldb * 2));
-  constexpr int LA = BM / 8 / NW, LB = BN / 8 / NW;  // 1 KB blocks per wave and operand
-  int voff_a[LA], voff_b[LB];
-#pragma unroll
-  for (int t = 0; t < LA; ++t) {
-    const int j = wave + t * NW;
-    voff_a[t] = ((j * 8 + r_in) * (int)p.lda + ((j & 1) ? cl_odd : cl_even) * 8) * 2;
-  }
-#pragma unroll
-  for (int t = 0; t < LB; ++t) {
-    const int j = wave + t * NW;
-    voff_b[t] = ((j * 8 + r_in) * (int)p.ldb + ((j & 1) ? cl_odd : cl_even) * 8) * 2;
-  }
+
+  NTOperand<AKC, BM, NW> opa;
+  NTOperand<BKC, BN, NW> opb;
+  nt_operand_init(opa, p.A, p.lda, m0, p.K, lane, wave);
+  nt_operand_init(opb, p.B, p.ldb, n0, p.K, lane, wave);
 
   auto issue_loads = [&](int kt, int stage) {
     uint8_t* base = smem + stage * STAGE;
-    const int soff = kt * BK * 2;
 #pragma unroll
-    for (int t = 0; t < LA; ++t)
-      raw_buffer_load_lds(rsrc_a, (__attribute__((address_space(3))) unsigned*)(base + (wave_s + t * NW) * 1024),
-                          16, voff_a[t], soff, 0, 0);
+    for (int t = 0; t < opa.BLOCKS; ++t)
+      raw_buffer_load_lds(opa.rsrc, (__attribute__((address_space(3))) unsigned*)(base + (wave_s + t * NW) * 1024),
+                          16, opa.voff[t], kt * opa.soff_step, 0, 0);
 #pragma unroll
-    for (int t = 0; t < LB; ++t)
-      raw_buffer_load_lds(rsrc_b,
+    for (int t = 0; t < opb.BLOCKS; ++t)
+      raw_buffer_load_lds(opb.rsrc,
                           (__attribute__((address_space(3))) unsigned*)(base + A_BYTES + (wave_s + t * NW) * 1024),
-                          16, voff_b[t], soff, 0, 0);
+                          16, opb.voff[t], kt * opb.soff_step, 0, 0);
   };
 
   floatx16 acc[TN][TM];
@@ -667,21 +722,54 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt16_kernel(NTParams p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
+  // Fragment addresses.  K-contiguous: row offset of the lane's MN-row plus
+  // the swizzled chunk of (sub-step, half).  MN-contiguous: the lane's K-row
+  // within a sub-step and its swizzled column bytes (loop invariant).
   const int fr = lane & 31, fh = lane >> 5;
+  const int rsw = (fr >> 1) & 7;  // fragment rows start at multiples of 32
+  const int g16 = (lane >> 4) & 3, i16 = lane & 15;
+  const int tr_row = (8 * (g16 >> 1) + (i16 >> 2));
+  auto tr_col = [&](int mb) {  // byte offset of the lane's 8-byte piece in a K-row
+    return ((((mb >> 3) ^ (4 * ((i16 >> 2) & 3))) + 2 * (g16 & 1) + ((i16 >> 1) & 1)) * 16) + 8 * (i16 & 1);
+  };
   int a_off[TM], b_off[TN];
 #pragma unroll
-  for (int j = 0; j < TM; ++j) a_off[j] = (wm * WTM + j * 32 + fr) * 128;
+  for (int j = 0; j < TM; ++j) {
+    const int mb = wm * WTM + j * 32;
+    a_off[j] = AKC ? (mb + fr) * 128 : tr_row * (BM * 2) + tr_col(mb);
+  }
 #pragma unroll
-  for (int i = 0; i < TN; ++i) b_off[i] = A_BYTES + (wn * WTN + i * 32 + fr) * 128;
-  const int rsw = (fr >> 1) & 7;  // fragment rows start at multiples of 32
+  for (int i = 0; i < TN; ++i) {
+    const int nb = wn * WTN + i * 32;
+    b_off[i] = A_BYTES + (BKC ? (nb + fr) * 128 : tr_row * (BN * 2) + tr_col(nb));
+  }
+
+  typedef short v4i16 __attribute__((ext_vector_type(4)));
+  auto tr_frag = [&](const uint8_t* addr, int rowb) -> u16x8 {
+    const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)addr);
+    const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)(addr + 4 * rowb));
+    u16x8 f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      f[e] = (uint16_t)lo[e];
+      f[e + 4] = (uint16_t)hi[e];
+    }
+    return f;
+  };
 
   u16x8 fa[2][TM], fb[2][TN];
   auto read_frags = [&](const uint8_t* st, int kk, int buf) {
     const int chunk = ((kk * 2 + fh) ^ rsw) * 16;
 #pragma unroll
-    for (int j = 0; j < TM; ++j) fa[buf][j] = *reinterpret_cast<const u16x8*>(st + a_off[j] + chunk);
+    for (int j = 0; j < TM; ++j) {
+      if constexpr (AKC) fa[buf][j] = *reinterpret_cast<const u16x8*>(st + a_off[j] + chunk);
+      else fa[buf][j] = tr_frag(st + a_off[j] + kk * 16 * (BM * 2), BM * 2);
+    }
 #pragma unroll
-    for (int i = 0; i < TN; ++i) fb[buf][i] = *reinterpret_cast<const u16x8*>(st + b_off[i] + chunk);
+    for (int i = 0; i < TN; ++i) {
+      if constexpr (BKC) fb[buf][i] = *reinterpret_cast<const u16x8*>(st + b_off[i] + chunk);
+      else fb[buf][i] = tr_frag(st + b_off[i] + kk * 16 * (BN * 2), BN * 2);
+    }
   };
   auto mfmas = [&](int buf) {
 #pragma unroll
@@ -694,14 +782,12 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt16_kernel(NTParams p) {
   // One ds_read after each MFMA, MFMA first: the lgkmcnt wait in front of a
   // sub-step's first MFMA then covers only reads issued during the previous
   // sub-step, never one issued just before it.
-  auto interleave = [&]() {
-#pragma unroll
-    for (int t = 0; t < TM + TN; ++t) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    }
-    if constexpr (TM * TN > TM + TN) __builtin_amdgcn_sched_group_barrier(0x008, TM * TN - (TM + TN), 0);
-  };
+  // ds reads per sub-step, spread over its MFMAs front-loaded (MFMA t is
+  // followed by its ceil-share of reads), so the last reads still have
+  // several MFMAs to land before the next sub-step needs them.
+  constexpr int NDS = (AKC ? TM : 2 * TM) + (BKC ? TN : 2 * TN);
+  constexpr int NMF = TM * TN;
+  auto interleave = [&]() { sched_interleave<NMF, NDS>(std::make_integer_sequence<int, NMF>{}); };
 
   // Pipeline: a K-step has KS sub-steps; the fragments of sub-step s+1 are
   // read while the MFMAs of sub-step s run.  The only barrier of a K-step
@@ -830,7 +916,7 @@ Status run_cfg(GemmParams& p, hipStream_t s) {
   return launch_status("gemm_mfma");
 }
 
-template <int IN, int OUT, int ACT, int BM, int BN, int WM, int WN>
+template <int IN, int OUT, int ACT, int BM, int BN, int WM, int WN, bool AKC, bool BKC>
 Status run_nt_act(const GemmParams& g, hipStream_t s) {
   NTParams p{};
   p.A = (const uint16_t*)g.A;
@@ -838,8 +924,8 @@ Status run_nt_act(const GemmParams& g, hipStream_t s) {
   p.C = g.C;
   p.bias = g.bias;
   p.aux = g.aux;
-  p.lda = g.a_rs;
-  p.ldb = g.b_cs;
+  p.lda = AKC ? g.a_rs : g.a_cs;  // memory row stride of A ([M][K] or [K][M])
+  p.ldb = BKC ? g.b_cs : g.b_rs;  // memory row stride of B ([N][K] or [K][N])
   p.ldc = g.c_rs;
   p.aux_ld = g.aux_rs;
   p.M = (int)g.M;
@@ -848,38 +934,58 @@ Status run_nt_act(const GemmParams& g, hipStream_t s) {
   p.bias_f32 = g.bias_f32;
   p.tiles_m = p.M / BM;
   p.tiles_n = p.N / BN;
-  gemm_nt16_kernel<IN, OUT, ACT, BM, BN, WM, WN>
+  gemm_nt16_kernel<IN, OUT, ACT, BM, BN, WM, WN, AKC, BKC>
       <<<(unsigned)(p.tiles_m * p.tiles_n), 64 * WM * WN, 0, s>>>(p);
   return launch_status("gemm_nt16");
 }
 
-template <int IN, int OUT, int BM, int BN, int WM, int WN>
-Status run_nt(const GemmParams& g, hipStream_t s) {
+template <int IN, int OUT, int BM, int BN, int WM, int WN, bool AKC, bool BKC>
+Status run_nt_layout(const GemmParams& g, hipStream_t s) {
   switch (g.act) {
-    case ACT_RELU: return run_nt_act<IN, OUT, ACT_RELU, BM, BN, WM, WN>(g, s);
-    case ACT_GELU: return run_nt_act<IN, OUT, ACT_GELU, BM, BN, WM, WN>(g, s);
-    case ACT_DGELU: return run_nt_act<IN, OUT, ACT_DGELU, BM, BN, WM, WN>(g, s);
-    default: return run_nt_act<IN, OUT, ACT_NONE, BM, BN, WM, WN>(g, s);
+    case ACT_RELU: return run_nt_act<IN, OUT, ACT_RELU, BM, BN, WM, WN, AKC, BKC>(g, s);
+    case ACT_GELU: return run_nt_act<IN, OUT, ACT_GELU, BM, BN, WM, WN, AKC, BKC>(g, s);
+    case ACT_DGELU: return run_nt_act<IN, OUT, ACT_DGELU, BM, BN, WM, WN, AKC, BKC>(g, s);
+    default: return run_nt_act<IN, OUT, ACT_NONE, BM, BN, WM, WN, AKC, BKC>(g, s);
   }
 }
 
-// The NT fast path applies when both operands are K-contiguous 16-bit
-// matrices with 16-byte aligned rows, C (and the aux matrix) have unit column
-// stride with 16-byte aligned rows, bias is contiguous, and the shape tiles
-// exactly.
+// Operand layouts: K-contiguous ([MN][K]) on every tile configuration;
+// MN-contiguous ([K][MN], read through the transposing LDS loads) on the
+// 256 x 256 configuration (MN_OK).
+template <int IN, int OUT, int BM, int BN, int WM, int WN, bool MN_OK>
+Status run_nt(const GemmParams& g, hipStream_t s) {
+  const bool akc = g.a_mode == LD_KCONTIG, bkc = g.b_mode == LD_KCONTIG;
+  if (akc && bkc) return run_nt_layout<IN, OUT, BM, BN, WM, WN, true, true>(g, s);
+  if constexpr (MN_OK) {
+    if (akc) return run_nt_layout<IN, OUT, BM, BN, WM, WN, true, false>(g, s);
+    if (bkc) return run_nt_layout<IN, OUT, BM, BN, WM, WN, false, true>(g, s);
+    return run_nt_layout<IN, OUT, BM, BN, WM, WN, false, false>(g, s);
+  }
+  return Status::Internal;  // excluded by nt_eligible
+}
+
+// The NT fast path applies to 16-bit operands that are each K-contiguous
+// ([MN][K]) or, on the 256 x 256 tiles, MN-contiguous ([K][MN]), with 16-byte
+// aligned bases and rows; C (and the aux matrix) have unit column stride with
+// 16-byte aligned rows, bias is contiguous, and the shape tiles exactly.
 template <int IN, int OUT>
-bool nt_eligible(const GemmParams& p, int BM, int BN) {
+bool nt_eligible(const GemmParams& p, int BM, int BN, bool mn_ok) {
   if (IN == IN_F32) return false;
-  if (p.a_mode != LD_KCONTIG || p.b_mode != LD_KCONTIG) return false;
+  auto operand_ok = [&](int mode, int64_t ld_k, int64_t ld_mn, int64_t rows_mn) {
+    if (mode == LD_KCONTIG) return (ld_k * 2) % 16 == 0 && rows_mn * ld_k * 2 < INT32_MAX;
+    if (mode == LD_MNCONTIG && mn_ok) return (ld_mn * 2) % 16 == 0 && p.K * ld_mn * 2 < INT32_MAX;
+    return false;
+  };
+  // A view [M, K]: K-contiguous row stride a_rs, MN-contiguous row stride a_cs.
+  // B view [K, N]: K-contiguous row stride b_cs, MN-contiguous row stride b_rs.
+  if (!operand_ok(p.a_mode, p.a_rs, p.a_cs, BM) || !operand_ok(p.b_mode, p.b_cs, p.b_rs, BN)) return false;
   if (p.M % BM || p.N % BN || p.K % 64) return false;
-  if ((uintptr_t)p.A % 16 || (uintptr_t)p.B % 16 || (p.a_rs * 2) % 16 || (p.b_cs * 2) % 16) return false;
+  if ((uintptr_t)p.A % 16 || (uintptr_t)p.B % 16) return false;
   const int osz = OUT == OUT_F32 ? 4 : 2;
   if (p.c_cs != 1 || (uintptr_t)p.C % 16 || (p.c_rs * osz) % 16) return false;
   if (p.aux && (((uintptr_t)p.aux % 16) || (p.aux_rs * osz) % 16)) return false;
   if (p.bias && (p.bias_s != 1 || (uintptr_t)p.bias % 16)) return false;
   if (p.M > INT32_MAX / 2 || p.N > INT32_MAX / 2 || p.K > INT32_MAX / 2) return false;
-  // buffer-load offsets: a tile's rows of A / B must span < 2^31 bytes
-  if ((int64_t)BM * p.a_rs * 2 >= INT32_MAX || (int64_t)BN * p.b_cs * 2 >= INT32_MAX) return false;
   return true;
 }
 
@@ -887,8 +993,9 @@ template <int IN, int OUT>
 Status run_gemm(GemmParams& p, hipStream_t s) {
   if constexpr (IN != IN_F32) {
     const int64_t tiles256 = (p.M / 256) * (p.N / 256);
-    if (tiles256 >= 128 && nt_eligible<IN, OUT>(p, 256, 256)) return run_nt<IN, OUT, 256, 256, 2, 4>(p, s);
-    if (nt_eligible<IN, OUT>(p, 128, 128)) return run_nt<IN, OUT, 128, 128, 2, 2>(p, s);
+    if (tiles256 >= 128 && nt_eligible<IN, OUT>(p, 256, 256, true))
+      return run_nt<IN, OUT, 256, 256, 2, 4, true>(p, s);
+    if (nt_eligible<IN, OUT>(p, 128, 128, false)) return run_nt<IN, OUT, 128, 128, 2, 2, false>(p, s);
   }
   // Large problems: 128x128 workgroup tiles (4 waves, 64x64 per wave).
   // Smaller ones: 64x64 tiles so that enough workgroups exist.

@@ -166,13 +166,28 @@ def _writes(it: Dict[str, Any], vid: int) -> bool:
     return vid in it.get("outputs", [])
 
 
-def normalize_gemm_layout(ir: IRGraph, lowered: Lowered, *, min_flops: float = 2.0 ** 30) -> Lowered:
+# Cost model of StageD's "cost" policy (MI355X measurements): a 2-D
+# transpose streams its bytes twice at ~5.5 TB/s; reading an M/N-contiguous
+# operand in place (transposing LDS loads) costs the GEMM ~10% more than the
+# K-contiguous form, at ~1.2 PFLOP/s.
+TRANSPOSE_BYTES_PER_S = 5.5e12
+GEMM_FLOPS_PER_S = 1.2e15
+MN_OPERAND_PENALTY = 0.10
+
+
+def normalize_gemm_layout(ir: IRGraph, lowered: Lowered, *, min_flops: float = 2.0 ** 30,
+                          policy: str = "all") -> Lowered:
     """StageD (not in the reference): rewrite 16-bit GEMMs whose operands are
     M/N-contiguous (transA=True on A, transB=False on B) into explicit 2-D
-    transposes plus the K-contiguous "NT" form (transA=False, transB=True)
-    that the fast MFMA kernel takes.  The transposed copies become new IR
-    values; a copy is reused while its source is not written in between.
-    Small GEMMs (< min_flops) are left to the general kernel."""
+    transposes plus the K-contiguous form (transA=False, transB=True).  The
+    GEMM kernel also reads M/N-contiguous operands in place, somewhat slower,
+    so the policy decides per operand: "all" transposes every such operand,
+    "cost" only those whose transpose is cheaper than the in-place penalty
+    (TRANSPOSE_BYTES_PER_S, GEMM_FLOPS_PER_S, MN_OPERAND_PENALTY).  The
+    transposed copies become new IR values; a copy is reused while its source
+    is not written in between.  Small GEMMs (< min_flops) are left alone."""
+    if policy not in ("all", "cost"):
+        raise ValueError(f"normalize_gemm_layout: unknown policy {policy!r}")
     out: Lowered = []
     cache: Dict[int, int] = {}  # source vid -> transposed vid (valid until the source is written)
     kind = lambda it: str(it.get("op", "")).strip().lower()  # noqa: E731
@@ -187,6 +202,12 @@ def normalize_gemm_layout(ir: IRGraph, lowered: Lowered, *, min_flops: float = 2
         cache[src] = tv.id
         return tv.id
 
+    def pays(vid: int, flops: float) -> bool:
+        if policy == "all" or vid in cache:
+            return True
+        nbytes = 2.0 * _numel(ir, vid)
+        return 2.0 * nbytes / TRANSPOSE_BYTES_PER_S < MN_OPERAND_PENALTY * flops / GEMM_FLOPS_PER_S
+
     for it in lowered:
         op = kind(it)
         if op in ("gemm", "gemm_epilogue"):
@@ -198,17 +219,21 @@ def normalize_gemm_layout(ir: IRGraph, lowered: Lowered, *, min_flops: float = 2
             M = sa[1] if ta else sa[0]
             K = sa[0] if ta else sa[1]
             N = sb[0] if tb else sb[1]
-            big = 2.0 * M * N * K >= min_flops
-            if ("float16" in dts or "bfloat16" in dts) and big and (ta or not tb):
-                it = dict(it)
-                ins = list(it["inputs"])
-                if ta:
-                    ins[0] = transposed(a)
-                if not tb:
-                    ins[1] = transposed(b)
-                attrs["transA"], attrs["transB"] = False, True
-                it["inputs"], it["attrs"] = ins, attrs
-                it.pop("kernel_id", None)
+            flops = 2.0 * M * N * K
+            if ("float16" in dts or "bfloat16" in dts) and flops >= min_flops and (ta or not tb):
+                do_a = ta and pays(a, flops)
+                do_b = (not tb) and pays(b, flops)
+                if do_a or do_b:
+                    it = dict(it)
+                    ins = list(it["inputs"])
+                    if do_a:
+                        ins[0] = transposed(a)
+                        attrs["transA"] = False
+                    if do_b:
+                        ins[1] = transposed(b)
+                        attrs["transB"] = True
+                    it["inputs"], it["attrs"] = ins, attrs
+                    it.pop("kernel_id", None)
         for o in it.get("outputs", []):
             for src in [s for s in cache if s == int(o)]:
                 del cache[src]
@@ -327,13 +352,16 @@ def apply_kernel_selection(ir: IRGraph, lowered: Lowered) -> Lowered:
 
 
 def compile_lowered(ir: IRGraph, *, fuse: bool = True, fuse_bias: bool = False,
-                    nt_layout: bool = False, nt_min_flops: float = 2.0 ** 30) -> Lowered:
-    """StageA -> StageC -> (StageD) -> StageB."""
+                    nt_layout: Any = False, nt_min_flops: float = 2.0 ** 30) -> Lowered:
+    """StageA -> StageC -> (StageD) -> StageB.  nt_layout: False (no StageD),
+    True / "all" (transpose every M/N-contiguous 16-bit operand) or "cost"
+    (transpose only where that is cheaper than reading it in place)."""
     low = lower_to_backend_ops(ir)
     if fuse:
         low = fuse_gemm_epilogue(ir, low, fuse_bias=fuse_bias)
     if nt_layout:
-        low = normalize_gemm_layout(ir, low, min_flops=nt_min_flops)
+        policy = "all" if nt_layout is True else str(nt_layout)
+        low = normalize_gemm_layout(ir, low, min_flops=nt_min_flops, policy=policy)
     return apply_kernel_selection(ir, low)
 
 

@@ -108,7 +108,7 @@ def test_stage_d_rewrites_backward_gemms_to_nt():
     K-contiguous form and reuses a transposed copy until its source changes."""
     from aicf_hip import mlp
 
-    ir, lowered, _ = mlp.build_mlp_mse(8192, 4096, 4)
+    ir, lowered, _ = mlp.build_mlp_mse(8192, 4096, 4, nt_layout=True)
     gemms = [it for it in lowered if it["op"] in ("gemm", "gemm_epilogue")]
     assert len(gemms) == 12
     for it in gemms:
@@ -124,3 +124,39 @@ def test_stage_d_rewrites_backward_gemms_to_nt():
             if ir.values[v].name.endswith("^T"):
                 assert v in made
         made.update(it["outputs"])
+
+
+def test_mlp_graph_without_stage_d_reads_operands_in_place():
+    """Without StageD the backward GEMMs keep their stored layouts: forward
+    X . W^T (K-contiguous both), dX = dZ . W (W M/N-contiguous), dW = dZ^T . H
+    (both M/N-contiguous); no transposes are emitted."""
+    from aicf_hip import mlp
+
+    ir, lowered, _ = mlp.build_mlp_mse(8192, 4096, 4, nt_layout=False)
+    assert not [it for it in lowered if it["op"] == "transpose"]
+    layouts = {}
+    for it in lowered:
+        if it["op"] in ("gemm", "gemm_epilogue"):
+            a = it["attrs"]
+            key = (bool(a.get("transA", False)), bool(a.get("transB", False)))
+            layouts[key] = layouts.get(key, 0) + 1
+    # 4 forward, 4 dX (the first layer's dX too, as the reference computes it), 4 dW
+    assert layouts == {(False, True): 4, (False, False): 4, (True, False): 4}
+
+
+def test_stage_d_cost_policy_transposes_only_the_weights():
+    """StageD "cost" at the benchmark shape: transposing a 4096^2 weight (32 MB)
+    is cheaper than the in-place penalty of its dX GEMM; transposing dZ or H
+    (64 MB each) is not, so the dW GEMMs read them in place."""
+    from aicf_hip import mlp
+
+    ir, lowered, _ = mlp.build_mlp_mse(8192, 4096, 4, nt_layout="cost")
+    tr = [it for it in lowered if it["op"] == "transpose"]
+    assert sorted(ir.values[it["inputs"][0]].name for it in tr) == [f"wb.{i}.W" for i in range(1, 5)]
+    layouts = {}
+    for it in lowered:
+        if it["op"] in ("gemm", "gemm_epilogue"):
+            a = it["attrs"]
+            key = (bool(a.get("transA", False)), bool(a.get("transB", False)))
+            layouts[key] = layouts.get(key, 0) + 1
+    assert layouts == {(False, True): 8, (True, False): 4}

@@ -433,6 +433,46 @@ def test_gemm_bf16(C, M, N, K, ta, tb):
     assert orc.rel_err(h(of), ref) < 1e-5  # fp32 out: only accumulation-order error
 
 
+@pytest.mark.parametrize("K", [64, 192])
+@pytest.mark.parametrize("ta,tb", [(False, True), (False, False), (True, True), (True, False)])
+def test_gemm_bf16_256_tiles_all_operand_layouts(C, ta, tb, K):
+    """256x256-tile path with each operand K-contiguous or MN-contiguous
+    (the latter read through the transposing LDS loads)."""
+    M = N = 4096
+    r = rng(K + 2 * ta + tb)
+    s = 1.0 / np.sqrt(K)
+    A = r.uniform(-1, 1, (K, M) if ta else (M, K)).astype(np.float32)
+    B = r.uniform(-s, s, (N, K) if tb else (K, N)).astype(np.float32)
+    Ab, Bb = orc.bf16_bits_from_f32(A), orc.bf16_bits_from_f32(B)
+    ref = _gemm_ref(orc.bf16_bits_to_f32(Ab).reshape(A.shape), orc.bf16_bits_to_f32(Bb).reshape(B.shape), ta, tb)
+    of = torch.empty((M, N), device="cuda")
+    C.launch_by_id("gemm_bf16_mfma_f32out_v0", C.OpKind.Gemm,
+                   [g(Ab, torch.bfloat16), g(Bb, torch.bfloat16)], [of], 0, struct.pack("<ii", ta, tb))
+    assert orc.rel_err(h(of), ref) < 1e-5
+    o = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    C.op_call(int(C.OpKind.Gemm), [g(Ab, torch.bfloat16), g(Bb, torch.bfloat16)], [o], 0,
+              struct.pack("<ii", ta, tb), 0)
+    assert orc.rel_err(orc.bf16_bits_to_f32(h(o)), ref) < 1e-2
+
+
+def test_gemm_bf16_dgelu_with_mn_contiguous_weight_256_tiles(C):
+    """dX = (dY . W) * gelu'(Z) with W stored [out, in] (MN-contiguous B), on
+    the 256x256-tile path: the backward GEMM of a Linear layer without a
+    transposed copy of W."""
+    M, N, K = 8192, 1024, 128  # dY [M, K], W [K, N] row-major, Z [M, N]
+    r = rng(77)
+    dY = orc.bf16_bits_from_f32(r.standard_normal((M, K)).astype(np.float32))
+    W = orc.bf16_bits_from_f32(r.uniform(-0.1, 0.1, (K, N)).astype(np.float32))
+    Z = orc.bf16_bits_from_f32(r.standard_normal((M, N)).astype(np.float32))
+    dz = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    C.launch_by_id("gemm_epilogue_bf16_mfma_v0", C.OpKind.GemmEpilogue,
+                   [g(dY, torch.bfloat16), g(W, torch.bfloat16), g(Z, torch.bfloat16)], [dz], GEPI,
+                   struct.pack("<iii", 0, 0, 5))
+    ref = _gemm_ref(orc.bf16_bits_to_f32(dY).reshape(M, K), orc.bf16_bits_to_f32(W).reshape(K, N),
+                    False, False) * orc.gelu_grad_f64(orc.bf16_bits_to_f32(Z).reshape(M, N).astype(np.float64))
+    assert orc.rel_err(orc.bf16_bits_to_f32(h(dz)).reshape(M, N), ref) < 1e-2
+
+
 @pytest.mark.parametrize("relu", [1, 0])
 @pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, True)])
 def test_gemm_epilogue_f32_gpel(C, relu, ta, tb):
