@@ -228,7 +228,7 @@ __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int& tm, i
     const int per = total >> 3;
     id = (id & 7) * per + (id >> 3);
   }
-  constexpr int GROUP_M = 8;
+  constexpr int GROUP_M = 4;  // measured best on MI355X for 256x256 tiles
   const int group = id / (GROUP_M * tiles_n);
   const int first_m = group * GROUP_M;
   const int gsize = (tiles_m - first_m) < GROUP_M ? (tiles_m - first_m) : GROUP_M;
