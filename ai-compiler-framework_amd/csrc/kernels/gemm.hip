@@ -368,21 +368,22 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_kernel(GemmParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Fast path for 16-bit inputs with both operands K-contiguous (X[M,K] and
-// W[N,K] row-major, the Linear layout) and tile-divisible shapes.
-//   * BM x BN x 64 workgroup tiles; WM x WN waves (two per SIMD for the
-//     256x256 tile), each wave owns (BM/WM) x (BN/WN) = TM x TN blocks of
-//     32x32 fp32 accumulators;
+// Tiled MFMA path for tile-divisible shapes: 16-bit operands (each
+// K-contiguous or M/N-contiguous) and fp32 operands (K-contiguous).
+//   * BM x BN workgroup tiles; a stage holds 128 bytes of K per row (64
+//     16-bit or 32 fp32 elements); WM x WN waves (two per SIMD for the
+//     256x256 tile), each owning (BM/WM) x (BN/WN) = TM x TN blocks of 32x32
+//     fp32 accumulators (v_mfma_f32_32x32x16_bf16/f16, or 4 x
+//     v_mfma_f32_32x32x2f32 per 16-byte fp32 fragment);
 //   * global -> LDS with gfx950's direct 16-byte LDS loads
 //     (buffer_load_dwordx4 ... lds): lane i of a wave fills bytes
-//     [16i, 16i+16) of a 1 KB LDS block = 8 rows of 64 K-elements, so there
-//     is no VGPR staging and no ds_write; the XOR swizzle that keeps the fragment reads
-//     bank-conflict free is applied by choosing which global chunk each lane
-//     fetches;
+//     [16i, 16i+16) of a 1 KB LDS block, so there is no VGPR staging and no
+//     ds_write; the XOR swizzle that keeps the fragment reads bank-conflict
+//     free is applied by choosing which global chunk each lane fetches;
 //   * two LDS stages and one barrier per K-step, placed before the last
 //     sub-step so that no wave waits on LDS after it;
 //   * the MFMA fragments of sub-step s+1 are read from LDS while the MFMAs of
-//     sub-step s run (two register sets), one ds_read after each MFMA
+//     sub-step s run (two register sets), spread over the MFMAs
 //     (sched_group_barrier);
 //   * MFMA operands swapped (A-operand = W rows, B-operand = X rows) so that
 //     each lane holds 4 consecutive output columns of one row;
@@ -415,8 +416,8 @@ __device__ __forceinline__ i32x4_t buffer_rsrc(const void* base, uint32_t bytes)
 }
 
 struct NTParams {
-  const uint16_t* A;  // [M, K], row stride lda
-  const uint16_t* B;  // [N, K], row stride ldb
+  const void* A;      // K-contiguous [M, K] or M-contiguous [K, M], row stride lda (elements)
+  const void* B;      // K-contiguous [N, K] or N-contiguous [K, N], row stride ldb (elements)
   void* C;            // [M, N], row stride ldc
   const void* bias;
   void* aux;
@@ -634,39 +635,39 @@ __device__ __forceinline__ void sched_interleave(std::integer_sequence<int, T...
 // Loads are buffer loads straight into LDS with per-lane offsets fixed for
 // the whole K loop (the K advance is the scalar offset); the host checks that
 // the bytes a resource spans fit a signed 32-bit offset.
-template <bool KC, int BMN, int NW>
+template <bool KC, int BMN, int NW, int ES>
 struct NTOperand {
-  static constexpr int BK = 64;
-  static constexpr int BYTES = BMN * BK * 2;
-  static constexpr int BLOCKS = BYTES / 1024 / NW;  // 1 KB load blocks per wave
-  static constexpr int ROWB = BMN * 2;               // MN-contiguous row bytes
+  static constexpr int BYTES = BMN * 128;            // a stage holds 128 B of K per row
+  static constexpr int BLOCKS = BYTES / 1024 / NW;   // 1 KB load blocks per wave
+  static constexpr int ROWB = BMN * ES;              // MN-contiguous row bytes
   static constexpr int CPR = ROWB / 16;              // chunks per MN-contiguous row
   static_assert(BYTES % (1024 * NW) == 0, "load blocks must split evenly over waves");
-  static_assert(KC || CPR >= 16, "MN-contiguous tiles need >= 16 chunks per row");
+  static_assert(KC || (ES == 2 && CPR >= 16), "MN-contiguous tiles: 16-bit, >= 16 chunks per row");
 
   i32x4_t rsrc;
   int voff[BLOCKS];
   int soff_step;  // scalar byte offset per K-step
 };
 
-template <bool KC, int BMN, int NW>
-__device__ __forceinline__ void nt_operand_init(NTOperand<KC, BMN, NW>& o, const uint16_t* X, int64_t ld,
+template <bool KC, int BMN, int NW, int ES>
+__device__ __forceinline__ void nt_operand_init(NTOperand<KC, BMN, NW, ES>& o, const void* X, int64_t ld,
                                                 int mn0, int K, int lane, int wave) {
+  const uint8_t* Xb = static_cast<const uint8_t*>(X);
   if constexpr (KC) {
-    o.rsrc = buffer_rsrc(X + (int64_t)mn0 * ld, (uint32_t)((int64_t)BMN * ld * 2));
+    o.rsrc = buffer_rsrc(Xb + (int64_t)mn0 * ld * ES, (uint32_t)((int64_t)BMN * ld * ES));
     const int r_in = lane >> 3;
     const int cl_even = (lane & 7) ^ (r_in >> 1);
     const int cl_odd = (lane & 7) ^ ((4 + (r_in >> 1)) & 7);
 #pragma unroll
     for (int t = 0; t < o.BLOCKS; ++t) {
       const int j = wave + t * NW;
-      o.voff[t] = ((j * 8 + r_in) * (int)ld + ((j & 1) ? cl_odd : cl_even) * 8) * 2;
+      o.voff[t] = (j * 8 + r_in) * (int)ld * ES + ((j & 1) ? cl_odd : cl_even) * 16;
     }
-    o.soff_step = 64 * 2;
+    o.soff_step = 128;
   } else {
-    constexpr int CPR = NTOperand<KC, BMN, NW>::CPR;
+    constexpr int CPR = NTOperand<KC, BMN, NW, ES>::CPR;
     constexpr int RPB = 64 / CPR;  // rows per 1 KB block
-    o.rsrc = buffer_rsrc(X + mn0, (uint32_t)((int64_t)K * ld * 2));
+    o.rsrc = buffer_rsrc(Xb + (int64_t)mn0 * ES, (uint32_t)((int64_t)K * ld * ES));
 #pragma unroll
     for (int t = 0; t < o.BLOCKS; ++t) {
       const int q = wave + t * NW;
@@ -679,13 +680,13 @@ __device__ __forceinline__ void nt_operand_init(NTOperand<KC, BMN, NW>& o, const
 }
 
 template <int IN, int OUT, int ACT, int BM, int BN, int WM, int WN, bool AKC, bool BKC>
-__global__ __launch_bounds__(64 * WM * WN) void gemm_nt16_kernel(NTParams p) {
-  constexpr int BK = 64;
-  constexpr int KS = BK / 16;  // MFMA sub-steps per K-step
+__global__ __launch_bounds__(64 * WM * WN) void gemm_nt_kernel(NTParams p) {
+  constexpr int ES = IN == IN_F32 ? 4 : 2;  // element bytes
+  constexpr int KS = 4;                      // MFMA sub-steps per K-step (one 16-byte chunk pair each)
   constexpr int NW = WM * WN;
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int TM = WTM / 32, TN = WTN / 32;
-  constexpr int A_BYTES = BM * BK * 2, B_BYTES = BN * BK * 2;
+  constexpr int A_BYTES = BM * 128, B_BYTES = BN * 128;  // 128 B of K per row and stage
   constexpr int STAGE = A_BYTES + B_BYTES;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE];
 
@@ -696,8 +697,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt16_kernel(NTParams p) {
   const int wm = wave / WN, wn = wave % WN;
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
 
-  NTOperand<AKC, BM, NW> opa;
-  NTOperand<BKC, BN, NW> opb;
+  NTOperand<AKC, BM, NW, ES> opa;
+  NTOperand<BKC, BN, NW, ES> opb;
   nt_operand_init(opa, p.A, p.lda, m0, p.K, lane, wave);
   nt_operand_init(opb, p.B, p.ldb, n0, p.K, lane, wave);
 
@@ -763,21 +764,37 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt16_kernel(NTParams p) {
 #pragma unroll
     for (int j = 0; j < TM; ++j) {
       if constexpr (AKC) fa[buf][j] = *reinterpret_cast<const u16x8*>(st + a_off[j] + chunk);
-      else fa[buf][j] = tr_frag(st + a_off[j] + kk * 16 * (BM * 2), BM * 2);
+      else fa[buf][j] = tr_frag(st + a_off[j] + kk * 16 * (BM * ES), BM * ES);
     }
 #pragma unroll
     for (int i = 0; i < TN; ++i) {
       if constexpr (BKC) fb[buf][i] = *reinterpret_cast<const u16x8*>(st + b_off[i] + chunk);
-      else fb[buf][i] = tr_frag(st + b_off[i] + kk * 16 * (BN * 2), BN * 2);
+      else fb[buf][i] = tr_frag(st + b_off[i] + kk * 16 * (BN * ES), BN * ES);
     }
   };
+  // 16-bit: one 32x32x16 MFMA per block and sub-step (8 K per lane half).
+  // fp32: the 16-byte fragment holds 4 K values; MFMA e (32x32x2) takes
+  // element e from both halves, so A and B see the same K permutation.
   auto mfmas = [&](int buf) {
+    if constexpr (ES == 2) {
 #pragma unroll
-    for (int i = 0; i < TN; ++i)
+      for (int i = 0; i < TN; ++i)
 #pragma unroll
-      for (int j = 0; j < TM; ++j)
-        acc[i][j] = mfma32<IN>(reinterpret_cast<const uint16_t*>(&fb[buf][i]),
-                               reinterpret_cast<const uint16_t*>(&fa[buf][j]), acc[i][j]);
+        for (int j = 0; j < TM; ++j)
+          acc[i][j] = mfma32<IN>(reinterpret_cast<const uint16_t*>(&fb[buf][i]),
+                                 reinterpret_cast<const uint16_t*>(&fa[buf][j]), acc[i][j]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+          for (int j = 0; j < TM; ++j) {
+            const float a = reinterpret_cast<const float*>(&fb[buf][i])[e];
+            const float b = reinterpret_cast<const float*>(&fa[buf][j])[e];
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc[i][j], 0, 0, 0);
+          }
+    }
   };
   // One ds_read after each MFMA, MFMA first: the lgkmcnt wait in front of a
   // sub-step's first MFMA then covers only reads issued during the previous
@@ -786,7 +803,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt16_kernel(NTParams p) {
   // followed by its ceil-share of reads), so the last reads still have
   // several MFMAs to land before the next sub-step needs them.
   constexpr int NDS = (AKC ? TM : 2 * TM) + (BKC ? TN : 2 * TN);
-  constexpr int NMF = TM * TN;
+  constexpr int NMF = TM * TN * (ES == 4 ? 4 : 1);
   auto interleave = [&]() { sched_interleave<NMF, NDS>(std::make_integer_sequence<int, NMF>{}); };
 
   // Pipeline: a K-step has KS sub-steps; the fragments of sub-step s+1 are
@@ -795,7 +812,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt16_kernel(NTParams p) {
   // registers): after it the next stage is visible to every wave (so its
   // first fragments are read during the last MFMAs) and the current stage
   // is no longer read by anyone (so the loads of K-step kt+2 refill it).
-  const int nk = p.K / BK;
+  const int nk = p.K / (128 / ES);
   constexpr int LAST = (KS - 1) & 1;  // fragment buffer of the last sub-step
   issue_loads(0, 0);
   __builtin_amdgcn_s_waitcnt(0);
@@ -919,8 +936,8 @@ Status run_cfg(GemmParams& p, hipStream_t s) {
 template <int IN, int OUT, int ACT, int BM, int BN, int WM, int WN, bool AKC, bool BKC>
 Status run_nt_act(const GemmParams& g, hipStream_t s) {
   NTParams p{};
-  p.A = (const uint16_t*)g.A;
-  p.B = (const uint16_t*)g.B;
+  p.A = g.A;
+  p.B = g.B;
   p.C = g.C;
   p.bias = g.bias;
   p.aux = g.aux;
@@ -934,9 +951,9 @@ Status run_nt_act(const GemmParams& g, hipStream_t s) {
   p.bias_f32 = g.bias_f32;
   p.tiles_m = p.M / BM;
   p.tiles_n = p.N / BN;
-  gemm_nt16_kernel<IN, OUT, ACT, BM, BN, WM, WN, AKC, BKC>
+  gemm_nt_kernel<IN, OUT, ACT, BM, BN, WM, WN, AKC, BKC>
       <<<(unsigned)(p.tiles_m * p.tiles_n), 64 * WM * WN, 0, s>>>(p);
-  return launch_status("gemm_nt16");
+  return launch_status("gemm_nt");
 }
 
 template <int IN, int OUT, int BM, int BN, int WM, int WN, bool AKC, bool BKC>
@@ -970,16 +987,17 @@ Status run_nt(const GemmParams& g, hipStream_t s) {
 // 16-byte aligned rows, bias is contiguous, and the shape tiles exactly.
 template <int IN, int OUT>
 bool nt_eligible(const GemmParams& p, int BM, int BN, bool mn_ok) {
-  if (IN == IN_F32) return false;
+  constexpr int ES = IN == IN_F32 ? 4 : 2;
+  mn_ok = mn_ok && ES == 2;  // the transposing LDS read is 16-bit
   auto operand_ok = [&](int mode, int64_t ld_k, int64_t ld_mn, int64_t rows_mn) {
-    if (mode == LD_KCONTIG) return (ld_k * 2) % 16 == 0 && rows_mn * ld_k * 2 < INT32_MAX;
-    if (mode == LD_MNCONTIG && mn_ok) return (ld_mn * 2) % 16 == 0 && p.K * ld_mn * 2 < INT32_MAX;
+    if (mode == LD_KCONTIG) return (ld_k * ES) % 16 == 0 && rows_mn * ld_k * ES < INT32_MAX;
+    if (mode == LD_MNCONTIG && mn_ok) return (ld_mn * ES) % 16 == 0 && p.K * ld_mn * ES < INT32_MAX;
     return false;
   };
   // A view [M, K]: K-contiguous row stride a_rs, MN-contiguous row stride a_cs.
   // B view [K, N]: K-contiguous row stride b_cs, MN-contiguous row stride b_rs.
   if (!operand_ok(p.a_mode, p.a_rs, p.a_cs, BM) || !operand_ok(p.b_mode, p.b_cs, p.b_rs, BN)) return false;
-  if (p.M % BM || p.N % BN || p.K % 64) return false;
+  if (p.M % BM || p.N % BN || p.K % (128 / ES)) return false;
   if ((uintptr_t)p.A % 16 || (uintptr_t)p.B % 16) return false;
   const int osz = OUT == OUT_F32 ? 4 : 2;
   if (p.c_cs != 1 || (uintptr_t)p.C % 16 || (p.c_rs * osz) % 16) return false;
@@ -991,10 +1009,16 @@ bool nt_eligible(const GemmParams& p, int BM, int BN, bool mn_ok) {
 
 template <int IN, int OUT>
 Status run_gemm(GemmParams& p, hipStream_t s) {
-  if constexpr (IN != IN_F32) {
+  {
+    constexpr bool MN = IN != IN_F32;
     const int64_t tiles256 = (p.M / 256) * (p.N / 256);
-    if (tiles256 >= 128 && nt_eligible<IN, OUT>(p, 256, 256, true))
-      return run_nt<IN, OUT, 256, 256, 2, 4, true>(p, s);
+    const int64_t tiles128 = (p.M / 128) * (p.N / 128);
+    if (tiles256 >= 128 && nt_eligible<IN, OUT>(p, 256, 256, MN))
+      return run_nt<IN, OUT, 256, 256, 2, 4, MN>(p, s);
+    if (tiles128 >= 128 && nt_eligible<IN, OUT>(p, 128, 128, false))
+      return run_nt<IN, OUT, 128, 128, 2, 2, false>(p, s);
+    // fewer tiles than CUs at 128x128: 64x64 tiles (4 waves of 32x32)
+    if (nt_eligible<IN, OUT>(p, 64, 64, false)) return run_nt<IN, OUT, 64, 64, 2, 2, false>(p, s);
     if (nt_eligible<IN, OUT>(p, 128, 128, false)) return run_nt<IN, OUT, 128, 128, 2, 2, false>(p, s);
   }
   // Large problems: 128x128 workgroup tiles (4 waves, 64x64 per wave).

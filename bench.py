@@ -83,6 +83,72 @@ def bench_gemm(C, M, N, K, act_kind=None, iters=20, warmup=5, save_preact=False)
     return {"ms": ms, "tflops": 2.0 * M * N * K / (ms * 1e-3) / 1e12}
 
 
+# C4: GEMM + bias + activation over the configured shapes (GEPI kinds:
+# 1 bias only, 0 bias+ReLU, 3 bias+GELU)
+C4_SHAPES = [(1024, 1024, 1024), (4096, 4096, 4096), (8192, 8192, 8192),
+             (8192, 4096, 256), (8192, 4096, 11008)]
+C4_ACTS = {"none": 1, "relu": 0, "gelu": 3}
+
+
+def bench_c4(C, dtype="bf16", shapes=C4_SHAPES, acts=("none", "relu", "gelu"), iters=10):
+    """X~U(-1,1)/sqrt(K) [M,K], W [N,K], b [N]; act(X.W^T + b).  bf16: bf16 in,
+    fp32 accumulate, bf16 out; fp32: fp32 throughout."""
+    import torch
+
+    out = {}
+    for (M, N, K) in shapes:
+        g = torch.Generator(device="cuda")
+        g.manual_seed(M + N + K)
+        s = 1.0 / math.sqrt(K)
+        tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+        X = ((torch.rand((M, K), device="cuda", generator=g) * 2 - 1) * s).to(tdt)
+        W = ((torch.rand((N, K), device="cuda", generator=g) * 2 - 1) * s).to(tdt)
+        b = ((torch.rand(N, device="cuda", generator=g) * 2 - 1) * s)
+        Y = torch.empty((M, N), device="cuda", dtype=tdt)
+        kid = "gemm_epilogue_bf16_mfma_v0" if dtype == "bf16" else "gemm_epilogue_f32_mfma_v0"
+        flops = 2.0 * M * N * K
+        for act in acts:
+            pay = struct.pack("<iii", 0, 1, C4_ACTS[act])
+            fn = lambda: C.launch_by_id(kid, C.OpKind.GemmEpilogue, [X, W, b], [Y], GEPI, pay)  # noqa: E731
+            n = iters if flops < 1e12 else max(3, iters // 2)
+            ms = time_launches(fn, n, 2)
+            tf = flops / (ms * 1e-3) / 1e12
+            peak = PEAK_BF16_TFLOPS if dtype == "bf16" else PEAK_FP32_TFLOPS
+            out[f"c4_{dtype}_{M}x{N}x{K}_{act}"] = {"value": round(tf, 2), "unit": "TFLOP/s",
+                                                    "frac": round(tf / peak, 4), "ms": round(ms, 4)}
+    return out
+
+
+# C1: the reference MLP (fp32, B=64, 784->256(ReLU)->10, softmax-xent, Adam)
+def bench_c1(steps=200, warmup=5):
+    """Replayed-graph time of one C1 train step."""
+    import torch
+
+    from aicf_cuda import _C
+    from aicf_hip import mlp
+
+    ir, lowered, plan = mlp.build_mlp_xent()
+    data = mlp.init_mlp_xent()
+    params = {k: torch.from_numpy(v.copy()).cuda() for k, v in data.items() if "." in k}
+    inputs = {"x": torch.from_numpy(data["x"]).cuda(), "t": torch.from_numpy(data["t"]).cuda()}
+    ex = mlp.make_executor(ir, lowered, plan)
+    ex.build_env(inputs=inputs, params=params, reuse_static=False)
+    ex.capture(inputs=inputs, params=params, reuse_static=True)
+    gs = torch.cuda.ExternalStream(int(_C.graph_stream()))
+    ex.replay(warmup)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(gs)
+    ex.replay(steps)
+    e1.record(gs)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / steps
+    loss = float(ex.value("loss").item())
+    ex.reset_graph()
+    return {"value": round(us, 2), "unit": "us/step", "steps_per_s": round(1e6 / us, 1),
+            "ops_per_step": len(lowered), "loss_after": loss}
+
+
 # ------------------------------------------------------------------ softmax
 def bench_softmax(C, rows, cols, iters=20, warmup=3):
     """Row softmax + row max + row sum, fp32; rotates buffer sets so the
@@ -369,6 +435,13 @@ def main():
         comps["adamw_2^28"] = {"value": round(ad["gbs"], 1), "unit": "GB/s",
                                "frac": round(ad["gbs"] / PEAK_HBM_GBS, 4), "ms": round(ad["ms"], 4)}
         log(f"[bench] adam {ad}")
+        c1 = bench_c1()
+        comps["c1_mlp_fp32_64x784x256x10_step"] = c1
+        log(f"[bench] c1 {c1}")
+        for dt, shapes in (("bf16", C4_SHAPES), ("fp32", C4_SHAPES[:3])):
+            c4 = bench_c4(C, dt, shapes)
+            comps.update(c4)
+            log(f"[bench] c4 {dt} {c4}")
 
     cpu = None
     if not args.no_cpu:

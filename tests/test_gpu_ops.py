@@ -407,8 +407,9 @@ def test_gemm_f16_probe_shapes(C, ta, tb):
 
 
 @pytest.mark.parametrize("M,N,K,ta,tb", [
-    (4096, 4096, 128, False, True),   # 256x256-tile fast path
-    (1024, 1024, 1024, False, True),
+    (4096, 4096, 128, False, True),   # 256x256 tiles
+    (2048, 1024, 128, False, True),   # 128x128 tiles
+    (1024, 1024, 1024, False, True),  # 64x64 tiles
     (100, 72, 784, False, True),
     (64, 256, 784, False, True),
     (256, 4096, 256, False, True),
@@ -471,6 +472,27 @@ def test_gemm_bf16_dgelu_with_mn_contiguous_weight_256_tiles(C):
     ref = _gemm_ref(orc.bf16_bits_to_f32(dY).reshape(M, K), orc.bf16_bits_to_f32(W).reshape(K, N),
                     False, False) * orc.gelu_grad_f64(orc.bf16_bits_to_f32(Z).reshape(M, N).astype(np.float64))
     assert orc.rel_err(orc.bf16_bits_to_f32(h(dz)).reshape(M, N), ref) < 1e-2
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 256, 96), (512, 384, 160), (2048, 1024, 96), (4096, 4096, 64)])
+def test_gemm_f32_tiled_paths(C, M, N, K):
+    """fp32 X[M,K] . W[N,K]^T on the tiled MFMA paths (64x64, 128x128 and
+    256x256 tiles, 32x32x2 fp32 MFMA), plain and with the bias+GELU /
+    bias+ReLU epilogues, vs the fp64 oracle."""
+    r = rng(M + N + K)
+    X = r.uniform(-1, 1, (M, K)).astype(np.float32)
+    W = (r.uniform(-1, 1, (N, K)) / np.sqrt(K)).astype(np.float32)
+    b = r.uniform(-1, 1, N).astype(np.float32)
+    ref = _gemm_ref(X, W, False, True)
+    o = torch.empty((M, N), device="cuda")
+    C.op_call(int(C.OpKind.Gemm), [g(X), g(W)], [o], 0, struct.pack("<ii", 0, 1), 0)
+    assert orc.rel_err(h(o), ref) < 1e-4
+    C.op_call(int(C.OpKind.GemmEpilogue), [g(X), g(W), g(b)], [o], GEPI, struct.pack("<iii", 0, 1, 3), 0)
+    assert orc.rel_err(h(o), orc.gelu_f64(ref + b[None, :])) < 1e-4
+    C.op_call(int(C.OpKind.GemmEpilogue), [g(X), g(W), g(b)], [o], GPEL, struct.pack("<iii", 0, 1, 1), 0)
+    want = np.maximum(ref + b[None, :], 0)
+    assert orc.rel_err(h(o), want) < 1e-4
+    assert np.all(h(o)[want == 0] == 0)
 
 
 @pytest.mark.parametrize("relu", [1, 0])
