@@ -27,7 +27,8 @@ INCLUDE = REPO / "include"
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 HIPCC = str(ROCM / "bin" / "hipcc")
 
-HIP_SOURCES = ["kernels/optim.hip", "kernels/eltwise.hip", "kernels/reduce.hip", "kernels/gemm.hip"]
+HIP_SOURCES = ["kernels/optim.hip", "kernels/eltwise.hip", "kernels/reduce.hip", "kernels/gemm.hip",
+               "kernels/norm.hip"]
 CXX_SOURCES = ["registry/registry.cpp", "registry/register_all.cpp", "runtime/graph.cpp"]
 
 HIP_FLAGS = [

@@ -1,8 +1,7 @@
 // Registration table: every kernel id the reference pins
 // (src/backends/cuda/registry/register_all.cpp:105-290), with the same
-// OpKind and priority, mapped to the gfx950 implementations, plus the ids of
-// the appended ops.  LayerNorm / BatchNorm ids are not registered (those
-// kinds are out of scope), so by-id dispatch of them returns NotImplemented.
+// OpKind, priority and schema gate, mapped to the gfx950 implementations,
+// plus the ids of the appended ops.
 #include <cstdio>
 #include <cstdlib>
 
@@ -51,6 +50,13 @@ KernelVariant make_reduce_sum_lastdim_bf16_to_f32_variant();
 KernelVariant make_row_softmax_f32_variant();
 KernelVariant make_row_reduce_f32_variant();
 KernelVariant make_softmax_xent_f32_variant();
+// norm.hip
+KernelVariant make_layernorm_fwd_f32_variant();
+KernelVariant make_layernorm_fwd_f16_variant();
+KernelVariant make_layernorm_bwd_f32_variant();
+KernelVariant make_layernorm_bwd_f16_variant();
+KernelVariant make_batchnorm_fwd_f16_variant();
+KernelVariant make_batchnorm_bwd_f16_variant();
 // gemm.hip
 KernelVariant make_gemm_f32_naive_variant();
 KernelVariant make_gemm_f16_tc_wmma_out_f16_variant();
@@ -138,6 +144,14 @@ void register_all_kernels_into(KernelRegistry& R) {
 
   reg(OpKind::StepInc, make_step_inc_variant(), 0, "step_inc_v0");
   reg(OpKind::BiasCorr, make_biascorr_variant(), 0, "bias_corr_v0");
+
+  // LayerNorm / BatchNorm (reference: f16 10, f32 0)
+  reg(OpKind::LayerNormFwd, make_layernorm_fwd_f16_variant(), 10, "layernorm_fwd_f16_v0");
+  reg(OpKind::LayerNormFwd, make_layernorm_fwd_f32_variant(), 0, "layernorm_fwd_f32_v0");
+  reg(OpKind::LayerNormBwd, make_layernorm_bwd_f16_variant(), 10, "layernorm_bwd_f16_v0");
+  reg(OpKind::LayerNormBwd, make_layernorm_bwd_f32_variant(), 0, "layernorm_bwd_f32_v0");
+  reg(OpKind::BatchNormFwd, make_batchnorm_fwd_f16_variant(), 10, "batchnorm_fwd_f16_v0");
+  reg(OpKind::BatchNormBwd, make_batchnorm_bwd_f16_variant(), 10, "batchnorm_bwd_f16_v0");
 
   // appended kinds
   reg(OpKind::RowSoftmax, make_row_softmax_f32_variant(), 0, "row_softmax_f32_v0");

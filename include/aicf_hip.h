@@ -85,6 +85,8 @@ extern "C" {
 #define AICF_SCHEMA_ADAM 0x4D414441u /* adam_step/launcher.cu:32     <ffff> lr,b1,b2,eps (+<f> wd) */
 #define AICF_SCHEMA_BCOR 0x524F4342u /* biascorr/launcher.cu:31      <ff>  beta1, beta2 */
 #define AICF_SCHEMA_SGDS 0x53444753u /* sgd_step/launcher.cu:31      <f>   lr */
+#define AICF_SCHEMA_LNEP 0x50454E4Cu /* layernorm/launcher.cu:41      <f>   eps (default 1e-5) */
+#define AICF_SCHEMA_BNEP 0x50454E42u /* batchnorm/launcher.cu:51      <fI>  eps, flags (bit0 use_running_stats) */
 #define AICF_SCHEMA_RRED 0x44455252u /* appended: b"RRED" little-endian, <i> 0=sum 1=max */
 
 /* GEPI epilogue kinds.  0..2 are the values core_v2/exec.py:223-252 packs;

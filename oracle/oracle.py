@@ -320,6 +320,82 @@ def gemm_ref_f32(A, B, transA=False, transB=False, rows=None):
 
 
 # ---------------------------------------------------------------- metrics
+# ---------------------------------------------------------------- LayerNorm
+def layernorm_fwd_f64(x, gamma=None, beta=None, eps=1e-5):
+    """layernorm/launcher.cu:128-216 (layernorm_fwd_*_kernel): per row mean,
+    biased variance, rstd = 1/sqrt(var + eps), y = (x - mean) rstd [* gamma +
+    beta].  fp64, on the stored inputs."""
+    x = np.asarray(x, np.float64)
+    mu = x.mean(axis=1)
+    var = ((x - mu[:, None]) ** 2).mean(axis=1)
+    rs = 1.0 / np.sqrt(var + eps)
+    y = (x - mu[:, None]) * rs[:, None]
+    if gamma is not None:
+        y = y * np.asarray(gamma, np.float64)[None, :] + np.asarray(beta, np.float64)[None, :]
+    return y, mu, rs
+
+
+def layernorm_bwd_f64(x, dy, mean, rstd, gamma=None):
+    """layernorm/launcher.cu:221-371 (bwd_dx and bwd_dg_db kernels):
+    dyh = dy * gamma, xhat = (x - mean) rstd,
+    dx = (N dyh - sum(dyh) - xhat sum(dyh xhat)) rstd / N,
+    dgamma = sum_m dy xhat, dbeta = sum_m dy (None without gamma)."""
+    x, dy = np.asarray(x, np.float64), np.asarray(dy, np.float64)
+    mean, rstd = np.asarray(mean, np.float64), np.asarray(rstd, np.float64)
+    N = x.shape[1]
+    xh = (x - mean[:, None]) * rstd[:, None]
+    dyh = dy if gamma is None else dy * np.asarray(gamma, np.float64)[None, :]
+    s1 = dyh.sum(axis=1, keepdims=True)
+    s2 = (dyh * xh).sum(axis=1, keepdims=True)
+    dx = (N * dyh - s1 - xh * s2) * (rstd[:, None] / N)
+    if gamma is None:
+        return dx, None, None
+    return dx, (dy * xh).sum(axis=0), dy.sum(axis=0)
+
+
+# ---------------------------------------------------------------- BatchNorm (NCHW)
+def batchnorm_fwd_train_f64(x, gamma=None, beta=None, eps=1e-5):
+    """batchnorm/launcher.cu:113-188,402-440 (training): per channel batch
+    mean and biased variance over N, H, W; rstd = 1/sqrt(var + eps);
+    y = (x - mean) rstd [* gamma + beta].  Returns (y, mean, rstd)."""
+    x = np.asarray(x, np.float64)
+    mu = x.mean(axis=(0, 2, 3))
+    var = ((x - mu[None, :, None, None]) ** 2).mean(axis=(0, 2, 3))
+    rs = 1.0 / np.sqrt(var + eps)
+    y = (x - mu[None, :, None, None]) * rs[None, :, None, None]
+    if gamma is not None:
+        y = y * np.asarray(gamma, np.float64)[None, :, None, None] + \
+            np.asarray(beta, np.float64)[None, :, None, None]
+    return y, mu, rs
+
+
+def batchnorm_fwd_infer_f64(x, rmean, rvar, gamma=None, beta=None, eps=1e-5):
+    """batchnorm/launcher.cu:190-222 (bn_infer_apply_f16): running statistics."""
+    x = np.asarray(x, np.float64)
+    rs = 1.0 / np.sqrt(np.asarray(rvar, np.float64) + eps)
+    y = (x - np.asarray(rmean, np.float64)[None, :, None, None]) * rs[None, :, None, None]
+    if gamma is not None:
+        y = y * np.asarray(gamma, np.float64)[None, :, None, None] + \
+            np.asarray(beta, np.float64)[None, :, None, None]
+    return y
+
+
+def batchnorm_bwd_f64(x, dy, gamma, mean, rstd):
+    """batchnorm/launcher.cu:224-290,528-590 (affine training backward):
+    dbeta = sum dy, dgamma = sum dy xhat,
+    dx = (NHW dy - dbeta - xhat dgamma) gamma rstd / NHW."""
+    x, dy = np.asarray(x, np.float64), np.asarray(dy, np.float64)
+    mean, rstd = np.asarray(mean, np.float64), np.asarray(rstd, np.float64)
+    g = np.asarray(gamma, np.float64)
+    cnt = x.shape[0] * x.shape[2] * x.shape[3]
+    xh = (x - mean[None, :, None, None]) * rstd[None, :, None, None]
+    s1 = dy.sum(axis=(0, 2, 3))
+    s2 = (dy * xh).sum(axis=(0, 2, 3))
+    dx = (cnt * dy - s1[None, :, None, None] - xh * s2[None, :, None, None]) * \
+        (g * rstd / cnt)[None, :, None, None]
+    return dx, s2, s1
+
+
 def rel_err(y, r) -> float:
     """Normwise relative error max|y - r| / max(max|r|, 1e-30)."""
     y = np.asarray(y, np.float64)

@@ -56,10 +56,19 @@ REFERENCE_IDS = [
     (10, "adam_step_f32_v0", 0),
     (11, "step_inc_v0", 0),
     (12, "bias_corr_v0", 0),
+    (13, "layernorm_fwd_f16_v0", 10),
+    (13, "layernorm_fwd_f32_v0", 0),
+    (14, "layernorm_bwd_f16_v0", 10),
+    (14, "layernorm_bwd_f32_v0", 0),
+    (15, "batchnorm_fwd_f16_v0", 10),
+    (16, "batchnorm_bwd_f16_v0", 10),
 ]
-OUT_OF_SCOPE_IDS = [(13, "layernorm_fwd_f16_v0"), (13, "layernorm_fwd_f32_v0"),
-                    (14, "layernorm_bwd_f16_v0"), (14, "layernorm_bwd_f32_v0"),
-                    (15, "batchnorm_fwd_f16_v0"), (16, "batchnorm_bwd_f16_v0")]
+# register_all.cpp:259-290: schema gates (0 = none)
+REFERENCE_GATES = {"layernorm_fwd_f16_v0": int.from_bytes(b"LNEP", "little"),
+                   "layernorm_fwd_f32_v0": int.from_bytes(b"LNEP", "little"),
+                   "layernorm_bwd_f16_v0": 0, "layernorm_bwd_f32_v0": 0,
+                   "batchnorm_fwd_f16_v0": int.from_bytes(b"BNEP", "little"),
+                   "batchnorm_bwd_f16_v0": 0}
 
 FAKE = 0x100000  # never dereferenced: every call below is rejected on the host
 
@@ -121,8 +130,11 @@ def test_reference_kernel_ids_and_priorities(lib):
         prios = [lib.aicf_registry_priority(kind, i) for i in range(n)]
         assert prios[ids.index(kid)] == prio, kid
         assert prios == sorted(prios, reverse=True), f"kind {kind} not in priority order"
-    for kind, kid in OUT_OF_SCOPE_IDS:
-        assert lib.aicf_registry_has(kind, kid.encode()) == 0
+    for kind, kid, _ in REFERENCE_IDS:
+        if kid in REFERENCE_GATES:
+            n = lib.aicf_registry_count(kind)
+            ids = [lib.aicf_registry_kernel_id(kind, i).decode() for i in range(n)]
+            assert lib.aicf_registry_schema(kind, ids.index(kid)) == REFERENCE_GATES[kid], kid
     # reference schema gates: Adam requires ADAM, BiasCorr requires BCOR
     assert lib.aicf_registry_schema(10, [lib.aicf_registry_kernel_id(10, i).decode()
                                          for i in range(2)].index("adam_step_f32_v0")) == \
@@ -210,9 +222,22 @@ def test_by_id_status_rules(lib):
     # empty id -> InvalidArgument; unknown id -> NotImplemented
     assert _call(lib, 1, [P], [P], kid="") == INV
     assert _call(lib, 1, [P], [P], kid="no_such_kernel_v0") == NOTIMPL
-    # out-of-scope kinds keep their values but have no variants
-    assert _call(lib, 13, [P], [P], kid="layernorm_fwd_f32_v0") == NOTIMPL
+    # LayerNorm fwd is schema-gated (LNEP): schema 0 by id -> InvalidArgument,
+    # by op_call -> no eligible variant -> NotImplemented (registry.cpp:35-38,181-190)
+    assert _call(lib, 13, [P], [P], kid="layernorm_fwd_f32_v0") == INV
     assert _call(lib, 13, [P], [P]) == NOTIMPL
+    lnep = int.from_bytes(b"LNEP", "little")
+    # right schema, wrong rank (v2_layernorm_probe NEG rank) -> unsupported
+    x3 = d((2, 3, 4))
+    assert _call(lib, 13, [x3], [x3, d((2,)), d((2,))], lnep, struct.pack("<f", 1e-5)) == NOTIMPL
+    assert _call(lib, 13, [x3], [x3, d((2,)), d((2,))], lnep, struct.pack("<f", 1e-5),
+                 kid="layernorm_fwd_f32_v0") == INV
+    # BatchNorm: wrong rank -> NotImplemented; wrong schema -> NotImplemented (v2_batchnorm_probe)
+    bnep = int.from_bytes(b"BNEP", "little")
+    x2 = d((8, 16), F16)
+    assert _call(lib, 15, [x2], [x2], bnep, struct.pack("<fI", 1e-5, 1)) == NOTIMPL
+    x4 = d((8, 16, 8, 8), F16)
+    assert _call(lib, 15, [x4, d((16,)), d((16,))], [x4], 0x12345678, b"\x00" * 8) == NOTIMPL
     # unsupported call to an existing id -> InvalidArgument
     assert _call(lib, 1, [d((8, 7))], [d((8, 8))], kid="relu_f32_v0") == INV
     # kid registered under another kind -> NotImplemented

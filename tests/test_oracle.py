@@ -259,3 +259,65 @@ def test_gemm_f64_matches_numpy(ta, tb):
     assert orc.rel_err(g32, ref) < 1e-6
     part = orc.gemm_ref_f32(A, B, ta, tb, rows=(8, 16))
     assert np.array_equal(part[8:16], g32[8:16]) and not part[:8].any()
+
+
+# ---------------------------------------------------------------- LayerNorm / BatchNorm
+@pytest.mark.parametrize("affine", [False, True])
+def test_layernorm_matches_torch(affine):
+    r = rng(21)
+    M, N = 7, 33  # v2_layernorm_probe.py shapes include (7, 33)
+    x = r.standard_normal((M, N)) * 3 + 1.5
+    dy = r.standard_normal((M, N))
+    g = r.standard_normal(N) if affine else None
+    b = r.standard_normal(N) if affine else None
+    y, mu, rs = orc.layernorm_fwd_f64(x, g, b, eps=1e-5)
+    xt = torch.from_numpy(x).requires_grad_(True)
+    gt = torch.from_numpy(g).requires_grad_(True) if affine else None
+    bt = torch.from_numpy(b).requires_grad_(True) if affine else None
+    yt = torch.nn.functional.layer_norm(xt, (N,), gt, bt, eps=1e-5)
+    assert np.max(np.abs(y - yt.detach().numpy())) < 1e-12
+    assert np.max(np.abs(mu - x.mean(1))) < 1e-13
+    assert np.max(np.abs(rs - 1 / np.sqrt(x.var(1) + 1e-5))) < 1e-12
+    yt.backward(torch.from_numpy(dy))
+    dx, dg, db = orc.layernorm_bwd_f64(x, dy, mu, rs, g)
+    assert np.max(np.abs(dx - xt.grad.numpy())) < 1e-11
+    if affine:
+        assert np.max(np.abs(dg - gt.grad.numpy())) < 1e-11
+        assert np.max(np.abs(db - bt.grad.numpy())) < 1e-11
+    else:
+        assert dg is None and db is None
+
+
+def test_layernorm_constant_row_closed_form():
+    x = np.full((2, 16), 3.25)
+    y, mu, rs = orc.layernorm_fwd_f64(x, eps=1e-5)
+    assert np.all(y == 0) and np.all(mu == 3.25)
+    assert np.allclose(rs, 1 / np.sqrt(1e-5), rtol=1e-15)
+
+
+@pytest.mark.parametrize("affine", [False, True])
+def test_batchnorm_matches_torch(affine):
+    r = rng(22)
+    Nb, C, H, W = 7, 5, 5, 3
+    x = r.standard_normal((Nb, C, H, W)) * 2 - 0.5
+    dy = r.standard_normal((Nb, C, H, W))
+    g = r.standard_normal(C) if affine else None
+    b = r.standard_normal(C) if affine else None
+    y, mu, rs = orc.batchnorm_fwd_train_f64(x, g, b, eps=1e-5)
+    xt = torch.from_numpy(x).requires_grad_(True)
+    gt = torch.from_numpy(g).requires_grad_(True) if affine else None
+    bt = torch.from_numpy(b).requires_grad_(True) if affine else None
+    yt = torch.nn.functional.batch_norm(xt, None, None, gt, bt, training=True, momentum=0.0, eps=1e-5)
+    assert np.max(np.abs(y - yt.detach().numpy())) < 1e-12
+    if affine:
+        yt.backward(torch.from_numpy(dy))
+        dx, dg, db = orc.batchnorm_bwd_f64(x, dy, g, mu, rs)
+        assert np.max(np.abs(dx - xt.grad.numpy())) < 1e-11
+        assert np.max(np.abs(dg - gt.grad.numpy())) < 1e-11
+        assert np.max(np.abs(db - bt.grad.numpy())) < 1e-11
+    rm, rv = r.standard_normal(C), r.uniform(0.5, 1.5, C)
+    yi = orc.batchnorm_fwd_infer_f64(x, rm, rv, g, b, eps=1e-5)
+    yti = torch.nn.functional.batch_norm(torch.from_numpy(x), torch.from_numpy(rm), torch.from_numpy(rv),
+                                         None if g is None else torch.from_numpy(g),
+                                         None if b is None else torch.from_numpy(b), training=False, eps=1e-5)
+    assert np.max(np.abs(yi - yti.numpy())) < 1e-12
