@@ -292,6 +292,41 @@ PYBIND11_MODULE(_C, m) {
   });
   m.def("graph_stream", []() -> uint64_t { return aicf_graph_stream(); });
 
+  // graph handles (not in the reference binding): several instantiated graphs
+  // side by side, re-capture updating the executable in place
+  m.def("graph_create", []() -> uint64_t {
+    uint64_t h = 0;
+    hip_check(aicf_graph_create(&h), "graph_create");
+    return h;
+  });
+  m.def("graph_destroy", [](uint64_t h) { hip_check(aicf_graph_destroy(h), "graph_destroy"); },
+        py::arg("handle"));
+  m.def(
+      "graph_begin_h",
+      [](uint64_t h) -> uint64_t {
+        {
+          std::lock_guard<std::mutex> lock(g_mu);
+          g_trace.clear();
+        }
+        uint64_t s = 0;
+        hip_check(aicf_graph_begin_h(h, &s), "hipStreamBeginCapture");
+        return s;
+      },
+      py::arg("handle"));
+  m.def("graph_end_h", [](uint64_t h) { hip_check(aicf_graph_end_h(h), "hipGraphInstantiate"); },
+        py::arg("handle"));
+  m.def(
+      "graph_launch_h",
+      [](uint64_t h) { hip_check(aicf_graph_launch_h(h, current_stream()), "hipGraphLaunch"); },
+      py::arg("handle"));
+  m.def("graph_reset_h", [](uint64_t h) { hip_check(aicf_graph_reset_h(h), "graph_reset"); },
+        py::arg("handle"));
+  m.def("graph_stream_h", [](uint64_t h) -> uint64_t { return aicf_graph_stream_h(h); },
+        py::arg("handle"));
+  m.def("graph_state_h", [](uint64_t h) -> int { return aicf_graph_state_h(h); }, py::arg("handle"));
+  m.def("graph_updates_h", [](uint64_t h) -> uint64_t { return aicf_graph_updates_h(h); },
+        py::arg("handle"));
+
   // introspection helpers (not in the reference binding)
   m.def("registry_kernel_ids", [](int kind) {
     std::vector<std::string> ids;

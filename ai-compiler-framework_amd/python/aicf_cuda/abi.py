@@ -57,6 +57,15 @@ SIGNATURES = {
     "aicf_graph_reset": (ctypes.c_int32, []),
     "aicf_graph_stream": (ctypes.c_uint64, []),
     "aicf_graph_state": (ctypes.c_int32, []),
+    "aicf_graph_create": (ctypes.c_int32, [ctypes.POINTER(ctypes.c_uint64)]),
+    "aicf_graph_destroy": (ctypes.c_int32, [ctypes.c_uint64]),
+    "aicf_graph_begin_h": (ctypes.c_int32, [ctypes.c_uint64, ctypes.POINTER(ctypes.c_uint64)]),
+    "aicf_graph_end_h": (ctypes.c_int32, [ctypes.c_uint64]),
+    "aicf_graph_launch_h": (ctypes.c_int32, [ctypes.c_uint64, ctypes.c_void_p]),
+    "aicf_graph_reset_h": (ctypes.c_int32, [ctypes.c_uint64]),
+    "aicf_graph_stream_h": (ctypes.c_uint64, [ctypes.c_uint64]),
+    "aicf_graph_state_h": (ctypes.c_int32, [ctypes.c_uint64]),
+    "aicf_graph_updates_h": (ctypes.c_uint64, [ctypes.c_uint64]),
     "aicf_last_error": (ctypes.c_char_p, []),
 }
 

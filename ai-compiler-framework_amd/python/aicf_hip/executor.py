@@ -12,6 +12,10 @@ Follows the reference's PlannedExecutor (core_v2/exec.py:302-497):
     (exec.py:396,423-431);
   * capture = graph_begin, the same op loop on the capture stream,
     graph_end; replay = n x graph_launch (exec.py:467-497).
+With own_graph=True the executor captures into a graph handle of its own
+(_C.graph_create) instead of the process-wide graph, so several executors
+stay instantiated side by side; capturing again on that handle (recapture,
+e.g. after binding other input tensors) updates the executable in place.
 Attributes are packed for every op that has any (the reference packs only
 gemm, gemm_epilogue and adam_step, exec.py:263-277, so e.g. sgd_step ran
 with its default lr).
@@ -131,7 +135,8 @@ def _canon(s: str) -> str:
 
 class PlannedExecutor:
     def __init__(self, *, ir: IRGraph, lowered: List[Dict[str, Any]], plan: BindingPlan,
-                 device: Optional[torch.device] = None, opts: Optional[ExecOptions] = None):
+                 device: Optional[torch.device] = None, opts: Optional[ExecOptions] = None,
+                 own_graph: bool = False):
         self.ir = ir
         self.lowered = lowered
         self.plan = plan
@@ -139,6 +144,8 @@ class PlannedExecutor:
         self.opts = opts or ExecOptions()
         self.env: Dict[int, torch.Tensor] = {}
         self._captured = False
+        self._own_graph = bool(own_graph)
+        self._handle: Optional[int] = None
         # resolve kinds and pack attributes once; the per-op host work in the
         # loop is then only the tensor list lookup and the binding call
         self._ops = []
@@ -250,16 +257,41 @@ class PlannedExecutor:
     def capture(self, *, inputs: Dict[str, Any], params: Dict[str, Any],
                 reuse_static: bool = True) -> Dict[int, torch.Tensor]:
         self.build_env(inputs=inputs, params=params, reuse_static=reuse_static)
+        self._capture_env()
+        return self.env
+
+    @torch.no_grad()
+    def recapture(self, *, inputs: Optional[Dict[str, Any]] = None,
+                  params: Optional[Dict[str, Any]] = None) -> Dict[int, torch.Tensor]:
+        """Binds the given tensors over the current environment (statics are
+        kept) and captures again.  On an own graph handle the executable is
+        updated in place when the op sequence is unchanged."""
+        if not self.env:
+            raise RuntimeError("[exec] recapture called before capture()")
+        self.build_env(inputs=dict(inputs or {}), params=dict(params or {}), reuse_static=True)
+        self._capture_env()
+        return self.env
+
+    def _capture_env(self) -> None:
         # work queued on torch's stream (initialisation of the bound tensors)
         # must be complete before the first replay reads them
         torch.cuda.synchronize()
-        s = int(_C.graph_begin())
-        try:
-            self._execute_lowered(stream=s)
-        finally:
-            _C.graph_end()
+        self._captured = False
+        if self._own_graph:
+            if self._handle is None:
+                self._handle = int(_C.graph_create())
+            s = int(_C.graph_begin_h(self._handle))
+            try:
+                self._execute_lowered(stream=s)
+            finally:
+                _C.graph_end_h(self._handle)
+        else:
+            s = int(_C.graph_begin())
+            try:
+                self._execute_lowered(stream=s)
+            finally:
+                _C.graph_end()
         self._captured = True
-        return self.env
 
     @torch.no_grad()
     def replay(self, n: int = 1) -> None:
@@ -267,11 +299,37 @@ class PlannedExecutor:
             return
         if not self._captured:
             raise RuntimeError("[exec] replay called before capture()")
-        for _ in range(int(n)):
-            _C.graph_launch()
+        if self._handle is not None:
+            for _ in range(int(n)):
+                _C.graph_launch_h(self._handle)
+        else:
+            for _ in range(int(n)):
+                _C.graph_launch()
+
+    @property
+    def graph_handle(self) -> Optional[int]:
+        return self._handle
+
+    @property
+    def graph_updates(self) -> int:
+        """Captures applied to this executor's own graph by in-place update."""
+        return int(_C.graph_updates_h(self._handle)) if self._handle is not None else 0
+
+    def graph_stream(self) -> int:
+        return int(_C.graph_stream_h(self._handle)) if self._handle is not None else int(_C.graph_stream())
 
     def reset_graph(self) -> None:
-        _C.graph_reset()
+        if self._handle is not None:
+            _C.graph_reset_h(self._handle)
+        else:
+            _C.graph_reset()
+        self._captured = False
+
+    def close(self) -> None:
+        """Releases the own graph handle (its graph, stream and event)."""
+        if self._handle is not None:
+            h, self._handle = self._handle, None
+            _C.graph_destroy(h)
         self._captured = False
 
     def value(self, name: str) -> torch.Tensor:

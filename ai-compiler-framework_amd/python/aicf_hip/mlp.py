@@ -189,9 +189,10 @@ def init_mlp_mse(B: int, D: int, L: int, seed: int = 0, device: str = "cuda:0"):
     return {"x": x, "t": t}, {"flat.params": P}
 
 
-def make_executor(ir, lowered, plan, device="cuda:0", require_kernel_id=True) -> PlannedExecutor:
+def make_executor(ir, lowered, plan, device="cuda:0", require_kernel_id=True,
+                  own_graph=False) -> PlannedExecutor:
     return PlannedExecutor(ir=ir, lowered=lowered, plan=plan, device=torch.device(device),
-                           opts=ExecOptions(require_kernel_id=require_kernel_id))
+                           opts=ExecOptions(require_kernel_id=require_kernel_id), own_graph=own_graph)
 
 
 def refresh_shadow(ex: PlannedExecutor) -> None:

@@ -321,7 +321,7 @@ def pmc_report(fetch_csv, write_csv):
                 if row.get("Counter_Name") != counter:
                     continue
                 name = row.get("Kernel_Name", "")
-                key = "gemm" if "gemm_nt16" in name else "copy" if "map1" in name else None
+                key = "gemm" if "gemm_nt" in name else "copy" if "map1" in name else None
                 if key:
                     vals[key].append(float(row["Counter_Value"]))
         return vals

@@ -58,10 +58,10 @@ extern "C" {
 #define AICF_OP_ADAM_STEP 10
 #define AICF_OP_STEP_INC 11
 #define AICF_OP_BIAS_CORR 12
-#define AICF_OP_LAYERNORM_FWD 13 /* reserved: no variant registered */
-#define AICF_OP_LAYERNORM_BWD 14 /* reserved: no variant registered */
-#define AICF_OP_BATCHNORM_FWD 15 /* reserved: no variant registered */
-#define AICF_OP_BATCHNORM_BWD 16 /* reserved: no variant registered */
+#define AICF_OP_LAYERNORM_FWD 13
+#define AICF_OP_LAYERNORM_BWD 14
+#define AICF_OP_BATCHNORM_FWD 15
+#define AICF_OP_BATCHNORM_BWD 16
 #define AICF_OP_GEMM_EPILOGUE 17
 /* appended kinds (no counterpart in the reference) */
 #define AICF_OP_ROW_SOFTMAX 18  /* X[R,C] -> softmax Y (+ row max, row sum of X) */
@@ -198,6 +198,40 @@ int32_t aicf_graph_reset(void);
 uint64_t aicf_graph_stream(void);
 /* 1 while capturing, 2 when a graph is instantiated, 0 otherwise. */
 int32_t aicf_graph_state(void);
+
+/*
+ * Graph handles.  The reference keeps exactly one graph per process (the
+ * singleton above, which is handle 0 here); these entry points have no
+ * counterpart there.  They let several plans stay instantiated at once and
+ * let a plan be captured again with other buffers bound without building a
+ * new executable.  Each created handle owns its own non-blocking stream and
+ * captures in thread-local mode.  Handle 0 is accepted by every *_h call and
+ * behaves like the singleton, except that aicf_graph_begin_h keeps its
+ * executable for an in-place update.
+ */
+/* Creates an empty graph handle (never 0). */
+int32_t aicf_graph_create(uint64_t* out_handle);
+/* Ends a dangling capture, destroys the graph objects, stream and event of
+ * `handle`.  INVALID_ARGUMENT for handle 0 or an unknown handle. */
+int32_t aicf_graph_destroy(uint64_t handle);
+/* Begins a capture on the handle's stream (written to *out_stream).  An
+ * executable graph from an earlier capture is kept until aicf_graph_end_h
+ * and is not launchable meanwhile. */
+int32_t aicf_graph_begin_h(uint64_t handle, uint64_t* out_stream);
+/* Ends the capture.  When the handle already holds an executable graph it is
+ * updated in place (hipGraphExecUpdate) if the new capture has the same
+ * topology; otherwise a new executable is instantiated. */
+int32_t aicf_graph_end_h(uint64_t handle);
+/* As aicf_graph_launch, on the handle's graph and stream. */
+int32_t aicf_graph_launch_h(uint64_t handle, void* caller_stream);
+/* As aicf_graph_reset, for one handle (the handle stays valid). */
+int32_t aicf_graph_reset_h(uint64_t handle);
+/* The handle's stream (0 before its first capture or for unknown handles). */
+uint64_t aicf_graph_stream_h(uint64_t handle);
+/* As aicf_graph_state; -1 for an unknown handle. */
+int32_t aicf_graph_state_h(uint64_t handle);
+/* Number of captures applied to the handle by in-place update. */
+uint64_t aicf_graph_updates_h(uint64_t handle);
 
 /* Message of the last failing HIP runtime call made by this library on the
  * calling thread ("" if none). */

@@ -256,3 +256,31 @@ def test_graph_misuse_is_rejected_without_a_gpu(lib):
     assert lib.aicf_graph_launch(None) == INV
     assert b"no captured graph" in lib.aicf_last_error()
     assert lib.aicf_graph_stream() == 0
+
+
+def test_graph_handles_without_a_gpu(lib):
+    """Handle bookkeeping needs no device: create / query / misuse / destroy."""
+    import ctypes
+
+    h = ctypes.c_uint64(0)
+    assert lib.aicf_graph_create(ctypes.byref(h)) == 0 and h.value != 0
+    h2 = ctypes.c_uint64(0)
+    assert lib.aicf_graph_create(ctypes.byref(h2)) == 0 and h2.value not in (0, h.value)
+    hv = ctypes.c_uint64(h.value)
+    assert lib.aicf_graph_state_h(hv) == 0
+    assert lib.aicf_graph_stream_h(hv) == 0
+    assert lib.aicf_graph_updates_h(hv) == 0
+    assert lib.aicf_graph_end_h(hv) == INV
+    assert b"not capturing" in lib.aicf_last_error()
+    assert lib.aicf_graph_launch_h(hv, None) == INV
+    assert b"no captured graph" in lib.aicf_last_error()
+    assert lib.aicf_graph_reset_h(hv) == 0
+    assert lib.aicf_graph_destroy(ctypes.c_uint64(0)) == INV
+    assert lib.aicf_graph_destroy(hv) == 0
+    assert lib.aicf_graph_state_h(hv) == -1
+    assert lib.aicf_graph_destroy(hv) == INV
+    assert b"unknown graph handle" in lib.aicf_last_error()
+    assert lib.aicf_graph_launch_h(hv, None) == INV
+    assert lib.aicf_graph_destroy(ctypes.c_uint64(h2.value)) == 0
+    # handle 0 is the process-wide graph and always exists
+    assert lib.aicf_graph_state_h(ctypes.c_uint64(0)) == lib.aicf_graph_state()
