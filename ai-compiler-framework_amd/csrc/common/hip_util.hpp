@@ -43,12 +43,19 @@ typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
   return __uint_as_float(static_cast<uint32_t>(h) << 16);
 }
-// Round-to-nearest-even; NaN stays a quiet NaN.
+// fp32 -> bf16, round-to-nearest-even, NaN -> quiet NaN (top payload bits
+// kept, quiet bit set): gfx950's v_cvt_pk_bf16_f32, two values per
+// instruction.  Its results equal the integer formulation
+// (u + 0x7fff + ((u >> 16) & 1)) >> 16, with (u >> 16) | 0x40 for NaN, on
+// every rounding tie, denormal, infinity and NaN pattern; that formulation
+// written with a NaN branch compiled to divergent code in unrolled loops.
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{lo, hi}), bf16x2_t));
+}
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  return static_cast<uint16_t>(f32x2_to_bf16x2(f, 0.0f));
 }
 // binary16 <-> fp32 with integer operations only.  The reference converts
 // with __half2float (exact) and __float2half_rn (one RNE rounding of the

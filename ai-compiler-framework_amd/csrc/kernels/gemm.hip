@@ -498,10 +498,13 @@ __device__ __forceinline__ void nt_epilogue_staged(const NTParams& p,
   auto put4 = [&](int off, const float* v) {
     if constexpr (OB == 4) {
       *reinterpret_cast<f32x4*>(tile + off) = f32x4{v[0], v[1], v[2], v[3]};
+    } else if constexpr (OUT == OUT_BF16) {
+      typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+      *reinterpret_cast<u32x2*>(tile + off) = u32x2{f32x2_to_bf16x2(v[0], v[1]), f32x2_to_bf16x2(v[2], v[3])};
     } else {
       u16x4 o;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = OUT == OUT_BF16 ? f32_to_bf16(v[e]) : f32_to_f16(v[e]);
+      for (int e = 0; e < 4; ++e) o[e] = f32_to_f16(v[e]);
       *reinterpret_cast<u16x4*>(tile + off) = o;
     }
   };
