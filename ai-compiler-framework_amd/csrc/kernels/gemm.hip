@@ -28,6 +28,7 @@
 //     MFMAs of tile k run, with one barrier per K step;
 //   * workgroup ids are remapped so that consecutive tiles of one XCD share
 //     A rows (grouped column-major raster per XCD).
+#include <type_traits>
 #include <utility>
 
 #include "../common/hip_util.hpp"
@@ -371,9 +372,9 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_kernel(GemmParams p) {
 // Tiled MFMA path for tile-divisible shapes: 16-bit operands (each
 // K-contiguous or M/N-contiguous) and fp32 operands (K-contiguous).
 //   * BM x BN workgroup tiles; a stage holds 128 bytes of K per row (64
-//     16-bit or 32 fp32 elements); WM x WN waves (two per SIMD for the
-//     256x256 tile), each owning (BM/WM) x (BN/WN) = TM x TN blocks of 32x32
-//     fp32 accumulators (v_mfma_f32_32x32x16_bf16/f16, or 4 x
+//     16-bit or 32 fp32 elements); WM x WN waves (one or two per SIMD for
+//     the 256x256 tile), each owning (BM/WM) x (BN/WN) = TM x TN blocks of
+//     32x32 fp32 accumulators (v_mfma_f32_32x32x16_bf16/f16, or 4 x
 //     v_mfma_f32_32x32x2f32 per 16-byte fp32 fragment);
 //   * global -> LDS with gfx950's direct 16-byte LDS loads
 //     (buffer_load_dwordx4 ... lds): lane i of a wave fills bytes
@@ -384,7 +385,9 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_kernel(GemmParams p) {
 //     sub-step so that no wave waits on LDS after it;
 //   * the MFMA fragments of sub-step s+1 are read from LDS while the MFMAs of
 //     sub-step s run (two register sets), spread over the MFMAs
-//     (sched_group_barrier);
+//     (sched_group_barrier); with K-contiguous operands the next K-step's
+//     loads are spread over two sub-steps as well (all at once, they back up
+//     the address queue of the CU and stall the MFMA issue);
 //   * MFMA operands swapped (A-operand = W rows, B-operand = X rows) so that
 //     each lane holds 4 consecutive output columns of one row;
 //   * the epilogue stages the output tile through LDS and stores whole rows;
@@ -621,6 +624,43 @@ __device__ __forceinline__ void sched_interleave(std::integer_sequence<int, T...
   (sched_interleave_step<NMF, NDS, T>(), ...);
 }
 
+template <int V>
+using template_int_t = std::integral_constant<int, V>;
+
+// Schedule of one MFMA sub-step of the NT kernel: MFMA t is followed by its
+// FPER fragments' LDS reads (front-loaded, so the last reads still have
+// several MFMAs to land before the next sub-step needs them) and by its
+// share of the NV loads (load u after MFMA t when t*NV/NMF <= u <
+// (t+1)*NV/NMF).  sched_group_barrier masks: 0x008 MFMA, 0x100 DS read,
+// 0x020 VMEM read.
+template <int TM, int TN, int ES, bool AKC, bool BKC>
+struct NTSched {
+  static constexpr int NMF = TM * TN * (ES == 4 ? 4 : 1);  // MFMAs per sub-step
+  static constexpr int NFR = TM + TN;                      // fragments per sub-step
+  static constexpr int FPER = (NFR + NMF - 1) / NMF;       // fragments per MFMA
+  static constexpr int ds_instrs(int lo, int hi) {
+    int n = 0;
+    for (int r = lo; r < hi && r < NFR; ++r) n += r < TM ? (AKC ? 1 : 2) : (BKC ? 1 : 2);
+    return n;
+  }
+  template <bool R, int NV, int T>
+  static __device__ __forceinline__ void step() {
+    constexpr int nds = R ? ds_instrs(T * FPER, (T + 1) * FPER) : 0;
+    constexpr int vlo = T * NV / NMF, vhi = (T + 1) * NV / NMF;
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    if constexpr (nds > 0) __builtin_amdgcn_sched_group_barrier(0x100, nds, 0);
+    if constexpr (vhi > vlo) __builtin_amdgcn_sched_group_barrier(0x020, vhi - vlo, 0);
+  }
+  template <bool R, int NV, int... T>
+  static __device__ __forceinline__ void seq(std::integer_sequence<int, T...>) {
+    (step<R, NV, T>(), ...);
+  }
+  template <bool R, int NV>
+  static __device__ __forceinline__ void pin() {
+    seq<R, NV>(std::make_integer_sequence<int, NMF>{});
+  }
+};
+
 // One operand of the NT kernel: BMN rows (the M or N dimension) x BK = 64
 // K-elements per stage.
 //   KC (K-contiguous, memory [MN][K] with row stride ld): 1 KB LDS blocks of
@@ -775,6 +815,122 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt_kernel(NTParams p) {
       else fb[buf][i] = tr_frag(st + b_off[i] + kk * 16 * (BN * ES), BN * ES);
     }
   };
+  if constexpr (AKC && BKC) {
+  // Single operations of the pipeline, emitted one by one in the order the
+  // schedule below pins (the compiler keeps LDS-writing loads and LDS reads
+  // in program order, so the order has to be written out).
+  //   fragment r: r < TM is A fragment r, else B fragment r - TM (one
+  //     ds_read_b128, or two ds_read_b64_tr_b16 for an M/N-contiguous tile);
+  //   MFMA t: block (i, j) = (t / TM % TN, t % TM); fp32 runs 4 MFMAs per
+  //     block and sub-step, t / (TM * TN) selecting the fragment element;
+  //   load u: 1 KB direct-to-LDS block u of the wave (A blocks first).
+  auto read_one = [&](const uint8_t* st, int kk, int buf, int r) {
+    const int chunk = ((kk * 2 + fh) ^ rsw) * 16;
+    if (r < TM) {
+      if constexpr (AKC) fa[buf][r] = *reinterpret_cast<const u16x8*>(st + a_off[r] + chunk);
+      else fa[buf][r] = tr_frag(st + a_off[r] + kk * 16 * (BM * ES), BM * ES);
+    } else {
+      const int i = r - TM;
+      if constexpr (BKC) fb[buf][i] = *reinterpret_cast<const u16x8*>(st + b_off[i] + chunk);
+      else fb[buf][i] = tr_frag(st + b_off[i] + kk * 16 * (BN * ES), BN * ES);
+    }
+  };
+  auto mfma_one = [&](int buf, int t) {
+    const int i = (t / TM) % TN, j = t % TM;
+    if constexpr (ES == 2) {
+      acc[i][j] = mfma32<IN>(reinterpret_cast<const uint16_t*>(&fb[buf][i]),
+                             reinterpret_cast<const uint16_t*>(&fa[buf][j]), acc[i][j]);
+    } else {
+      const int e = t / (TM * TN);
+      const float a = reinterpret_cast<const float*>(&fb[buf][i])[e];
+      const float b = reinterpret_cast<const float*>(&fa[buf][j])[e];
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc[i][j], 0, 0, 0);
+    }
+  };
+  auto load_one = [&](int kt, int stage, int u) {
+    uint8_t* base = smem + stage * STAGE;
+    if (u < opa.BLOCKS)
+      raw_buffer_load_lds(opa.rsrc, (__attribute__((address_space(3))) unsigned*)(base + (wave_s + u * NW) * 1024),
+                          16, opa.voff[u], kt * opa.soff_step, 0, 0);
+    else
+      raw_buffer_load_lds(
+          opb.rsrc, (__attribute__((address_space(3))) unsigned*)(base + A_BYTES + (wave_s + (u - opa.BLOCKS) * NW) * 1024),
+          16, opb.voff[u - opa.BLOCKS], kt * opb.soff_step, 0, 0);
+  };
+  using Sched = NTSched<TM, TN, ES, AKC, BKC>;
+  constexpr int NMF = Sched::NMF, NFR = Sched::NFR, FPER = Sched::FPER;
+  constexpr int NVM = opa.BLOCKS + opb.BLOCKS;  // loads per wave and K-step
+  // One sub-step: the MFMAs on fragment buffer `buf`; when R, the fragments
+  // of sub-step rkk of stage `rst` into buffer rbuf (front-loaded, FPER per
+  // MFMA); loads [VLO, VHI) of K-step lkt into stage lst, spread evenly.
+  auto substep = [&](auto R, auto VLO, auto VHI, int buf, const uint8_t* rst, int rkk, int rbuf, int lkt,
+                     int lst) {
+    constexpr int vlo = decltype(VLO)::value, vhi = decltype(VHI)::value, nv = vhi - vlo;
+#pragma unroll
+    for (int t = 0; t < NMF; ++t) {
+      mfma_one(buf, t);
+      if constexpr (decltype(R)::value) {
+#pragma unroll
+        for (int q = 0; q < FPER; ++q)
+          if (t * FPER + q < NFR) read_one(rst, rkk, rbuf, t * FPER + q);
+      }
+      if constexpr (nv > 0) {
+#pragma unroll
+        for (int u = vlo + t * nv / NMF; u < vlo + (t + 1) * nv / NMF; ++u) load_one(lkt, lst, u);
+      }
+    }
+    Sched::template pin<decltype(R)::value, nv>();
+  };
+  using Rd = std::true_type;
+  using NoRd = std::false_type;
+  template_int_t<0> z;
+
+  // Pipeline.  A K-step (128 bytes of K per row) has four sub-steps; the
+  // fragments of sub-step s+1 are read during the MFMAs of sub-step s, from
+  // two register sets.  The body of the K loop starts with the K-step's only
+  // barrier: after it the stage of K-step kt+1 is visible to every wave and
+  // the stage of K-step kt is read by none, so the loads of K-step kt+2
+  // refill it.  The body then runs the last sub-step of kt (its fragments are
+  // already in registers) and sub-steps 0-2 of kt+1, with the loads of kt+2
+  // spread over its first two sub-steps: issued all at once after the barrier
+  // they back up the address queue and stall the MFMA issue, and issued in
+  // the third sub-step they have too little time left before the next wait.
+  const int nk = p.K / (128 / ES);
+  constexpr int L1 = NVM / 2;  // loads in the first of the two sub-steps
+  issue_loads(0, 0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (nk > 1) issue_loads(1, 1);
+  read_frags(smem, 0, 0);
+  substep(Rd{}, z, z, 0, smem, 1, 1, 0, 0);
+  substep(Rd{}, z, z, 1, smem, 2, 0, 0, 0);
+  substep(Rd{}, z, z, 0, smem, 3, 1, 0, 0);
+  int kt = 0;
+  for (; kt + 2 < nk; ++kt) {
+    __builtin_amdgcn_s_waitcnt(0);  // own loads of K-step kt+1 and fragment reads done
+    __syncthreads();
+    const uint8_t* nx = smem + ((kt + 1) & 1) * STAGE;
+    const int ls = kt & 1;
+    substep(Rd{}, z, template_int_t<L1>{}, 1, nx, 0, 0, kt + 2, ls);
+    substep(Rd{}, template_int_t<L1>{}, template_int_t<NVM>{}, 0, nx, 1, 1, kt + 2, ls);
+    substep(Rd{}, z, z, 1, nx, 2, 0, 0, 0);
+    substep(Rd{}, z, z, 0, nx, 3, 1, 0, 0);
+  }
+  if (kt + 1 < nk) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    const uint8_t* nx = smem + ((kt + 1) & 1) * STAGE;
+    substep(Rd{}, z, z, 1, nx, 0, 0, 0, 0);
+    substep(Rd{}, z, z, 0, nx, 1, 1, 0, 0);
+    substep(Rd{}, z, z, 1, nx, 2, 0, 0, 0);
+    substep(Rd{}, z, z, 0, nx, 3, 1, 0, 0);
+  }
+  substep(NoRd{}, z, z, 1, nullptr, 0, 0, 0, 0);
+  } else {
+  // M/N-contiguous operands: their transposing LDS reads are not known to be
+  // disjoint from the in-flight direct-to-LDS loads, so the compiler waits
+  // for all loads before each such read that follows one; the loads are
+  // therefore issued in one group after the barrier (one wait per K-step).
   // 16-bit: one 32x32x16 MFMA per block and sub-step (8 K per lane half).
   // fp32: the 16-byte fragment holds 4 K values; MFMA e (32x32x2) takes
   // element e from both halves, so A and B see the same K permutation.
@@ -846,6 +1002,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt_kernel(NTParams p) {
       interleave();
     }
     mfmas(LAST);
+  }
   }
 
   __syncthreads();  // every wave is done reading the last stage
@@ -984,6 +1141,24 @@ Status run_nt(const GemmParams& g, hipStream_t s) {
   return Status::Internal;  // excluded by nt_eligible
 }
 
+// 256 x 256 tiles.  bf16 with K-contiguous operands and a one-output
+// epilogue (none, ReLU): four waves of 128 x 128, one per SIMD, which issue
+// the MFMAs back to back.  Everything else: eight waves of 128 x 64; the
+// GELU (two outputs) and dGELU (pre-activation read) epilogues move twice
+// the bytes per wave with four waves, f16's integer-rounded epilogue needs
+// the registers, and the M/N-contiguous loop waits for its loads once per
+// K-step, which the second wave on each SIMD covers.
+template <int IN, int OUT>
+Status run_nt256(const GemmParams& g, hipStream_t s) {
+  if constexpr (IN == IN_BF16) {
+    if (g.a_mode == LD_KCONTIG && g.b_mode == LD_KCONTIG) {
+      if (g.act == ACT_NONE) return run_nt_act<IN, OUT, ACT_NONE, 256, 256, 2, 2, true, true>(g, s);
+      if (g.act == ACT_RELU) return run_nt_act<IN, OUT, ACT_RELU, 256, 256, 2, 2, true, true>(g, s);
+    }
+  }
+  return run_nt<IN, OUT, 256, 256, 2, 4, IN != IN_F32>(g, s);
+}
+
 // The NT fast path applies to 16-bit operands that are each K-contiguous
 // ([MN][K]) or, on the 256 x 256 tiles, MN-contiguous ([K][MN]), with 16-byte
 // aligned bases and rows; C (and the aux matrix) have unit column stride with
@@ -1016,8 +1191,7 @@ Status run_gemm(GemmParams& p, hipStream_t s) {
     constexpr bool MN = IN != IN_F32;
     const int64_t tiles256 = (p.M / 256) * (p.N / 256);
     const int64_t tiles128 = (p.M / 128) * (p.N / 128);
-    if (tiles256 >= 128 && nt_eligible<IN, OUT>(p, 256, 256, MN))
-      return run_nt<IN, OUT, 256, 256, 2, 4, MN>(p, s);
+    if (tiles256 >= 128 && nt_eligible<IN, OUT>(p, 256, 256, MN)) return run_nt256<IN, OUT>(p, s);
     if (tiles128 >= 128 && nt_eligible<IN, OUT>(p, 128, 128, false))
       return run_nt<IN, OUT, 128, 128, 2, 2, false>(p, s);
     // fewer tiles than CUs at 128x128: 64x64 tiles (4 waves of 32x32)
