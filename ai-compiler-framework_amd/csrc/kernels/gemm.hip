@@ -406,6 +406,22 @@ typedef int i32x4_t __attribute__((ext_vector_type(4)));
 __device__ void raw_buffer_load_lds(i32x4_t rsrc, __attribute__((address_space(3))) unsigned* lds,
                                     int size, int voffset, int soffset, int offset,
                                     int aux) __asm("llvm.amdgcn.raw.buffer.load.lds");
+// The same load written as inline asm (M0 = LDS address, set by the
+// compiler through the constraint; the nop covers the M0 -> LDS-DMA hazard).
+// The compiler does not know that it writes LDS, so it adds no vmcnt wait in
+// front of the LDS reads that follow it: it cannot prove that a transposing
+// ds_read_b64_tr_b16 does not alias an in-flight direct-to-LDS load, and
+// with the intrinsic it waits for all loads before every such read.  The
+// kernel orders every LDS read of a stage after that stage's loads itself
+// (s_waitcnt 0 + barrier at the top of each K-step).  The memory clobber
+// keeps the loads in program order with the LDS reads.
+__device__ __forceinline__ void asm_buffer_load_lds(i32x4_t rsrc, uint32_t lds_addr, int voffset,
+                                                    int soffset) {
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+               :
+               : "v"(voffset), "s"(rsrc), "s"(soffset), "{m0}"(lds_addr)
+               : "memory");
+}
 __device__ __forceinline__ i32x4_t buffer_rsrc(const void* base, uint32_t bytes) {
   struct __attribute__((packed)) Rsrc {
     const void* ptr;
@@ -608,22 +624,6 @@ __device__ __forceinline__ void nt_epilogue_staged(const NTParams& p,
   }
 }
 
-// Scheduling pattern of one MFMA sub-step: NMF MFMAs, each followed by its
-// front-loaded share of the NDS LDS reads (sched_group_barrier masks: 0x008
-// MFMA, 0x100 DS read).
-template <int NMF, int NDS, int T>
-__device__ __forceinline__ void sched_interleave_step() {
-  constexpr int PER = (NDS + NMF - 1) / NMF;
-  constexpr int lo = T * PER < NDS ? T * PER : NDS;
-  constexpr int hi = (T + 1) * PER < NDS ? (T + 1) * PER : NDS;
-  __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-  if constexpr (hi > lo) __builtin_amdgcn_sched_group_barrier(0x100, hi - lo, 0);
-}
-template <int NMF, int NDS, int... T>
-__device__ __forceinline__ void sched_interleave(std::integer_sequence<int, T...>) {
-  (sched_interleave_step<NMF, NDS, T>(), ...);
-}
-
 template <int V>
 using template_int_t = std::integral_constant<int, V>;
 
@@ -745,17 +745,28 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt_kernel(NTParams p) {
   nt_operand_init(opa, p.A, p.lda, m0, p.K, lane, wave);
   nt_operand_init(opb, p.B, p.ldb, n0, p.K, lane, wave);
 
-  auto issue_loads = [&](int kt, int stage) {
+  // Load u of the wave for K-step kt into stage `stage`: 1 KB direct-to-LDS
+  // block u (A blocks first).  With an M/N-contiguous operand the loads are
+  // issued as inline asm (no compiler waits in front of the transposing
+  // reads); K-contiguous kernels use the intrinsic, which the scheduler
+  // places by itself.
+  constexpr bool ASM_LDS = !(AKC && BKC);
+  constexpr int NVM = opa.BLOCKS + opb.BLOCKS;  // loads per wave and K-step
+  auto load_one = [&](int kt, int stage, int u) {
     uint8_t* base = smem + stage * STAGE;
+    const bool is_a = u < opa.BLOCKS;
+    uint8_t* dst = is_a ? base + (wave_s + u * NW) * 1024 : base + A_BYTES + (wave_s + (u - opa.BLOCKS) * NW) * 1024;
+    const i32x4_t rsrc = is_a ? opa.rsrc : opb.rsrc;
+    const int voff = is_a ? opa.voff[u] : opb.voff[u - opa.BLOCKS];
+    const int soff = kt * (is_a ? opa.soff_step : opb.soff_step);
+    if constexpr (ASM_LDS)
+      asm_buffer_load_lds(rsrc, (uint32_t)(uintptr_t)dst, voff, soff);
+    else
+      raw_buffer_load_lds(rsrc, (__attribute__((address_space(3))) unsigned*)dst, 16, voff, soff, 0, 0);
+  };
+  auto issue_loads = [&](int kt, int stage) {
 #pragma unroll
-    for (int t = 0; t < opa.BLOCKS; ++t)
-      raw_buffer_load_lds(opa.rsrc, (__attribute__((address_space(3))) unsigned*)(base + (wave_s + t * NW) * 1024),
-                          16, opa.voff[t], kt * opa.soff_step, 0, 0);
-#pragma unroll
-    for (int t = 0; t < opb.BLOCKS; ++t)
-      raw_buffer_load_lds(opb.rsrc,
-                          (__attribute__((address_space(3))) unsigned*)(base + A_BYTES + (wave_s + t * NW) * 1024),
-                          16, opb.voff[t], kt * opb.soff_step, 0, 0);
+    for (int u = 0; u < NVM; ++u) load_one(kt, stage, u);
   };
 
   floatx16 acc[TN][TM];
@@ -815,7 +826,6 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt_kernel(NTParams p) {
       else fb[buf][i] = tr_frag(st + b_off[i] + kk * 16 * (BN * ES), BN * ES);
     }
   };
-  if constexpr (AKC && BKC) {
   // Single operations of the pipeline, emitted one by one in the order the
   // schedule below pins (the compiler keeps LDS-writing loads and LDS reads
   // in program order, so the order has to be written out).
@@ -847,19 +857,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt_kernel(NTParams p) {
       acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc[i][j], 0, 0, 0);
     }
   };
-  auto load_one = [&](int kt, int stage, int u) {
-    uint8_t* base = smem + stage * STAGE;
-    if (u < opa.BLOCKS)
-      raw_buffer_load_lds(opa.rsrc, (__attribute__((address_space(3))) unsigned*)(base + (wave_s + u * NW) * 1024),
-                          16, opa.voff[u], kt * opa.soff_step, 0, 0);
-    else
-      raw_buffer_load_lds(
-          opb.rsrc, (__attribute__((address_space(3))) unsigned*)(base + A_BYTES + (wave_s + (u - opa.BLOCKS) * NW) * 1024),
-          16, opb.voff[u - opa.BLOCKS], kt * opb.soff_step, 0, 0);
-  };
   using Sched = NTSched<TM, TN, ES, AKC, BKC>;
   constexpr int NMF = Sched::NMF, NFR = Sched::NFR, FPER = Sched::FPER;
-  constexpr int NVM = opa.BLOCKS + opb.BLOCKS;  // loads per wave and K-step
   // One sub-step: the MFMAs on fragment buffer `buf`; when R, the fragments
   // of sub-step rkk of stage `rst` into buffer rbuf (front-loaded, FPER per
   // MFMA); loads [VLO, VHI) of K-step lkt into stage lst, spread evenly.
@@ -879,7 +878,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt_kernel(NTParams p) {
         for (int u = vlo + t * nv / NMF; u < vlo + (t + 1) * nv / NMF; ++u) load_one(lkt, lst, u);
       }
     }
-    Sched::template pin<decltype(R)::value, nv>();
+    Sched::template pin<decltype(R)::value, ASM_LDS ? 0 : nv>();  // asm loads are in no sched group
   };
   using Rd = std::true_type;
   using NoRd = std::false_type;
@@ -926,84 +925,6 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt_kernel(NTParams p) {
     substep(Rd{}, z, z, 0, nx, 3, 1, 0, 0);
   }
   substep(NoRd{}, z, z, 1, nullptr, 0, 0, 0, 0);
-  } else {
-  // M/N-contiguous operands: their transposing LDS reads are not known to be
-  // disjoint from the in-flight direct-to-LDS loads, so the compiler waits
-  // for all loads before each such read that follows one; the loads are
-  // therefore issued in one group after the barrier (one wait per K-step).
-  // 16-bit: one 32x32x16 MFMA per block and sub-step (8 K per lane half).
-  // fp32: the 16-byte fragment holds 4 K values; MFMA e (32x32x2) takes
-  // element e from both halves, so A and B see the same K permutation.
-  auto mfmas = [&](int buf) {
-    if constexpr (ES == 2) {
-#pragma unroll
-      for (int i = 0; i < TN; ++i)
-#pragma unroll
-        for (int j = 0; j < TM; ++j)
-          acc[i][j] = mfma32<IN>(reinterpret_cast<const uint16_t*>(&fb[buf][i]),
-                                 reinterpret_cast<const uint16_t*>(&fa[buf][j]), acc[i][j]);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-#pragma unroll
-        for (int i = 0; i < TN; ++i)
-#pragma unroll
-          for (int j = 0; j < TM; ++j) {
-            const float a = reinterpret_cast<const float*>(&fb[buf][i])[e];
-            const float b = reinterpret_cast<const float*>(&fa[buf][j])[e];
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc[i][j], 0, 0, 0);
-          }
-    }
-  };
-  // One ds_read after each MFMA, MFMA first: the lgkmcnt wait in front of a
-  // sub-step's first MFMA then covers only reads issued during the previous
-  // sub-step, never one issued just before it.
-  // ds reads per sub-step, spread over its MFMAs front-loaded (MFMA t is
-  // followed by its ceil-share of reads), so the last reads still have
-  // several MFMAs to land before the next sub-step needs them.
-  constexpr int NDS = (AKC ? TM : 2 * TM) + (BKC ? TN : 2 * TN);
-  constexpr int NMF = TM * TN * (ES == 4 ? 4 : 1);
-  auto interleave = [&]() { sched_interleave<NMF, NDS>(std::make_integer_sequence<int, NMF>{}); };
-
-  // Pipeline: a K-step has KS sub-steps; the fragments of sub-step s+1 are
-  // read while the MFMAs of sub-step s run.  The only barrier of a K-step
-  // sits before its last sub-step (whose fragments are already in
-  // registers): after it the next stage is visible to every wave (so its
-  // first fragments are read during the last MFMAs) and the current stage
-  // is no longer read by anyone (so the loads of K-step kt+2 refill it).
-  const int nk = p.K / (128 / ES);
-  constexpr int LAST = (KS - 1) & 1;  // fragment buffer of the last sub-step
-  issue_loads(0, 0);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (nk > 1) issue_loads(1, 1);
-  read_frags(smem, 0, 0);
-  for (int kt = 0; kt + 1 < nk; ++kt) {
-    const uint8_t* st = smem + (kt & 1) * STAGE;
-#pragma unroll
-    for (int kk = 0; kk < KS - 1; ++kk) {
-      read_frags(st, kk + 1, (kk & 1) ^ 1);
-      mfmas(kk & 1);
-      interleave();
-    }
-    __builtin_amdgcn_s_waitcnt(0);  // own loads of K-step kt+1 and fragment reads done
-    __syncthreads();
-    if (kt + 2 < nk) issue_loads(kt + 2, kt & 1);
-    read_frags(smem + ((kt + 1) & 1) * STAGE, 0, LAST ^ 1);
-    mfmas(LAST);
-    interleave();
-  }
-  {
-    const uint8_t* st = smem + ((nk - 1) & 1) * STAGE;
-#pragma unroll
-    for (int kk = 0; kk < KS - 1; ++kk) {
-      read_frags(st, kk + 1, (kk & 1) ^ 1);
-      mfmas(kk & 1);
-      interleave();
-    }
-    mfmas(LAST);
-  }
-  }
 
   __syncthreads();  // every wave is done reading the last stage
   nt_epilogue_staged<OUT, ACT, BM, BN, WM, WN, 2 * STAGE>(p, acc, smem, m0, n0);
@@ -1145,9 +1066,8 @@ Status run_nt(const GemmParams& g, hipStream_t s) {
 // epilogue (none, ReLU): four waves of 128 x 128, one per SIMD, which issue
 // the MFMAs back to back.  Everything else: eight waves of 128 x 64; the
 // GELU (two outputs) and dGELU (pre-activation read) epilogues move twice
-// the bytes per wave with four waves, f16's integer-rounded epilogue needs
-// the registers, and the M/N-contiguous loop waits for its loads once per
-// K-step, which the second wave on each SIMD covers.
+// the bytes per wave with four waves, and f16's integer-rounded epilogue
+// needs the registers.
 template <int IN, int OUT>
 Status run_nt256(const GemmParams& g, hipStream_t s) {
   if constexpr (IN == IN_BF16) {
