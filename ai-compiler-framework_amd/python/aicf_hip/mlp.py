@@ -117,9 +117,9 @@ def build_mlp_mse(B: int = 8192, D: int = 4096, L: int = 4, *, lr: float = 1e-3,
     """bf16 activations/weights, fp32 master parameters in one flat buffer.
     The GEMM kernel reads M/N-contiguous operands in place; StageD
     (nt_layout) may still insert explicit transposes: "cost" where a
-    transpose is cheaper than the in-place read (at the benchmark shape: the
-    weights of the dX GEMMs, not dZ / H of the dW GEMMs), True for every such
-    operand, False for none."""
+    transpose is cheaper than the in-place read (none at the measured
+    in-place cost of this kernel), True for every such operand, False for
+    none."""
     ir = IRGraph(name=f"mlp_mse_{B}x{D}x{L}")
     lay = FlatLayout(D, L)
     nv = lambda n, s, dt=F32, view=None: ir.new_value(name=n, shape=s, dtype=dt,  # noqa: E731

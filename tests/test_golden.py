@@ -144,12 +144,31 @@ def test_mlp_graph_without_stage_d_reads_operands_in_place():
     assert layouts == {(False, True): 4, (False, False): 4, (True, False): 4}
 
 
-def test_stage_d_cost_policy_transposes_only_the_weights():
-    """StageD "cost" at the benchmark shape: transposing a 4096^2 weight (32 MB)
-    is cheaper than the in-place penalty of its dX GEMM; transposing dZ or H
-    (64 MB each) is not, so the dW GEMMs read them in place."""
-    from aicf_hip import mlp
+def test_stage_d_cost_policy_reads_every_operand_in_place():
+    """StageD "cost" at the benchmark shape: the GEMM kernel reads
+    M/N-contiguous operands at the K-contiguous rate, so no transpose pays
+    for itself and the lowered step is the same as without StageD."""
+    from aicf_hip import lower, mlp
 
+    assert lower.MN_OPERAND_PENALTY == 0.0
+    ir, lowered, _ = mlp.build_mlp_mse(8192, 4096, 4, nt_layout="cost")
+    assert not [it for it in lowered if it["op"] == "transpose"]
+    layouts = {}
+    for it in lowered:
+        if it["op"] in ("gemm", "gemm_epilogue"):
+            a = it["attrs"]
+            key = (bool(a.get("transA", False)), bool(a.get("transB", False)))
+            layouts[key] = layouts.get(key, 0) + 1
+    assert layouts == {(False, True): 4, (False, False): 4, (True, False): 4}
+
+
+def test_stage_d_cost_policy_transposes_when_in_place_reads_cost_more(monkeypatch):
+    """With a 10% in-place penalty (the model's input, not a measurement of
+    this kernel), transposing a 4096^2 weight (32 MB) is cheaper than the
+    penalty of its dX GEMM, transposing dZ or H (64 MB each) is not."""
+    from aicf_hip import lower, mlp
+
+    monkeypatch.setattr(lower, "MN_OPERAND_PENALTY", 0.10)
     ir, lowered, _ = mlp.build_mlp_mse(8192, 4096, 4, nt_layout="cost")
     tr = [it for it in lowered if it["op"] == "transpose"]
     assert sorted(ir.values[it["inputs"][0]].name for it in tr) == [f"wb.{i}.W" for i in range(1, 5)]
