@@ -220,9 +220,8 @@ __device__ __forceinline__ floatx16 mfma32<IN_F16>(const uint16_t* a, const uint
 // Grouped raster: workgroup w of XCD x (dispatch order w*8+x) gets
 // tile (tm, tn) so that each XCD sweeps a contiguous run of tiles and
 // GROUP_M consecutive tile rows share B columns in its L2.
-__device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int& tm, int& tn) {
+__device__ __forceinline__ void tile_coords_of(int id, int tiles_m, int tiles_n, int& tm, int& tn) {
   const int total = tiles_m * tiles_n;
-  int id = blockIdx.x;
   // XCD-aware remap: hardware id i runs on XCD (i % 8); give every XCD a
   // contiguous range of logical ids.
   if ((total & 7) == 0) {
@@ -236,6 +235,9 @@ __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int& tm, i
   const int in_group = id % (GROUP_M * tiles_n);
   tm = first_m + in_group % gsize;
   tn = in_group / gsize;
+}
+__device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int& tm, int& tn) {
+  tile_coords_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
 }
 
 template <int IN, int OUT, int BM, int BN, int BK, int WM, int WN>
@@ -733,17 +735,12 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt_kernel(NTParams p) {
   constexpr int STAGE = A_BYTES + B_BYTES;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE];
 
-  int tm_i, tn_i;
-  tile_coords(p.tiles_m, p.tiles_n, tm_i, tn_i);
-  const int m0 = tm_i * BM, n0 = tn_i * BN;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / WN, wn = wave % WN;
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
-
+  int m0 = 0, n0 = 0;
   NTOperand<AKC, BM, NW, ES> opa;
   NTOperand<BKC, BN, NW, ES> opb;
-  nt_operand_init(opa, p.A, p.lda, m0, p.K, lane, wave);
-  nt_operand_init(opb, p.B, p.ldb, n0, p.K, lane, wave);
 
   // Load u of the wave for K-step kt into stage `stage`: 1 KB direct-to-LDS
   // block u (A blocks first).  With an M/N-contiguous operand the loads are
@@ -770,12 +767,6 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt_kernel(NTParams p) {
   };
 
   floatx16 acc[TN][TM];
-#pragma unroll
-  for (int i = 0; i < TN; ++i)
-#pragma unroll
-    for (int j = 0; j < TM; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
   // Fragment addresses.  K-contiguous: row offset of the lane's MN-row plus
   // the swizzled chunk of (sub-step, half).  MN-contiguous: the lane's K-row
@@ -894,6 +885,28 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt_kernel(NTParams p) {
   // spread over its first two sub-steps: issued all at once after the barrier
   // they back up the address queue and stall the MFMA issue, and issued in
   // the third sub-step they have too little time left before the next wait.
+  // Tiles: the grid covers all tiles (one per workgroup), or, persistent,
+  // one workgroup per CU loops over tiles blockIdx.x + q * gridDim.x, so that
+  // the global stores of a tile's epilogue drain while the next tile's loads
+  // and MFMAs run.  With a grid that is a multiple of 8, tile % 8 is the
+  // workgroup's XCD, as the remap in tile_coords_of assumes.
+  const int total_tiles = p.tiles_m * p.tiles_n;
+  for (int tile = blockIdx.x; tile < total_tiles; tile += gridDim.x) {
+  {
+    int tm_i, tn_i;
+    tile_coords_of(tile, p.tiles_m, p.tiles_n, tm_i, tn_i);
+    m0 = tm_i * BM;
+    n0 = tn_i * BN;
+  }
+  nt_operand_init(opa, p.A, p.lda, m0, p.K, lane, wave);
+  nt_operand_init(opb, p.B, p.ldb, n0, p.K, lane, wave);
+#pragma unroll
+  for (int i = 0; i < TN; ++i)
+#pragma unroll
+    for (int j = 0; j < TM; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
   const int nk = p.K / (128 / ES);
   constexpr int L1 = NVM / 2;  // loads in the first of the two sub-steps
   issue_loads(0, 0);
@@ -928,6 +941,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt_kernel(NTParams p) {
 
   __syncthreads();  // every wave is done reading the last stage
   nt_epilogue_staged<OUT, ACT, BM, BN, WM, WN, 2 * STAGE>(p, acc, smem, m0, n0);
+  __syncthreads();  // the staged tile is read out before the next tile's loads refill the stages
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1014,6 +1029,19 @@ Status run_cfg(GemmParams& p, hipStream_t s) {
   return launch_status("gemm_mfma");
 }
 
+// Compute units of the current device (cached per device; 0 if unknown).
+int device_cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 template <int IN, int OUT, int ACT, int BM, int BN, int WM, int WN, bool AKC, bool BKC>
 Status run_nt_act(const GemmParams& g, hipStream_t s) {
   NTParams p{};
@@ -1032,8 +1060,15 @@ Status run_nt_act(const GemmParams& g, hipStream_t s) {
   p.bias_f32 = g.bias_f32;
   p.tiles_m = p.M / BM;
   p.tiles_n = p.N / BN;
-  gemm_nt_kernel<IN, OUT, ACT, BM, BN, WM, WN, AKC, BKC>
-      <<<(unsigned)(p.tiles_m * p.tiles_n), 64 * WM * WN, 0, s>>>(p);
+  // 256 x 256 tiles hold one workgroup per CU: with more tiles than CUs,
+  // launch one persistent workgroup per CU (a multiple of 8, one per XCD
+  // slot) that loops over its tiles.
+  unsigned grid = (unsigned)(p.tiles_m * p.tiles_n);
+  if constexpr (BM == 256 && BN == 256) {
+    const int ncu = device_cu_count();
+    if (ncu > 0 && ncu % 8 == 0 && grid > (unsigned)ncu) grid = (unsigned)ncu;
+  }
+  gemm_nt_kernel<IN, OUT, ACT, BM, BN, WM, WN, AKC, BKC><<<grid, 64 * WM * WN, 0, s>>>(p);
   return launch_status("gemm_nt");
 }
 

@@ -330,20 +330,67 @@ struct RowReducer {
   }
 };
 
+// Statistics of a row segment, combined in one reduction round:
+//   m  maximum (and i, the first column holding it, for cross-entropy),
+//   s  sum of exp(x - m) over the segment (rescaled when segments merge),
+//   sx sum of x.
+// Merging is symmetric in its two arguments (max, tie-aware argmax, and
+// sums), so every lane of a butterfly ends with bit-identical statistics.
+struct RowStat {
+  float m, s, sx;
+  int i;
+};
+template <int MODE>
+__device__ __forceinline__ void stat_merge(RowStat& a, const RowStat& b) {
+  if constexpr (MODE == MODE_SUM) {
+    a.sx += b.sx;
+  } else if constexpr (MODE == MODE_MAX) {
+    a.m = fmaxf(a.m, b.m);
+  } else {
+    const float M = fmaxf(a.m, b.m);
+    const float x = a.m == M ? a.s : a.s * __expf(a.m - M);  // exact when this side holds the max
+    const float y = b.m == M ? b.s : b.s * __expf(b.m - M);
+    if constexpr (MODE == MODE_XENT) {
+      if (b.m > a.m || (b.m == a.m && b.i < a.i)) a.i = b.i;
+    } else {
+      a.sx += b.sx;
+    }
+    a.m = M;
+    a.s = x + y;
+  }
+}
+template <int MODE>
+__device__ __forceinline__ RowStat stat_shfl(const RowStat& v, int off) {
+  RowStat r;
+  r.m = __shfl_xor(v.m, off, 64);
+  r.s = __shfl_xor(v.s, off, 64);
+  r.sx = __shfl_xor(v.sx, off, 64);
+  r.i = MODE == MODE_XENT ? __shfl_xor(v.i, off, 64) : 0;
+  return r;
+}
+
 // Register-resident row kernel: row = LPR lanes x VPT float4.  Element j of
 // lane l, vector k sits at column (k * LPR + l) * 4 + j, so every vector load
-// of a lane group is one contiguous, coalesced segment.
+// of a lane group is one contiguous, coalesced segment.  Each lane reduces
+// its own values (exp taken against its own maximum), the lanes of a row
+// merge their statistics by butterfly, and the waves of a row (LPR > 64)
+// merge through LDS after one barrier, in a fixed order.  The outputs
+// then scale each lane's exponentials by exp(m_lane - M) / S.  A row whose
+// values are all equal gets exactly 1/C when C is a power of two (every
+// exponential and scale factor is then exactly 1 and S = C).
 template <int LPR, int VPT, int MODE>
 __global__ __launch_bounds__(LPR >= 256 ? LPR : 256) void row_reg_kernel(RowArgs a) {
-  constexpr int ROWS_PER_BLOCK = LPR >= 256 ? 1 : 256 / LPR;
-  constexpr int NW = LPR > 64 ? LPR / 64 : 1;
-  __shared__ float lds[NW > 1 ? NW : 1];
-  __shared__ int ilds[NW > 1 ? NW : 1];
-  const int sub = LPR >= 256 ? 0 : (int)threadIdx.x / LPR;
-  const int l = LPR >= 256 ? (int)threadIdx.x : (int)threadIdx.x % LPR;
-  const int64_t row = (int64_t)blockIdx.x * ROWS_PER_BLOCK + sub;
+  constexpr int THREADS = LPR >= 256 ? LPR : 256;
+  constexpr int RPB = THREADS / LPR;            // rows per workgroup
+  constexpr int NW = LPR > 64 ? LPR / 64 : 1;   // waves per row
+  constexpr int TW = THREADS / 64;              // waves per workgroup
+  constexpr int BF = LPR < 64 ? LPR : 64;       // butterfly width
+  __shared__ float lds_m[TW], lds_s[TW], lds_sx[TW];
+  __shared__ int lds_i[TW];
+  const int sub = (int)threadIdx.x / LPR;
+  const int l = (int)threadIdx.x % LPR;
+  const int64_t row = (int64_t)blockIdx.x * RPB + sub;
   const bool active = row < a.R;  // uniform across the lanes of a row
-  const RowReducer<LPR> rr{lds};
   const int64_t C = a.C;
   const f32x4* xr = reinterpret_cast<const f32x4*>(a.x + (active ? row : 0) * C);
 
@@ -356,99 +403,98 @@ __global__ __launch_bounds__(LPR >= 256 ? LPR : 256) void row_reg_kernel(RowArgs
       v[k] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  if constexpr (MODE == MODE_SUM) {
-    float s = 0.0f;
+  // this lane's statistics
+  RowStat st{v[0][0], 0.0f, 0.0f, l * 4};
+  if constexpr (MODE == MODE_SUM || MODE == MODE_SOFTMAX) {
 #pragma unroll
-    for (int k = 0; k < VPT; ++k) s += (v[k][0] + v[k][1]) + (v[k][2] + v[k][3]);
-    s = rr.sum(s);
-    if (active && l == 0) a.rsum[row] = s;
-    return;
+    for (int k = 0; k < VPT; ++k) st.sx += (v[k][0] + v[k][1]) + (v[k][2] + v[k][3]);
   }
-
-  float mx = v[0][0];
-#pragma unroll
-  for (int k = 0; k < VPT; ++k)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) mx = fmaxf(mx, v[k][j]);
-
-  if constexpr (MODE == MODE_MAX) {
-    mx = rr.max(mx);
-    if (active && l == 0) a.rmax[row] = mx;
-    return;
-  }
-
-  int amx_idx = 0;
   if constexpr (MODE == MODE_XENT) {
-    // first index of the lane's maximum, then a tie-aware reduction
-    float bv = v[0][0];
-    int bi = l * 4;
+#pragma unroll
+    for (int k = 0; k < VPT; ++k)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (v[k][j] > st.m) {
+          st.m = v[k][j];
+          st.i = (k * LPR + l) * 4 + j;
+        }
+  } else if constexpr (MODE != MODE_SUM) {
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) st.m = fmaxf(st.m, fmaxf(fmaxf(v[k][0], v[k][1]), fmaxf(v[k][2], v[k][3])));
+  }
+  const float m_lane = st.m;
+  if constexpr (MODE == MODE_SOFTMAX || MODE == MODE_XENT) {
+    const float mref = m_lane == -INFINITY ? 0.0f : m_lane;  // an all -inf lane contributes 0
 #pragma unroll
     for (int k = 0; k < VPT; ++k)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int col = (k * LPR + l) * 4 + j;
-        if (v[k][j] > bv) {
-          bv = v[k][j];
-          bi = col;
-        }
+        const float e = __expf(v[k][j] - mref);
+        v[k][j] = e;
+        st.s += e;
       }
-    rr.argmax(bv, bi, ilds);
-    mx = bv;
-    amx_idx = bi;
-  } else {
-    mx = rr.max(mx);
   }
 
-  float se = 0.0f, sx = 0.0f;
+  // merge over the row
 #pragma unroll
-  for (int k = 0; k < VPT; ++k)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if constexpr (MODE == MODE_SOFTMAX) sx += v[k][j];
-      const float e = __expf(v[k][j] - mx);
-      v[k][j] = e;
-      se += e;
+  for (int off = BF / 2; off > 0; off >>= 1) stat_merge<MODE>(st, stat_shfl<MODE>(st, off));
+  if constexpr (NW > 1) {
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+      lds_m[w] = st.m;
+      lds_s[w] = st.s;
+      lds_sx[w] = st.sx;
+      lds_i[w] = st.i;
     }
-  se = rr.sum(se);
-  if constexpr (MODE == MODE_SOFTMAX) {
-    if (a.rsum) sx = rr.sum(sx);
+    __syncthreads();
+    const int w0 = sub * NW;
+    st = RowStat{lds_m[w0], lds_s[w0], lds_sx[w0], lds_i[w0]};
+#pragma unroll
+    for (int k = 1; k < NW; ++k)
+      stat_merge<MODE>(st, RowStat{lds_m[w0 + k], lds_s[w0 + k], lds_sx[w0 + k], lds_i[w0 + k]});
   }
-  const float inv = 1.0f / se;
+  if (!active) return;
 
-  f32x4* yr = reinterpret_cast<f32x4*>(a.y + (active ? row : 0) * C);
+  if constexpr (MODE == MODE_SUM) {
+    if (l == 0) a.rsum[row] = st.sx;
+    return;
+  }
+  if constexpr (MODE == MODE_MAX) {
+    if (l == 0) a.rmax[row] = st.m;
+    return;
+  }
+  const float c = (m_lane == st.m ? 1.0f : __expf(m_lane - st.m)) / st.s;
+  f32x4* yr = reinterpret_cast<f32x4*>(a.y + row * C);
   if constexpr (MODE == MODE_SOFTMAX) {
-    if (!active) return;
 #pragma unroll
     for (int k = 0; k < VPT; ++k) {
       f32x4 o;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) o[j] = v[k][j] * inv;
+      for (int j = 0; j < 4; ++j) o[j] = v[k][j] * c;
       __builtin_nontemporal_store(o, yr + k * LPR + l);
     }
     if (l == 0) {
-      if (a.rmax) a.rmax[row] = mx;
-      if (a.rsum) a.rsum[row] = sx;
+      if (a.rmax) a.rmax[row] = st.m;
+      if (a.rsum) a.rsum[row] = st.sx;
     }
   } else {  // MODE_XENT
-    if (!active) return;
     const int lab = a.labels[row];
     const bool valid = lab >= 0 && (int64_t)lab < C;
-    const float s = a.inv_batch;
+    const float sc = a.inv_batch;
 #pragma unroll
     for (int k = 0; k < VPT; ++k) {
       f32x4 o;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int col = (k * LPR + l) * 4 + j;
-        const float p = v[k][j] * inv;
-        o[j] = (p - (col == lab ? 1.0f : 0.0f)) * s;
+        o[j] = (v[k][j] * c - (col == lab ? 1.0f : 0.0f)) * sc;
       }
-      yr[k * LPR + l] = o;
+      __builtin_nontemporal_store(o, yr + k * LPR + l);
     }
     if (l == 0) {
-      a.argmax[row] = amx_idx;
+      a.argmax[row] = st.i;
       // loss_i = log(sum exp(z - m)) + m - z[label]
-      a.row_loss[row] = valid ? (logf(se) + mx - a.x[row * C + lab]) : __builtin_nanf("");
+      a.row_loss[row] = valid ? (logf(st.s) + st.m - a.x[row * C + lab]) : __builtin_nanf("");
     }
   }
 }
@@ -552,15 +598,15 @@ Status launch_rows(const RowArgs& a, void* stream) {
     return launch_status("row_kernel");                                                      \
   }
   ROW_CASE(16, 1)     // C = 64
-  ROW_CASE(32, 1)     // C = 128
+  ROW_CASE(16, 2)     // C = 128
   ROW_CASE(32, 2)     // C = 256
   ROW_CASE(64, 2)     // C = 512
-  ROW_CASE(64, 4)     // C = 1024
-  ROW_CASE(64, 8)     // C = 2048
+  ROW_CASE(128, 2)    // C = 1024
+  ROW_CASE(128, 4)    // C = 2048
   ROW_CASE(256, 4)    // C = 4096
-  ROW_CASE(256, 8)    // C = 8192
+  ROW_CASE(512, 4)    // C = 8192
   ROW_CASE(512, 8)    // C = 16384
-  ROW_CASE(1024, 8)   // C = 32768
+  ROW_CASE(512, 16)   // C = 32768
 #undef ROW_CASE
   row_loop_kernel<MODE><<<(unsigned)R, 256, 0, s>>>(a);
   return launch_status("row_loop_kernel");

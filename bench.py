@@ -177,6 +177,126 @@ def bench_softmax(C, rows, cols, iters=20, warmup=3):
     return {"ms": ms, "gbs": nbytes / (ms * 1e-3) / 1e9, "bytes": nbytes, "buffer_sets": nsets}
 
 
+# ------------------------------------------------------------------ row reductions / losses
+RRED = int.from_bytes(b"RRED", "little")
+
+
+def _rotating_sets(make, per_set_bytes):
+    """Enough buffer sets that one pass over them exceeds the 256 MB MALL."""
+    nsets = max(1, min(64, math.ceil(512e6 / per_set_bytes)))
+    return [make() for _ in range(nsets)]
+
+
+def bench_rowreduce(C, rows, cols, op, iters=20, warmup=3):
+    """Row max (op 1) or row sum (op 0) of X [rows, cols] fp32: one read of X."""
+    import torch
+
+    g = torch.Generator(device="cuda")
+    g.manual_seed(4)
+    sets = _rotating_sets(lambda: (torch.randn((rows, cols), device="cuda", generator=g) * 2.0,
+                                   torch.empty(rows, device="cuda")), rows * cols * 4)
+    k = [0]
+    pay = struct.pack("<i", op)
+
+    def fn():
+        x, o = sets[k[0] % len(sets)]
+        k[0] += 1
+        C.op_call(int(C.OpKind.RowReduce), [x], [o], RRED, pay, 0)
+
+    ms = time_launches(fn, iters, warmup)
+    nbytes = 4 * rows * cols + 4 * rows
+    return {"ms": ms, "gbs": nbytes / (ms * 1e-3) / 1e9, "buffer_sets": len(sets)}
+
+
+def bench_xent(C, rows, cols, iters=20, warmup=3):
+    """Fused softmax cross-entropy forward + backward: logits [rows, cols] fp32
+    and int32 labels -> mean loss, dlogits, argmax, per-row loss."""
+    import torch
+
+    g = torch.Generator(device="cuda")
+    g.manual_seed(5)
+
+    def make():
+        z = torch.randn((rows, cols), device="cuda", generator=g) * 3.0
+        lab = torch.randint(0, cols, (rows,), device="cuda", generator=g, dtype=torch.int32)
+        return (z, lab, torch.empty((), device="cuda"), torch.empty_like(z),
+                torch.empty(rows, dtype=torch.int32, device="cuda"), torch.empty(rows, device="cuda"))
+
+    sets = _rotating_sets(make, rows * cols * 8)
+    k = [0]
+
+    def fn():
+        z, lab, loss, dz, am, rl = sets[k[0] % len(sets)]
+        k[0] += 1
+        C.op_call(int(C.OpKind.SoftmaxXent), [z, lab], [loss, dz, am, rl], 0, b"", 0)
+
+    ms = time_launches(fn, iters, warmup)
+    nbytes = 8 * rows * cols + 16 * rows  # logits in, dlogits out, labels, argmax, row loss (r+w)
+    return {"ms": ms, "gbs": nbytes / (ms * 1e-3) / 1e9, "buffer_sets": len(sets)}
+
+
+def bench_mse(C, rows, cols, iters=20, warmup=3):
+    """Fused MSE loss + gradient of the train step: bf16 prediction, fp32
+    target -> bf16 gradient and the mean loss (8 bytes per element)."""
+    import torch
+
+    g = torch.Generator(device="cuda")
+    g.manual_seed(6)
+
+    def make():
+        p = torch.randn((rows, cols), device="cuda", generator=g).to(torch.bfloat16)
+        t = torch.randn((rows, cols), device="cuda", generator=g)
+        return p, t, torch.empty_like(p), torch.empty((), device="cuda"), torch.empty(1024, device="cuda")
+
+    sets = _rotating_sets(make, rows * cols * 8)
+    k = [0]
+
+    def fn():
+        p, t, d, loss, part = sets[k[0] % len(sets)]
+        k[0] += 1
+        C.launch_by_id("mse_loss_grad_v0", C.OpKind.MseGrad, [p, t], [d, loss, part])
+
+    ms = time_launches(fn, iters, warmup)
+    nbytes = 8 * rows * cols
+    return {"ms": ms, "gbs": nbytes / (ms * 1e-3) / 1e9, "buffer_sets": len(sets)}
+
+
+def bench_colsum(C, rows, cols, iters=20, warmup=3):
+    """Bias gradient of the train step: column sum of dY [rows, cols] bf16 ->
+    fp32 [cols] (2 bytes per element read), with the [64, cols] partials
+    buffer the lowered step passes (two passes: 64 row slices, then their
+    fixed-order sum)."""
+    import torch
+
+    g = torch.Generator(device="cuda")
+    g.manual_seed(7)
+    sets = _rotating_sets(lambda: (torch.randn((rows, cols), device="cuda", generator=g).to(torch.bfloat16),
+                                   torch.empty(cols, device="cuda"), torch.empty((64, cols), device="cuda")),
+                          rows * cols * 2)
+    k = [0]
+
+    def fn():
+        x, o, part = sets[k[0] % len(sets)]
+        k[0] += 1
+        C.launch_by_id("reduce_sum_keep_lastdim_bf16_to_f32_v0", C.OpKind.ReduceSum, [x], [o, part])
+
+    ms = time_launches(fn, iters, warmup)
+    nbytes = 2 * rows * cols + 4 * cols
+    return {"ms": ms, "gbs": nbytes / (ms * 1e-3) / 1e9, "buffer_sets": len(sets)}
+
+
+def bench_torch_matmul(M, N, K, iters=20, warmup=5):
+    """The vendor library on the same box (torch.matmul -> hipBLASLt), bf16
+    X[M,K] . W[N,K]^T, as a reference line for the GEMM kernel."""
+    import torch
+
+    X = torch.randn((M, K), device="cuda").to(torch.bfloat16)
+    W = torch.randn((N, K), device="cuda").to(torch.bfloat16)
+    Y = torch.empty((M, N), device="cuda", dtype=torch.bfloat16)
+    ms = time_launches(lambda: torch.matmul(X, W.t(), out=Y), iters, warmup)
+    return {"ms": ms, "tflops": 2.0 * M * N * K / (ms * 1e-3) / 1e12}
+
+
 # ------------------------------------------------------------------ Adam
 def bench_adam(C, n=1 << 28, steps=10):
     """Fused AdamW over a flat fp32 buffer, t = 1..steps, in place."""
@@ -307,10 +427,50 @@ def roofline_only(C, B, D, launches):
     log(f"[bench] roofline-only: {launches + 1} gemm launches, 3 calibration copies; {g}")
 
 
-def pmc_report(fetch_csv, write_csv):
+def mfma_report(counter_csv, trace_csv, pattern):
+    """MFMA utilisation and effective clock of the dispatches whose kernel
+    name contains `pattern`, from one rocprofv3 run with --pmc
+    SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE SQ_INSTS_VALU_MFMA_MOPS_BF16 and
+    --kernel-trace.  SQ_VALU_MFMA_BUSY_CYCLES is summed over the 1024 SIMDs,
+    GRBM_GUI_ACTIVE over the 8 XCDs (cycles of each XCD's clock)."""
+    import csv
+    from collections import defaultdict
+
+    cnt = defaultdict(lambda: defaultdict(float))
+    names = {}
+    with open(counter_csv, newline="") as f:
+        for row in csv.DictReader(f):
+            d = int(row["Dispatch_Id"])
+            cnt[d][row["Counter_Name"]] += float(row["Counter_Value"])
+            names[d] = row.get("Kernel_Name", "")
+    dur = {}
+    with open(trace_csv, newline="") as f:
+        for row in csv.DictReader(f):
+            dur[int(row["Dispatch_Id"])] = (int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) * 1e-9
+    rows = []
+    for d in sorted(cnt):
+        if pattern not in names[d] or d not in dur:
+            continue
+        c = cnt[d]
+        gui = c["GRBM_GUI_ACTIVE"] / 8.0
+        flop = c["SQ_INSTS_VALU_MFMA_MOPS_BF16"] * 512.0
+        rows.append((d, dur[d], gui / dur[d] / 1e9, c["SQ_VALU_MFMA_BUSY_CYCLES"] / (gui * 1024.0),
+                     flop / dur[d] / 1e12))
+    lines = [f"| dispatch | us | clock GHz | MFMA busy | TFLOP/s |", "|---:|---:|---:|---:|---:|"]
+    for d, t, clk, util, tf in rows:
+        lines.append(f"| {d} | {t * 1e6:.1f} | {clk:.2f} | {util * 100:.1f}% | {tf:.0f} |")
+    if rows:
+        n = len(rows)
+        lines.append(f"| mean | {sum(r[1] for r in rows) / n * 1e6:.1f} | {sum(r[2] for r in rows) / n:.2f} | "
+                     f"{sum(r[3] for r in rows) / n * 100:.1f}% | {sum(r[4] for r in rows) / n:.0f} |")
+    return lines
+
+
+def pmc_report(fetch_csv, write_csv, mfma_csv=None, trace_csv=None):
     """Markdown summary of two rocprofv3 --pmc runs of --roofline-only
     (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch).  Each counter is scaled
-    by calibration copy's expected/measured ratio."""
+    by calibration copy's expected/measured ratio.  With the MFMA counter run
+    and its kernel trace, also the MFMA utilisation and clock per dispatch."""
     import csv
     from statistics import mean
 
@@ -340,7 +500,8 @@ def pmc_report(fetch_csv, write_csv):
         "python3 bench.py --roofline-only",
         "rocprofv3 --pmc WRITE_SIZE --output-format csv -d gpurun_out/pmc_write -o run -- "
         "python3 bench.py --roofline-only",
-        "python3 bench.py --pmc-report <fetch counter_collection.csv> <write counter_collection.csv>",
+        "python3 bench.py --pmc-report <fetch counter_collection.csv> <write counter_collection.csv> "
+        "<mfma counter_collection.csv> <mfma kernel_trace.csv>",
         "```",
         "",
         f"calibration copy (copy_bf16_v0, {CALIB_KIB:.0f} KiB read + written): "
@@ -354,6 +515,196 @@ def pmc_report(fetch_csv, write_csv):
         f"traffic_bytes_per_launch: {int(round(fetch_b + write_b))}",
         "",
     ]
+    if mfma_csv and trace_csv:
+        lines += [
+            "## MFMA utilisation and clock of the same GEMM",
+            "",
+            "```",
+            "rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE SQ_INSTS_VALU_MFMA_MOPS_BF16 "
+            "--kernel-trace --output-format csv -d gpurun_out/pmc_mfma -o run -- python3 bench.py "
+            "--roofline-only",
+            "```",
+            "",
+            "MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE per XCD x 1024 SIMDs); clock = "
+            "GRBM_GUI_ACTIVE per XCD / kernel duration; TFLOP/s from SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512.",
+            "",
+        ] + mfma_report(mfma_csv, trace_csv, "gemm_nt") + [""]
+    print("\n".join(lines))
+
+
+# Streaming kernels profiled by --streaming-only: (label, kernel-name pattern,
+# algorithmic bytes per dispatch).  Shapes follow the benchmark configs.
+SR, SC = 16384, 32768
+STREAMING = [
+    ("row softmax (+max, +sum) 16384x32768 f32", "row_reg_kernel<512, 16, 0>", 8 * SR * SC + 8 * SR),
+    ("row sum 16384x32768 f32", "row_reg_kernel<512, 16, 1>", 4 * SR * SC + 4 * SR),
+    ("row max 16384x32768 f32", "row_reg_kernel<512, 16, 2>", 4 * SR * SC + 4 * SR),
+    ("softmax xent fwd+bwd 16384x8192 f32", "row_reg_kernel<512, 4, 3>", 8 * SR * 8192 + 16 * SR),
+    ("mse loss+grad 8192x4096 (bf16 p, f32 t, bf16 grad)", "mse_loss_grad_pass1", 8 * 8192 * 4096),
+    ("bias grad colsum 8192x4096 bf16 -> f32", "colsum_vec_kernel", 2 * 8192 * 4096 + 4 * 4096),
+    ("AdamW 2^28 f32 (P,G,M,V in; P,M,V out)", "adamw_vec4_kernel", 28 * (1 << 28)),
+]
+
+
+def streaming_only(C):
+    """Each streaming kernel of the benchmark three times at its benchmark
+    shape, then three calibration copies; the program profiled by the
+    FETCH_SIZE / WRITE_SIZE passes of the streaming traffic summary."""
+    import torch
+
+    g = torch.Generator(device="cuda")
+    g.manual_seed(8)
+    x = torch.randn((SR, SC), device="cuda", generator=g) * 2.0
+    y = torch.empty_like(x)
+    mx, sm = torch.empty(SR, device="cuda"), torch.empty(SR, device="cuda")
+    for _ in range(3):
+        C.op_call(int(C.OpKind.RowSoftmax), [x], [y, mx, sm], 0, b"", 0)
+    for op in (0, 1):
+        for _ in range(3):
+            C.op_call(int(C.OpKind.RowReduce), [x], [mx], RRED, struct.pack("<i", op), 0)
+    del x, y
+    z = torch.randn((SR, 8192), device="cuda", generator=g) * 3.0
+    lab = torch.randint(0, 8192, (SR,), device="cuda", generator=g, dtype=torch.int32)
+    loss, dz = torch.empty((), device="cuda"), torch.empty_like(z)
+    am, rl = torch.empty(SR, dtype=torch.int32, device="cuda"), torch.empty(SR, device="cuda")
+    for _ in range(3):
+        C.op_call(int(C.OpKind.SoftmaxXent), [z, lab], [loss, dz, am, rl], 0, b"", 0)
+    del z, dz
+    pb = torch.randn((8192, 4096), device="cuda", generator=g).to(torch.bfloat16)
+    t = torch.randn((8192, 4096), device="cuda", generator=g)
+    d, part = torch.empty_like(pb), torch.empty(1024, device="cuda")
+    for _ in range(3):
+        C.launch_by_id("mse_loss_grad_v0", C.OpKind.MseGrad, [pb, t], [d, loss, part])
+    o, opart = torch.empty(4096, device="cuda"), torch.empty((64, 4096), device="cuda")
+    for _ in range(3):
+        C.launch_by_id("reduce_sum_keep_lastdim_bf16_to_f32_v0", C.OpKind.ReduceSum, [d], [o, opart])
+    del pb, t, d
+    n = 1 << 28
+    P = torch.randn(n, device="cuda", generator=g) * 0.02
+    G = torch.randn(n, device="cuda", generator=g) * 1e-3
+    M, V = torch.zeros(n, device="cuda"), torch.zeros(n, device="cuda")
+    step = torch.zeros((), dtype=torch.int32, device="cuda")
+    pay = struct.pack("<fffff", 1e-3, 0.9, 0.999, 1e-8, 0.01)
+    for _ in range(3):
+        C.launch_by_id("step_inc_v0", C.OpKind.StepInc, [step], [step])
+        C.launch_by_id("adamw_step_f32_v1", C.OpKind.AdamStep, [P, G, M, V, step], [P, M, V], ADAM, pay)
+    del P, G, M, V
+    xc = torch.ones(CALIB_ELEMS, device="cuda", dtype=torch.bfloat16)
+    yc = torch.empty_like(xc)
+    for _ in range(3):
+        C.launch_by_id("copy_bf16_v0", C.OpKind.Copy, [xc], [yc], 0, b"")
+    torch.cuda.synchronize()
+    log("[bench] streaming-only: 7 kernels x 3 dispatches, 3 calibration copies")
+
+
+def pmc_streaming_report(fetch_csv, write_csv):
+    """Markdown summary of two rocprofv3 --pmc runs of --streaming-only:
+    HBM bytes per dispatch of each streaming kernel (calibrated like the GEMM
+    summary) against its algorithmic bytes."""
+    import csv
+    from collections import defaultdict
+    from statistics import mean
+
+    def per_kernel(path, counter):
+        vals = defaultdict(list)
+        with open(path, newline="") as f:
+            for row in csv.DictReader(f):
+                if row.get("Counter_Name") != counter:
+                    continue
+                name = row.get("Kernel_Name", "")
+                for label, pat, _ in STREAMING:
+                    if pat in name:
+                        vals[label].append(float(row["Counter_Value"]))
+                if "map1" in name:
+                    vals["copy"].append(float(row["Counter_Value"]))
+        return vals
+
+    fe, wr = per_kernel(fetch_csv, "FETCH_SIZE"), per_kernel(write_csv, "WRITE_SIZE")
+    f_r = CALIB_KIB / mean(fe["copy"])
+    f_w = CALIB_KIB / mean(wr["copy"])
+    lines = [
+        "# HBM traffic of the streaming kernels (one dispatch each, benchmark shapes)",
+        "",
+        "Commands (GPU box, repo root):",
+        "```",
+        "rocprofv3 --pmc FETCH_SIZE --output-format csv -d gpurun_out/pmc_sfetch -o run -- "
+        "python3 bench.py --streaming-only",
+        "rocprofv3 --pmc WRITE_SIZE --output-format csv -d gpurun_out/pmc_swrite -o run -- "
+        "python3 bench.py --streaming-only",
+        "python3 bench.py --pmc-streaming-report <fetch counter_collection.csv> "
+        "<write counter_collection.csv>",
+        "```",
+        "",
+        f"calibration copy (copy_bf16_v0, {CALIB_KIB:.0f} KiB read + written): FETCH_SIZE "
+        f"{mean(fe['copy']):.0f} KiB -> factor {f_r:.4f}; WRITE_SIZE {mean(wr['copy']):.0f} KiB -> "
+        f"factor {f_w:.4f}",
+        "",
+        "| kernel | algorithmic MB | HBM read MB | HBM write MB | HBM / algorithmic |",
+        "|---|---:|---:|---:|---:|",
+    ]
+    for label, _, alg in STREAMING:
+        if not fe.get(label) or not wr.get(label):
+            lines.append(f"| {label} | {alg / 1e6:.1f} | n/a | n/a | n/a |")
+            continue
+        rb = mean(fe[label]) * f_r * 1024
+        wb = mean(wr[label]) * f_w * 1024
+        lines.append(f"| {label} | {alg / 1e6:.1f} | {rb / 1e6:.1f} | {wb / 1e6:.1f} | "
+                     f"{(rb + wb) / alg:.3f} |")
+    lines.append("")
+    print("\n".join(lines))
+
+
+def stats_report(stats_csv, trace_csv, steps):
+    """Markdown summary of `rocprofv3 --kernel-trace --stats` over
+    `bench.py --steps N --no-cpu --no-components`: per-kernel totals, and the
+    launches of the replayed step (those between the first and the last
+    replay) grouped per step."""
+    import csv
+
+    with open(stats_csv, newline="") as f:
+        stats = list(csv.DictReader(f))
+    with open(trace_csv, newline="") as f:
+        trace = sorted(csv.DictReader(f), key=lambda r: int(r["Start_Timestamp"]))
+    short = lambda n: n.replace("aicf::hip::(anonymous namespace)::", "").split("(")[0][:80]  # noqa: E731
+    lines = [
+        "# Kernel time summary: bf16 MLP train step (hipGraph replay) + roofline GEMM",
+        "",
+        "Command (repo root, one MI355X):",
+        "",
+        "```",
+        f"rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/prof -o bench -- "
+        f"python3 -u bench.py --steps {steps} --no-cpu --no-components",
+        "python3 bench.py --stats-report gpurun_out/prof/bench_kernel_stats.csv "
+        f"gpurun_out/prof/bench_kernel_trace.csv {steps}",
+        "```",
+        "",
+        f"Process contents: warmup + {steps} timed replays of the captured step (batch 8192, 4 x 4096^2, "
+        "GELU, MSE, AdamW), then 23 launches of the forward bias+GELU GEMM for the roofline figure.",
+        "`gemm_nt_kernel<IN, OUT, ACT, BM, BN, WM, WN, AKC, BKC>`: IN 2 = bf16; OUT 2 = bf16, 0 = fp32; "
+        "ACT 0 none, 2 GELU (+ pre-activation store), 3 dGELU; WM x WN waves; AKC/BKC operand "
+        "K-contiguous (false: M/N-contiguous, read in place through transposing LDS reads).",
+        "",
+        "| kernel | calls | avg us | % time |",
+        "|---|---:|---:|---:|",
+    ]
+    for r in stats[:16]:
+        lines.append(f"| `{short(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
+                     f"{float(r['Percentage']):.2f} |")
+    # one replayed step = the kernels between two adamw launches (AdamW ends the step)
+    ends = [i for i, r in enumerate(trace) if "adamw" in r["Kernel_Name"]]
+    if len(ends) >= 3:
+        a, b = ends[-2] + 1, ends[-1] + 1
+        step = trace[a:b]
+        t0 = int(step[0]["Start_Timestamp"])
+        t1 = int(step[-1]["End_Timestamp"])
+        busy = sum(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in step)
+        lines += ["", f"Last replayed step, launch by launch ({len(step)} kernels, first start to last end "
+                  f"{(t1 - t0) / 1e3:.1f} us, kernels busy {busy / 1e3:.1f} us):", "",
+                  "| # | kernel | us |", "|---:|---|---:|"]
+        for i, r in enumerate(step):
+            lines.append(f"| {i} | `{short(r['Kernel_Name'])}` | "
+                         f"{(int(r['End_Timestamp']) - int(r['Start_Timestamp'])) / 1e3:.1f} |")
+    lines.append("")
     print("\n".join(lines))
 
 
@@ -381,11 +732,24 @@ def main():
     ap.add_argument("--cpu-rows", type=int, default=8)
     ap.add_argument("--roofline-only", action="store_true",
                     help="run only the roofline GEMM and a calibration copy (for rocprofv3 --pmc)")
-    ap.add_argument("--pmc-report", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
-                    help="summarise two rocprofv3 --pmc CSVs of --roofline-only and exit")
+    ap.add_argument("--pmc-report", nargs="+", metavar="CSV",
+                    help="summarise rocprofv3 --pmc CSVs of --roofline-only (FETCH, WRITE "
+                         "[, MFMA counters, kernel trace]) and exit")
+    ap.add_argument("--stats-report", nargs=3, metavar=("STATS_CSV", "TRACE_CSV", "STEPS"),
+                    help="summarise a rocprofv3 --kernel-trace --stats run of the step and exit")
+    ap.add_argument("--streaming-only", action="store_true",
+                    help="run each streaming kernel at its benchmark shape (for rocprofv3 --pmc)")
+    ap.add_argument("--pmc-streaming-report", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="summarise two rocprofv3 --pmc CSVs of --streaming-only and exit")
     args = ap.parse_args()
     if args.pmc_report:
         pmc_report(*args.pmc_report)
+        return
+    if args.stats_report:
+        stats_report(args.stats_report[0], args.stats_report[1], int(args.stats_report[2]))
+        return
+    if args.pmc_streaming_report:
+        pmc_streaming_report(*args.pmc_streaming_report)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); multi-GPU runs are not "
@@ -401,6 +765,9 @@ def main():
     log(f"[bench] device={torch.cuda.get_device_name(0)} mlp B={B} D={D} L={L}")
     if args.roofline_only:
         roofline_only(C, B, D, 5)
+        return
+    if args.streaming_only:
+        streaming_only(C)
         return
 
     res = bench_mlp(B, D, L, args.steps, args.warmup)
@@ -431,10 +798,46 @@ def main():
                                               "ms": round(sm["ms"], 5),
                                               "buffer_sets": sm["buffer_sets"]}
             log(f"[bench] softmax {cols} {sm}")
+        for cols in (1024, 8192, 32768):
+            for name, op in (("rowmax", 1), ("rowsum", 0)):
+                rr = bench_rowreduce(C, 16384, cols, op)
+                comps[f"{name}_16384x{cols}"] = {"value": round(rr["gbs"], 1), "unit": "GB/s",
+                                                 "frac": round(rr["gbs"] / PEAK_HBM_GBS, 4),
+                                                 "ms": round(rr["ms"], 5), "buffer_sets": rr["buffer_sets"]}
+                log(f"[bench] {name} {cols} {rr}")
+        xe = bench_xent(C, 16384, 8192)
+        comps["softmax_xent_fwd_bwd_16384x8192"] = {"value": round(xe["gbs"], 1), "unit": "GB/s",
+                                                    "frac": round(xe["gbs"] / PEAK_HBM_GBS, 4),
+                                                    "ms": round(xe["ms"], 5)}
+        log(f"[bench] xent {xe}")
+        ms_ = bench_mse(C, B, D)
+        comps[f"mse_loss_grad_bf16_{B}x{D}"] = {"value": round(ms_["gbs"], 1), "unit": "GB/s",
+                                                "frac": round(ms_["gbs"] / PEAK_HBM_GBS, 4),
+                                                "ms": round(ms_["ms"], 5)}
+        log(f"[bench] mse {ms_}")
+        cs = bench_colsum(C, B, D)
+        comps[f"colsum_bf16_f32_{B}x{D}"] = {"value": round(cs["gbs"], 1), "unit": "GB/s",
+                                             "frac": round(cs["gbs"] / PEAK_HBM_GBS, 4),
+                                             "ms": round(cs["ms"], 5)}
+        log(f"[bench] colsum {cs}")
         ad = bench_adam(C)
         comps["adamw_2^28"] = {"value": round(ad["gbs"], 1), "unit": "GB/s",
                                "frac": round(ad["gbs"] / PEAK_HBM_GBS, 4), "ms": round(ad["ms"], 4)}
         log(f"[bench] adam {ad}")
+        for (M_, N_, K_) in ((8192, 8192, 8192), (B, D, D)):
+            tm = bench_torch_matmul(M_, N_, K_)
+            comps[f"vendor_hipblaslt_bf16_{M_}x{N_}x{K_}"] = {
+                "value": round(tm["tflops"], 2), "unit": "TFLOP/s",
+                "frac": round(tm["tflops"] / PEAK_BF16_TFLOPS, 4), "ms": round(tm["ms"], 4),
+                "note": "torch.matmul (hipBLASLt) in the same process, reference line only"}
+            log(f"[bench] torch.matmul {M_}x{N_}x{K_} {tm}")
+        nd = bench_mlp(B, D, L, args.steps, args.warmup, dead_dx=False)
+        comps["mlp_step_without_dead_input_dx"] = {
+            "value": round(nd["steps_per_s"], 3), "unit": "steps/s", "ms": round(nd["ms"], 4),
+            "gemms_per_step": nd["gemms"],
+            "note": "same step with the first layer's input gradient (never consumed) removed; "
+                    "the headline keeps it, as the reference's lowering emits it"}
+        log(f"[bench] mlp without dead dX {nd}")
         c1 = bench_c1()
         comps["c1_mlp_fp32_64x784x256x10_step"] = c1
         log(f"[bench] c1 {c1}")

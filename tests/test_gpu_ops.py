@@ -306,9 +306,13 @@ def test_reduce_sum_columns(C):
     assert orc.rel_err(h(o1), ref) < 1e-5
 
 
-@pytest.mark.parametrize("cols", [128, 1024, 8192, 32768, 1000, 64, 2048, 4096])
-def test_row_softmax_and_stats(C, cols):
-    rows = 64 if cols <= 8192 else 16
+@pytest.mark.parametrize("cols,rows", [(128, 64), (1024, 64), (8192, 64), (32768, 16), (1000, 64), (64, 64),
+                                       (2048, 64), (4096, 64), (256, 37), (128, 37), (1024, 37), (512, 5),
+                                       (16384, 3)])
+def test_row_softmax_and_stats(C, cols, rows):
+    """Register-resident shapes (one row per lane group, wave or workgroup,
+    including partial workgroups: 37 rows at 16 rows per workgroup) and the
+    looping kernel (C = 1000)."""
     x = (2.0 * rng(cols).standard_normal((rows, cols))).astype(np.float32)  # N(0, 4)
     x[-1, :] = -1e4
     y = torch.empty((rows, cols), device="cuda")
@@ -333,11 +337,14 @@ def test_row_softmax_and_stats(C, cols):
     assert orc.rel_err(h(y), ry) < 1e-5
 
 
-@pytest.mark.parametrize("B,Ccls", [(64, 10), (64, 1024), (37, 1000), (256, 128)])
+@pytest.mark.parametrize("B,Ccls", [(64, 10), (64, 1024), (37, 1000), (256, 128), (37, 128), (9, 8192),
+                                    (5, 32768)])
 def test_softmax_xent(C, B, Ccls):
     r = rng(B * Ccls)
     z = (3 * r.standard_normal((B, Ccls))).astype(np.float32)
     z[1, 3] = z[1, 5] = z[1].max() + 2.0  # tie -> first index
+    if Ccls >= 512:  # tie between columns held by different waves of the row
+        z[2, 300] = z[2, 7] = z[2].max() + 3.0
     lab = r.integers(0, Ccls, B).astype(np.int32)
     loss = torch.empty((), device="cuda")
     dz = torch.empty((B, Ccls), device="cuda")
@@ -347,6 +354,8 @@ def test_softmax_xent(C, B, Ccls):
     rloss, rdz, ram, rrl = orc.softmax_xent_f64(z, lab)
     assert np.array_equal(h(am), ram)
     assert h(am)[1] == 3
+    if Ccls >= 512:
+        assert h(am)[2] == 7
     assert abs(loss.item() - rloss) / abs(rloss) < 1e-5
     assert orc.rel_err(h(dz), rdz) < 1e-5
     assert orc.rel_err(h(rl), rrl) < 1e-5
@@ -472,6 +481,40 @@ def test_gemm_bf16_dgelu_with_mn_contiguous_weight_256_tiles(C):
     ref = _gemm_ref(orc.bf16_bits_to_f32(dY).reshape(M, K), orc.bf16_bits_to_f32(W).reshape(K, N),
                     False, False) * orc.gelu_grad_f64(orc.bf16_bits_to_f32(Z).reshape(M, N).astype(np.float64))
     assert orc.rel_err(orc.bf16_bits_to_f32(h(dz)).reshape(M, N), ref) < 1e-2
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 1), (1, 0), (0, 0), (1, 1)])
+def test_gemm_bf16_persistent_tiles(C, ta, tb):
+    """More 256x256 tiles (17 x 16 = 272) than CUs: one persistent workgroup
+    per CU loops over its tiles, 16 of them take a second tile.  All operand
+    layouts (fp32 output at 1e-5), bias+GELU with the pre-activation, and
+    dGELU epilogues."""
+    M, N, K = 17 * 256, 16 * 256, 128
+    r = rng(300 + 2 * ta + tb)
+    s = 1.0 / np.sqrt(K)
+    A = r.uniform(-1, 1, (K, M) if ta else (M, K)).astype(np.float32)
+    B = r.uniform(-s, s, (N, K) if tb else (K, N)).astype(np.float32)
+    Ab, Bb = orc.bf16_bits_from_f32(A), orc.bf16_bits_from_f32(B)
+    Af, Bf = orc.bf16_bits_to_f32(Ab).reshape(A.shape), orc.bf16_bits_to_f32(Bb).reshape(B.shape)
+    ref = _gemm_ref(Af, Bf, ta, tb)
+    ga, gb = g(Ab, torch.bfloat16), g(Bb, torch.bfloat16)
+    of = torch.empty((M, N), device="cuda")
+    C.launch_by_id("gemm_bf16_mfma_f32out_v0", C.OpKind.Gemm, [ga, gb], [of], 0, struct.pack("<ii", ta, tb))
+    assert orc.rel_err(h(of), ref) < 1e-5
+    bias = r.uniform(-s, s, N).astype(np.float32)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    z = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    C.launch_by_id("gemm_epilogue_bf16_mfma_v0", C.OpKind.GemmEpilogue, [ga, gb, g(bias)], [y, z], GEPI,
+                   struct.pack("<iii", ta, tb, 3))
+    z_ref = ref + bias[None, :]
+    assert orc.rel_err(orc.bf16_bits_to_f32(h(z)).reshape(M, N), z_ref) < 1e-2
+    assert orc.rel_err(orc.bf16_bits_to_f32(h(y)).reshape(M, N), orc.gelu_f64(z_ref)) < 1e-2
+    Zb = orc.bf16_bits_from_f32(r.standard_normal((M, N)).astype(np.float32))
+    dz = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    C.launch_by_id("gemm_epilogue_bf16_mfma_v0", C.OpKind.GemmEpilogue, [ga, gb, g(Zb, torch.bfloat16)], [dz],
+                   GEPI, struct.pack("<iii", ta, tb, 5))
+    d_ref = ref * orc.gelu_grad_f64(orc.bf16_bits_to_f32(Zb).reshape(M, N).astype(np.float64))
+    assert orc.rel_err(orc.bf16_bits_to_f32(h(dz)).reshape(M, N), d_ref) < 1e-2
 
 
 @pytest.mark.parametrize("M,N,K", [(256, 256, 96), (512, 384, 160), (2048, 1024, 96), (4096, 4096, 64)])
