@@ -724,6 +724,15 @@ __device__ __forceinline__ void nt_operand_init(NTOperand<KC, BMN, NW, ES>& o, c
   }
 }
 
+// Persistent tiles (one workgroup per CU looping over tiles) for the 8-wave
+// 256 x 256 configuration; the 4-wave one keeps one tile per workgroup: its
+// 256 accumulators per lane leave no room for the registers that a tile loop
+// carries through the epilogue (they spill to scratch and cost more than the
+// overlap gains).
+constexpr bool nt_persistent(int BM, int BN, int WM, int WN) {
+  return BM == 256 && BN == 256 && WM * WN == 8;
+}
+
 template <int IN, int OUT, int ACT, int BM, int BN, int WM, int WN, bool AKC, bool BKC>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_nt_kernel(NTParams p) {
   constexpr int ES = IN == IN_F32 ? 4 : 2;  // element bytes
@@ -891,6 +900,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt_kernel(NTParams p) {
   // and MFMAs run.  With a grid that is a multiple of 8, tile % 8 is the
   // workgroup's XCD, as the remap in tile_coords_of assumes.
   const int total_tiles = p.tiles_m * p.tiles_n;
+  constexpr bool PERSIST = nt_persistent(BM, BN, WM, WN);
   for (int tile = blockIdx.x; tile < total_tiles; tile += gridDim.x) {
   {
     int tm_i, tn_i;
@@ -941,6 +951,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt_kernel(NTParams p) {
 
   __syncthreads();  // every wave is done reading the last stage
   nt_epilogue_staged<OUT, ACT, BM, BN, WM, WN, 2 * STAGE>(p, acc, smem, m0, n0);
+  if constexpr (!PERSIST) break;  // one tile per workgroup: no loop-carried registers
   __syncthreads();  // the staged tile is read out before the next tile's loads refill the stages
   }
 }
@@ -1060,11 +1071,11 @@ Status run_nt_act(const GemmParams& g, hipStream_t s) {
   p.bias_f32 = g.bias_f32;
   p.tiles_m = p.M / BM;
   p.tiles_n = p.N / BN;
-  // 256 x 256 tiles hold one workgroup per CU: with more tiles than CUs,
-  // launch one persistent workgroup per CU (a multiple of 8, one per XCD
-  // slot) that loops over its tiles.
+  // 256 x 256 tiles hold one workgroup per CU: with more tiles than CUs, the
+  // persistent configuration launches one workgroup per CU (a multiple of 8,
+  // one per XCD slot) that loops over its tiles.
   unsigned grid = (unsigned)(p.tiles_m * p.tiles_n);
-  if constexpr (BM == 256 && BN == 256) {
+  if constexpr (nt_persistent(BM, BN, WM, WN)) {
     const int ncu = device_cu_count();
     if (ncu > 0 && ncu % 8 == 0 && grid > (unsigned)ncu) grid = (unsigned)ncu;
   }

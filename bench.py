@@ -466,6 +466,103 @@ def mfma_report(counter_csv, trace_csv, pattern):
     return lines
 
 
+def vendor_compare(C):
+    """Our bf16 GEMM and torch.matmul (hipBLASLt) on the same operands:
+    8192^3 NT, the step's 8192x4096x4096 NT, and the step's dW layout
+    (dZ^T . H, K = 8192; ours writes fp32, hipBLASLt bf16).  Per shape, four
+    alternating groups of 5 launches (ours, vendor, ours, vendor), so that
+    neither library always runs on a cooler or hotter part.  The program
+    profiled for the MFMA comparison."""
+    import torch
+
+    g = torch.Generator(device="cuda")
+    g.manual_seed(9)
+
+    def alternate(ours, vendor):
+        for _ in range(2):
+            for fn in (ours, vendor):
+                for _ in range(5):
+                    fn()
+
+    for (M, N, K) in ((8192, 8192, 8192), (8192, 4096, 4096)):
+        X = torch.randn((M, K), device="cuda", generator=g).to(torch.bfloat16)
+        W = torch.randn((N, K), device="cuda", generator=g).to(torch.bfloat16)
+        Y = torch.empty((M, N), device="cuda", dtype=torch.bfloat16)
+        alternate(lambda: C.launch_by_id("gemm_bf16_mfma_v0", C.OpKind.Gemm, [X, W], [Y], 0,
+                                         struct.pack("<ii", 0, 1)),
+                  lambda: torch.matmul(X, W.t(), out=Y))
+    dZ = torch.randn((8192, 4096), device="cuda", generator=g).to(torch.bfloat16)
+    H = torch.randn((8192, 4096), device="cuda", generator=g).to(torch.bfloat16)
+    dW = torch.empty((4096, 4096), device="cuda")
+    dWb = torch.empty((4096, 4096), device="cuda", dtype=torch.bfloat16)
+    alternate(lambda: C.launch_by_id("gemm_bf16_mfma_f32out_v0", C.OpKind.Gemm, [dZ, H], [dW], 0,
+                                     struct.pack("<ii", 1, 0)),
+              lambda: torch.matmul(dZ.t(), H, out=dWb))
+    torch.cuda.synchronize()
+    log("[bench] vendor-compare: 3 shapes x 2 x (5 ours, 5 torch.matmul) launches")
+
+
+def pmc_mfma_compare_report(counter_csv, trace_csv):
+    """MFMA utilisation and clock per (kernel, shape) of a --vendor-compare
+    run (rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE
+    SQ_INSTS_VALU_MFMA_MOPS_BF16 --kernel-trace); the first launch of each
+    group is dropped."""
+    import csv
+    from collections import OrderedDict, defaultdict
+
+    cnt = defaultdict(lambda: defaultdict(float))
+    names = {}
+    with open(counter_csv, newline="") as f:
+        for row in csv.DictReader(f):
+            d = int(row["Dispatch_Id"])
+            cnt[d][row["Counter_Name"]] += float(row["Counter_Value"])
+            names[d] = row.get("Kernel_Name", "")
+    dur = {}
+    with open(trace_csv, newline="") as f:
+        for row in csv.DictReader(f):
+            dur[int(row["Dispatch_Id"])] = (int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) * 1e-9
+    groups = OrderedDict()
+    for d in sorted(cnt):
+        n = names[d]
+        if not ("gemm_nt" in n or "Cijk" in n) or d not in dur:
+            continue
+        flop = cnt[d]["SQ_INSTS_VALU_MFMA_MOPS_BF16"] * 512.0
+        short = n.replace("void aicf::hip::(anonymous namespace)::", "").split("(")[0][:72]
+        key = ("ours " if "gemm_nt" in n else "hipBLASLt ") + short + f" | {flop / 1e9:.0f} GFLOP"
+        groups.setdefault(key, []).append(d)
+    lines = [
+        "# bf16 GEMM on MI355X: our kernel vs hipBLASLt, MFMA utilisation and clock",
+        "",
+        "Commands (GPU box, repo root):",
+        "```",
+        "rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE SQ_INSTS_VALU_MFMA_MOPS_BF16 --kernel-trace "
+        "--output-format csv -d gpurun_out/pmc_vendor -o run -- python3 bench.py --vendor-compare",
+        "python3 bench.py --pmc-mfma-compare-report gpurun_out/pmc_vendor/run_counter_collection.csv "
+        "gpurun_out/pmc_vendor/run_kernel_trace.csv",
+        "```",
+        "",
+        "MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE per XCD x 1024 SIMDs) = achieved / peak at "
+        "the clock the part actually ran; clock = GRBM_GUI_ACTIVE per XCD / kernel duration.  Shapes: "
+        "8192^3 NT (1100 GFLOP), 8192x4096x4096 NT (275), dW = dZ^T.H with K = 8192 (275, second "
+        "group of that size).",
+        "",
+        "| kernel | GFLOP | launches | us | clock GHz | MFMA busy | TFLOP/s | % of 2.5 PF |",
+        "|---|---:|---:|---:|---:|---:|---:|---:|",
+    ]
+    for key, ds in groups.items():
+        ds = ds[1:] if len(ds) > 4 else ds  # the first launch of each kernel warms it up
+        t = sum(dur[d] for d in ds) / len(ds)
+        gui = sum(cnt[d]["GRBM_GUI_ACTIVE"] for d in ds) / len(ds) / 8.0
+        busy = sum(cnt[d]["SQ_VALU_MFMA_BUSY_CYCLES"] for d in ds) / len(ds)
+        flop = sum(cnt[d]["SQ_INSTS_VALU_MFMA_MOPS_BF16"] for d in ds) / len(ds) * 512.0
+        name, gf = key.split(" | ")
+        lines.append(f"| `{name}` | {gf.split()[0]} | {len(ds)} | {t * 1e6:.1f} | {gui / t / 1e9:.2f} | "
+                     f"{busy / (gui * 1024.0) * 100:.1f}% | {flop / t / 1e12:.0f} | "
+                     f"{flop / t / 1e12 / PEAK_BF16_TFLOPS * 100:.1f}% |")
+    lines.append("")
+    print("\n".join(lines))
+
+
 def pmc_report(fetch_csv, write_csv, mfma_csv=None, trace_csv=None):
     """Markdown summary of two rocprofv3 --pmc runs of --roofline-only
     (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch).  Each counter is scaled
@@ -737,6 +834,10 @@ def main():
                          "[, MFMA counters, kernel trace]) and exit")
     ap.add_argument("--stats-report", nargs=3, metavar=("STATS_CSV", "TRACE_CSV", "STEPS"),
                     help="summarise a rocprofv3 --kernel-trace --stats run of the step and exit")
+    ap.add_argument("--vendor-compare", action="store_true",
+                    help="our GEMM and torch.matmul on the same shapes (for rocprofv3 --pmc)")
+    ap.add_argument("--pmc-mfma-compare-report", nargs=2, metavar=("COUNTER_CSV", "TRACE_CSV"),
+                    help="summarise a rocprofv3 MFMA-counter run of --vendor-compare and exit")
     ap.add_argument("--streaming-only", action="store_true",
                     help="run each streaming kernel at its benchmark shape (for rocprofv3 --pmc)")
     ap.add_argument("--pmc-streaming-report", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -744,6 +845,9 @@ def main():
     args = ap.parse_args()
     if args.pmc_report:
         pmc_report(*args.pmc_report)
+        return
+    if args.pmc_mfma_compare_report:
+        pmc_mfma_compare_report(*args.pmc_mfma_compare_report)
         return
     if args.stats_report:
         stats_report(args.stats_report[0], args.stats_report[1], int(args.stats_report[2]))
@@ -768,6 +872,9 @@ def main():
         return
     if args.streaming_only:
         streaming_only(C)
+        return
+    if args.vendor_compare:
+        vendor_compare(C)
         return
 
     res = bench_mlp(B, D, L, args.steps, args.warmup)
