@@ -483,13 +483,15 @@ def test_gemm_bf16_dgelu_with_mn_contiguous_weight_256_tiles(C):
     assert orc.rel_err(orc.bf16_bits_to_f32(h(dz)).reshape(M, N), ref) < 1e-2
 
 
-@pytest.mark.parametrize("ta,tb", [(0, 1), (1, 0), (0, 0), (1, 1)])
-def test_gemm_bf16_persistent_tiles(C, ta, tb):
+@pytest.mark.parametrize("ta,tb,K", [(0, 1, 128), (1, 0, 128), (0, 0, 128), (1, 1, 128), (0, 1, 192),
+                                     (0, 0, 192)])
+def test_gemm_bf16_persistent_tiles(C, ta, tb, K):
     """More 256x256 tiles (17 x 16 = 272) than CUs: one persistent workgroup
     per CU loops over its tiles, 16 of them take a second tile.  All operand
     layouts (fp32 output at 1e-5), bias+GELU with the pre-activation, and
-    dGELU epilogues."""
-    M, N, K = 17 * 256, 16 * 256, 128
+    dGELU epilogues.  K = 128 and 192 (2 and 3 K-steps) put the pre-activation
+    rows loaded during the last K-step in either stage buffer."""
+    M, N = 17 * 256, 16 * 256
     r = rng(300 + 2 * ta + tb)
     s = 1.0 / np.sqrt(K)
     A = r.uniform(-1, 1, (K, M) if ta else (M, K)).astype(np.float32)
