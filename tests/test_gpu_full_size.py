@@ -1,0 +1,128 @@
+"""GPU parity at the benchmark configurations' full sizes.
+
+The full outputs are too large for the fp64 oracle to recompute in
+seconds, so each test checks what does not depend on size:
+  * C2 row kernels (16384 rows x C): row max bit-exact on every row (max is
+    order-free), every softmax row sums to 1, the all -1e4 row is exactly
+    1/C, and sampled rows against the fp64 oracle;
+  * C3 AdamW over 2^28 parameters, t = 1..10: the update is elementwise, so
+    a sample of 2^20 parameters run through the oracle's fp32 restatement
+    must match the GPU bit for bit after every step;
+  * C4 GEMM + epilogue at every configured shape: rows are independent, so
+    sampled rows against an fp64 product of the same stored (bf16-rounded)
+    operands.
+Inputs follow BASELINE.json's configs (N(0,4) rows, N(0,0.02) / N(0,1e-3)
+Adam buffers, U(-1,1)/sqrt(K) GEMM operands), generated on the GPU from a
+seeded torch generator.
+"""
+from __future__ import annotations
+
+import math
+import struct
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+RRED = int.from_bytes(b"RRED", "little")
+ADAM = int.from_bytes(b"ADAM", "little")
+GEPI = int.from_bytes(b"GEPI", "little")
+
+
+def _host(t):
+    t = t.detach().cpu().contiguous()
+    if t.dtype == torch.bfloat16:
+        return orc.bf16_bits_to_f32(t.view(torch.int16).numpy().view(np.uint16)).reshape(t.shape)
+    return t.numpy()
+
+
+@pytest.mark.parametrize("cols", [128, 1024, 8192, 32768])
+def test_c2_row_softmax_max_sum_full_size(C, cols):
+    rows = 16384
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(cols)
+    x = torch.randn((rows, cols), device="cuda", generator=gen) * 2.0  # N(0, 4)
+    x[-1].fill_(-1e4)
+    y = torch.empty_like(x)
+    mx = torch.empty(rows, device="cuda")
+    sx = torch.empty(rows, device="cuda")
+    C.op_call(int(C.OpKind.RowSoftmax), [x], [y, mx, sx], 0, b"", 0)
+    rmax = torch.empty(rows, device="cuda")
+    rsum = torch.empty(rows, device="cuda")
+    C.op_call(int(C.OpKind.RowReduce), [x], [rmax], RRED, struct.pack("<i", 1), 0)
+    C.op_call(int(C.OpKind.RowReduce), [x], [rsum], RRED, struct.pack("<i", 0), 0)
+    xh = x.cpu().numpy()
+    yh = y.cpu().numpy()
+    ref_max = xh.max(axis=1)
+    assert np.array_equal(mx.cpu().numpy(), ref_max)
+    assert np.array_equal(rmax.cpu().numpy(), ref_max)
+    row_tot = yh.sum(axis=1, dtype=np.float64)
+    assert np.abs(row_tot - 1.0).max() < 1e-5
+    assert np.all(yh[-1] == np.float32(1.0 / cols))
+    sample = np.random.default_rng(cols).choice(rows - 1, 64, replace=False)
+    sample = np.append(sample, rows - 1)
+    ry, rmx, rsx = orc.softmax_rows_f64(xh[sample])
+    assert orc.rel_err(yh[sample], ry) < 1e-5
+    assert orc.rel_err(sx.cpu().numpy()[sample], rsx) < 1e-5
+    assert orc.rel_err(rsum.cpu().numpy()[sample], rsx) < 1e-5
+
+
+def test_c3_adamw_2p28_ten_steps_bit_exact_on_a_sample(C):
+    n = 1 << 28
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(28)
+    P = torch.randn(n, device="cuda", generator=gen) * 0.02
+    G = torch.randn(n, device="cuda", generator=gen) * 1e-3
+    M = torch.zeros(n, device="cuda")
+    V = torch.zeros(n, device="cuda")
+    step = torch.zeros((), dtype=torch.int32, device="cuda")
+    lr, b1, b2, eps, wd = 1e-3, 0.9, 0.999, 1e-8, 0.01
+    pay = struct.pack("<fffff", lr, b1, b2, eps, wd)
+    idx = torch.from_numpy(np.sort(np.random.default_rng(28).choice(n, 1 << 20, replace=False))).cuda()
+    p, gr = P[idx].cpu().numpy(), G[idx].cpu().numpy()
+    m = np.zeros_like(p)
+    v = np.zeros_like(p)
+    for t in range(1, 11):
+        C.launch_by_id("step_inc_v0", C.OpKind.StepInc, [step], [step])
+        C.launch_by_id("adamw_step_f32_v1", C.OpKind.AdamStep, [P, G, M, V, step], [P, M, V], ADAM, pay)
+        p, m, v = orc.adamw(p, gr, m, v, t, lr=lr, beta1=b1, beta2=b2, eps=eps, wd=wd)
+        assert np.array_equal(P[idx].cpu().numpy(), p), f"step {t}"
+        assert np.array_equal(M[idx].cpu().numpy(), m), f"step {t}"
+        assert np.array_equal(V[idx].cpu().numpy(), v), f"step {t}"
+    assert int(step.item()) == 10
+
+
+# (dtype, M, N, K, act): every C4 shape; GEPI kinds 1 bias only, 0 bias+ReLU, 3 bias+GELU
+C4_CASES = [
+    ("bf16", 8192, 8192, 8192, "gelu"), ("bf16", 8192, 8192, 8192, "none"),
+    ("bf16", 4096, 4096, 4096, "relu"), ("bf16", 1024, 1024, 1024, "gelu"),
+    ("bf16", 8192, 4096, 256, "relu"), ("bf16", 8192, 4096, 11008, "gelu"),
+    ("fp32", 8192, 8192, 8192, "gelu"), ("fp32", 4096, 4096, 4096, "relu"),
+    ("fp32", 1024, 1024, 1024, "none"),
+]
+ACT_KIND = {"none": 1, "relu": 0, "gelu": 3}
+
+
+@pytest.mark.parametrize("dt,M,N,K,act", C4_CASES)
+def test_c4_gemm_epilogue_full_size_sampled_rows(C, dt, M, N, K, act):
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(M + N + K)
+    s = 1.0 / math.sqrt(K)
+    tdt = torch.bfloat16 if dt == "bf16" else torch.float32
+    X = ((torch.rand((M, K), device="cuda", generator=gen) * 2 - 1) * s).to(tdt)
+    W = ((torch.rand((N, K), device="cuda", generator=gen) * 2 - 1) * s).to(tdt)
+    b = (torch.rand(N, device="cuda", generator=gen) * 2 - 1) * s
+    Y = torch.empty((M, N), device="cuda", dtype=tdt)
+    kid = "gemm_epilogue_bf16_mfma_v0" if dt == "bf16" else "gemm_epilogue_f32_mfma_v0"
+    C.launch_by_id(kid, C.OpKind.GemmEpilogue, [X, W, b], [Y], GEPI, struct.pack("<iii", 0, 1, ACT_KIND[act]))
+    rows = torch.from_numpy(np.sort(np.random.default_rng(K).choice(M, 16, replace=False))).cuda()
+    xs = _host(X[rows]).astype(np.float64)
+    wh = _host(W).astype(np.float64)
+    z = xs @ wh.T + b.cpu().numpy().astype(np.float64)[None, :]
+    ref = {"none": z, "relu": np.maximum(z, 0.0), "gelu": orc.gelu_f64(z)}[act]
+    tol = 1e-2 if dt == "bf16" else 1e-4
+    assert orc.rel_err(_host(Y[rows]), ref) < tol
