@@ -126,3 +126,51 @@ def test_c4_gemm_epilogue_full_size_sampled_rows(C, dt, M, N, K, act):
     ref = {"none": z, "relu": np.maximum(z, 0.0), "gelu": orc.gelu_f64(z)}[act]
     tol = 1e-2 if dt == "bf16" else 1e-4
     assert orc.rel_err(_host(Y[rows]), ref) < tol
+
+
+def test_c5_mlp_step_full_shape_forward_rows_and_adamw_bit_exact(C):
+    """C5 at its full shape (batch 8192, 4 x 4096^2, GELU, MSE, AdamW) replayed
+    once from its captured graph.  Forward rows are independent: 16 sampled
+    rows of every stored activation (z_i, h_i, y) against an fp64 chain from
+    the same bf16 inputs and weights that rounds each stored tensor to bf16.
+    The optimizer is elementwise: the oracle's AdamW applied to the GPU's own
+    gradients over all 67,125,248 parameters must reproduce the updated fp32
+    parameters, both moments and the bf16 shadow bit for bit."""
+    from aicf_hip import mlp
+
+    B, D, L = 8192, 4096, 4
+    ir, lowered, plan = mlp.build_mlp_mse(B, D, L)
+    ex = mlp.make_executor(ir, lowered, plan)
+    inputs, params = mlp.init_mlp_mse(B, D, L)
+    ex.build_env(inputs=inputs, params=params, reuse_static=False)
+    mlp.refresh_shadow(ex)
+    ex.capture(inputs=inputs, params=params, reuse_static=True)
+    P0 = ex.value("flat.params").cpu().numpy().copy()
+    Wb0 = ex.value("wb.flat").cpu().clone()
+    ex.replay(1)
+    torch.cuda.synchronize()
+
+    rows = torch.from_numpy(np.sort(np.random.default_rng(5).choice(B, 16, replace=False))).cuda()
+    lay = mlp.FlatLayout(D, L)
+    bf = lambda a: orc.bf16_round(a.astype(np.float32)).astype(np.float64)  # noqa: E731
+    h = _host(ex.value("x")[rows]).astype(np.float64)
+    wb0 = orc.bf16_bits_to_f32(Wb0.view(torch.int16).numpy().view(np.uint16))
+    for i in range(1, L + 1):
+        W = wb0[lay.w_off(i):lay.w_off(i) + D * D].reshape(D, D).astype(np.float64)
+        b = P0[lay.b_off(i):lay.b_off(i) + D].astype(np.float64)
+        z = bf(h @ W.T + b[None, :])
+        name = f"z{i}" if i < L else "y"
+        assert orc.rel_err(_host(ex.value(name)[rows]), z) < 1e-2, name
+        if i < L:
+            h = bf(orc.gelu_f64(z))
+            assert orc.rel_err(_host(ex.value(f"h{i}")[rows]), h) < 1e-2, f"h{i}"
+
+    G = ex.value("grad.flat").cpu().numpy()
+    Z = np.zeros_like(P0)
+    Pr, Mr, Vr, Wr = orc.adamw(P0, G, Z, Z, 1, 1e-3, 0.9, 0.999, 1e-8, 0.0, shadow=True)
+    assert np.array_equal(ex.value("flat.params").cpu().numpy(), Pr)
+    assert np.array_equal(ex.value("opt.m.flat").cpu().numpy(), Mr)
+    assert np.array_equal(ex.value("opt.v.flat").cpu().numpy(), Vr)
+    assert np.array_equal(ex.value("wb.flat").cpu().view(torch.int16).numpy().view(np.uint16), Wr)
+    assert np.isfinite(G).all() and np.abs(G).max() > 0
+    ex.reset_graph()
