@@ -515,11 +515,70 @@ Status mse_f16_launch(const TensorDesc* i, int ni, TensorDesc* o, int no, const 
 // (dPred same dtype as pred, loss f32 scalar, partials f32 [>= kMseBlocks]).
 //   dPred = (pred - target) * scale          (scale as mse_grad)
 //   loss  = mean((pred - target)^2)
-// Pass 1: kMseBlocks workgroups stride over the data, each writes its partial
-// sum of squares to partials[b].  Pass 2: one workgroup sums the partials in
-// a fixed order.  The result is deterministic for a given size.
+// Pass 1: when the partials buffer holds one value per 2048 elements and n
+// is a multiple of 8, one workgroup per 2048 elements, 8 per lane with
+// 16-byte nontemporal accesses and no loop (streams at ~79% of HBM peak at
+// 8192 x 4096, against ~69% for a grid-stride loop); otherwise kMseBlocks
+// workgroups stride over the data.  Each workgroup writes its partial sum of
+// squares to partials[b].  Pass 2: one workgroup sums the partials in a
+// fixed order.  The result is deterministic for a given size.
 // ---------------------------------------------------------------------------
 constexpr int kMseBlocks = 1024;
+constexpr int64_t kMseElemsPerBlock = 2048;  // one-shot pass 1: 256 lanes x 8
+
+template <bool BF16>
+__global__ __launch_bounds__(256) void mse_loss_grad_oneshot(const void* __restrict__ pred,
+                                                             const float* __restrict__ tgt,
+                                                             void* __restrict__ dpred,
+                                                             float* __restrict__ partial, int64_t n8,
+                                                             float scale) {
+  __shared__ float red[4];
+  float acc = 0.0f;
+  const int64_t v = (int64_t)blockIdx.x * 256 + threadIdx.x;  // group of 8 elements
+  if (v < n8) {
+    const f32x4 t0 = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(tgt) + 2 * v);
+    const f32x4 t1 = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(tgt) + 2 * v + 1);
+    float pv[8], tv[8];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      tv[c] = t0[c];
+      tv[c + 4] = t1[c];
+    }
+    if constexpr (BF16) {
+      const u16x8 pb = __builtin_nontemporal_load(reinterpret_cast<const u16x8*>(pred) + v);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) pv[c] = bf16_to_f32(pb[c]);
+    } else {
+      const f32x4 p0 = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(pred) + 2 * v);
+      const f32x4 p1 = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(pred) + 2 * v + 1);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        pv[c] = p0[c];
+        pv[c + 4] = p1[c];
+      }
+    }
+    float d[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const float e = pv[c] - tv[c];
+      acc = fmaf(e, e, acc);
+      d[c] = e * scale;
+    }
+    if constexpr (BF16) {
+      u16x8 db;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) db[c] = f32_to_bf16(d[c]);
+      __builtin_nontemporal_store(db, reinterpret_cast<u16x8*>(dpred) + v);
+    } else {
+      __builtin_nontemporal_store(f32x4{d[0], d[1], d[2], d[3]}, reinterpret_cast<f32x4*>(dpred) + 2 * v);
+      __builtin_nontemporal_store(f32x4{d[4], d[5], d[6], d[7]}, reinterpret_cast<f32x4*>(dpred) + 2 * v + 1);
+    }
+  }
+  acc = wave_sum(acc);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) partial[blockIdx.x] = (red[0] + red[1]) + (red[2] + red[3]);
+}
 
 template <bool BF16>
 __global__ __launch_bounds__(256) void mse_loss_grad_pass1(const void* __restrict__ pred,
@@ -575,17 +634,35 @@ __global__ __launch_bounds__(256) void mse_loss_grad_pass1(const void* __restric
   if (threadIdx.x == 0) partial[blockIdx.x] = (red[0] + red[1]) + (red[2] + red[3]);
 }
 
-__global__ __launch_bounds__(256) void mse_loss_grad_pass2(const float* __restrict__ partial,
-                                                           int nparts, float* __restrict__ loss,
-                                                           double inv_n) {
-  __shared__ double red[4];
+// One workgroup of 1024 lanes; each lane loads 8 partials at a time (all in
+// flight together) and adds them in a fixed order, then lanes and waves are
+// combined in a fixed order.
+__global__ __launch_bounds__(1024) void mse_loss_grad_pass2(const float* __restrict__ partial,
+                                                            int nparts, float* __restrict__ loss,
+                                                            double inv_n) {
+  constexpr int T = 1024, U = 8;
+  __shared__ double red[T / 64];
   double acc = 0.0;
-  for (int i = threadIdx.x; i < nparts; i += 256) acc += (double)partial[i];
+  for (int base = 0; base < nparts; base += T * U) {
+    float v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = base + u * T + (int)threadIdx.x;
+      v[u] = i < nparts ? partial[i] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc += (double)v[u];
+  }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
   __syncthreads();
-  if (threadIdx.x == 0) loss[0] = (float)(((red[0] + red[1]) + (red[2] + red[3])) * inv_n);
+  if (threadIdx.x == 0) {
+    double tot = 0.0;
+#pragma unroll
+    for (int w = 0; w < T / 64; ++w) tot += red[w];
+    loss[0] = (float)(tot * inv_n);
+  }
 }
 
 bool mse_loss_check(const TensorDesc* in, int ni, const TensorDesc* out, int no) {
@@ -611,14 +688,28 @@ Status mse_loss_launch(const TensorDesc* in, int ni, TensorDesc* out, int no, co
   const int64_t n = numel_of(in[0]);
   const float sc = mse_scale(a, n);
   hipStream_t s = as_stream(stream);
-  if (dt(in[0]) == DType::kBF16)
+  const bool bf = dt(in[0]) == DType::kBF16;
+  const int64_t oneshot_blocks = (n + kMseElemsPerBlock - 1) / kMseElemsPerBlock;
+  const bool oneshot = n % 8 == 0 && aligned(in[0].data, 16) && aligned(out[0].data, 16) &&
+                       oneshot_blocks <= numel_of(out[2]) && oneshot_blocks <= INT32_MAX;
+  int nparts = kMseBlocks;
+  if (oneshot) {
+    nparts = (int)oneshot_blocks;
+    if (bf)
+      mse_loss_grad_oneshot<true><<<(unsigned)nparts, 256, 0, s>>>(
+          in[0].data, (const float*)in[1].data, out[0].data, (float*)out[2].data, n / 8, sc);
+    else
+      mse_loss_grad_oneshot<false><<<(unsigned)nparts, 256, 0, s>>>(
+          in[0].data, (const float*)in[1].data, out[0].data, (float*)out[2].data, n / 8, sc);
+  } else if (bf) {
     mse_loss_grad_pass1<true><<<kMseBlocks, 256, 0, s>>>(in[0].data, (const float*)in[1].data,
                                                          out[0].data, (float*)out[2].data, n, sc);
-  else
+  } else {
     mse_loss_grad_pass1<false><<<kMseBlocks, 256, 0, s>>>(in[0].data, (const float*)in[1].data,
                                                           out[0].data, (float*)out[2].data, n, sc);
-  mse_loss_grad_pass2<<<1, 256, 0, s>>>((const float*)out[2].data, kMseBlocks,
-                                        (float*)out[1].data, 1.0 / (double)n);
+  }
+  mse_loss_grad_pass2<<<1, 1024, 0, s>>>((const float*)out[2].data, nparts, (float*)out[1].data,
+                                         1.0 / (double)n);
   return launch_status("mse_loss_grad_v0");
 }
 

@@ -333,7 +333,8 @@ struct RowReducer {
 // Statistics of a row segment, combined in one reduction round:
 //   m  maximum (and i, the first column holding it, for cross-entropy),
 //   s  sum of exp(x - m) over the segment (rescaled when segments merge),
-//   sx sum of x.
+//   sx sum of x; for cross-entropy, z[label] (held by the one lane that owns
+//      the label's column, zero elsewhere, so the sum is exact).
 // Merging is symmetric in its two arguments (max, tie-aware argmax, and
 // sums), so every lane of a butterfly ends with bit-identical statistics.
 struct RowStat {
@@ -352,9 +353,8 @@ __device__ __forceinline__ void stat_merge(RowStat& a, const RowStat& b) {
     const float y = b.m == M ? b.s : b.s * __expf(b.m - M);
     if constexpr (MODE == MODE_XENT) {
       if (b.m > a.m || (b.m == a.m && b.i < a.i)) a.i = b.i;
-    } else {
-      a.sx += b.sx;
     }
+    a.sx += b.sx;
     a.m = M;
     a.s = x + y;
   }
@@ -393,6 +393,8 @@ __global__ __launch_bounds__(LPR >= 256 ? LPR : 256) void row_reg_kernel(RowArgs
   const bool active = row < a.R;  // uniform across the lanes of a row
   const int64_t C = a.C;
   const f32x4* xr = reinterpret_cast<const f32x4*>(a.x + (active ? row : 0) * C);
+  // cross-entropy: the label is read first, so its latency hides behind the row loads
+  const int lab = (MODE == MODE_XENT && active) ? a.labels[row] : -1;
 
   f32x4 v[VPT];
 #pragma unroll
@@ -413,11 +415,14 @@ __global__ __launch_bounds__(LPR >= 256 ? LPR : 256) void row_reg_kernel(RowArgs
 #pragma unroll
     for (int k = 0; k < VPT; ++k)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < 4; ++j) {
+        const int col = (k * LPR + l) * 4 + j;
         if (v[k][j] > st.m) {
           st.m = v[k][j];
-          st.i = (k * LPR + l) * 4 + j;
+          st.i = col;
         }
+        if (col == lab) st.sx = v[k][j];
+      }
   } else if constexpr (MODE != MODE_SUM) {
 #pragma unroll
     for (int k = 0; k < VPT; ++k) st.m = fmaxf(st.m, fmaxf(fmaxf(v[k][0], v[k][1]), fmaxf(v[k][2], v[k][3])));
@@ -478,7 +483,6 @@ __global__ __launch_bounds__(LPR >= 256 ? LPR : 256) void row_reg_kernel(RowArgs
       if (a.rsum) a.rsum[row] = st.sx;
     }
   } else {  // MODE_XENT
-    const int lab = a.labels[row];
     const bool valid = lab >= 0 && (int64_t)lab < C;
     const float sc = a.inv_batch;
 #pragma unroll
@@ -494,7 +498,7 @@ __global__ __launch_bounds__(LPR >= 256 ? LPR : 256) void row_reg_kernel(RowArgs
     if (l == 0) {
       a.argmax[row] = st.i;
       // loss_i = log(sum exp(z - m)) + m - z[label]
-      a.row_loss[row] = valid ? (logf(st.s) + st.m - a.x[row * C + lab]) : __builtin_nanf("");
+      a.row_loss[row] = valid ? (logf(st.s) + st.m - st.sx) : __builtin_nanf("");
     }
   }
 }

@@ -151,7 +151,8 @@ def build_mlp_mse(B: int = 8192, D: int = 4096, L: int = 4, *, lr: float = 1e-3,
     ir.emit(op="Linear", inputs=[h[L - 1], Wbv[L], bias[L]], outputs=[y], attrs=lin)
     dY = nv("dY", (B, D), BF16)
     loss = nv("loss", ())
-    mse_ws = nv("mse.partials", (1024,))
+    # one partial per 2048 elements lets the loss kernel use its one-shot pass
+    mse_ws = nv("mse.partials", (max(1024, -(-B * D // 2048)),))
     ir.emit(op="MseLoss", inputs=[y, t], outputs=[dY, loss, mse_ws])
     db_ws = nv("db.partials", (64, D))
     dcur = dY

@@ -246,7 +246,8 @@ def bench_mse(C, rows, cols, iters=20, warmup=3):
     def make():
         p = torch.randn((rows, cols), device="cuda", generator=g).to(torch.bfloat16)
         t = torch.randn((rows, cols), device="cuda", generator=g)
-        return p, t, torch.empty_like(p), torch.empty((), device="cuda"), torch.empty(1024, device="cuda")
+        return (p, t, torch.empty_like(p), torch.empty((), device="cuda"),
+                torch.empty(max(1024, -(-rows * cols // 2048)), device="cuda"))  # as the step sizes it
 
     sets = _rotating_sets(make, rows * cols * 8)
     k = [0]
@@ -637,7 +638,7 @@ STREAMING = [
     ("row sum 16384x32768 f32", "row_reg_kernel<512, 16, 1>", 4 * SR * SC + 4 * SR),
     ("row max 16384x32768 f32", "row_reg_kernel<512, 16, 2>", 4 * SR * SC + 4 * SR),
     ("softmax xent fwd+bwd 16384x8192 f32", "row_reg_kernel<512, 4, 3>", 8 * SR * 8192 + 16 * SR),
-    ("mse loss+grad 8192x4096 (bf16 p, f32 t, bf16 grad)", "mse_loss_grad_pass1", 8 * 8192 * 4096),
+    ("mse loss+grad 8192x4096 (bf16 p, f32 t, bf16 grad)", "mse_loss_grad_oneshot", 8 * 8192 * 4096),
     ("bias grad colsum 8192x4096 bf16 -> f32", "colsum_vec_kernel", 2 * 8192 * 4096 + 4 * 4096),
     ("AdamW 2^28 f32 (P,G,M,V in; P,M,V out)", "adamw_vec4_kernel", 28 * (1 << 28)),
 ]
@@ -669,7 +670,7 @@ def streaming_only(C):
     del z, dz
     pb = torch.randn((8192, 4096), device="cuda", generator=g).to(torch.bfloat16)
     t = torch.randn((8192, 4096), device="cuda", generator=g)
-    d, part = torch.empty_like(pb), torch.empty(1024, device="cuda")
+    d, part = torch.empty_like(pb), torch.empty(8192 * 4096 // 2048, device="cuda")
     for _ in range(3):
         C.launch_by_id("mse_loss_grad_v0", C.OpKind.MseGrad, [pb, t], [d, loss, part])
     o, opart = torch.empty(4096, device="cuda"), torch.empty((64, 4096), device="cuda")

@@ -239,8 +239,11 @@ def test_mse_grad(C, shape):
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
-@pytest.mark.parametrize("shape", [(64, 256), (513, 1000), (2048, 4096)])
-def test_mse_loss_grad_fused(C, dtype, shape):
+@pytest.mark.parametrize("shape,nparts", [((64, 256), 1024), ((513, 1000), 1024), ((2048, 4096), 1024),
+                                          ((2048, 4096), 4096), ((37, 123), 1024)])
+def test_mse_loss_grad_fused(C, dtype, shape, nparts):
+    """Pass 1 one-shot (a partial per 2048 elements fits the buffer, n a
+    multiple of 8) or grid-stride (2048 x 4096 with 1024 partials; n = 4551)."""
     r = rng(7)
     p = r.standard_normal(shape).astype(np.float32)
     t = r.standard_normal(shape).astype(np.float32)
@@ -252,7 +255,7 @@ def test_mse_loss_grad_fused(C, dtype, shape):
         tp = g(p)
     d = torch.empty_like(tp)
     loss = torch.empty((), device="cuda")
-    part = torch.empty(1024, device="cuda")
+    part = torch.empty(nparts, device="cuda")
     C.launch_by_id("mse_loss_grad_v0", C.OpKind.MseGrad, [tp, g(t)], [d, loss, part])
     ref = orc.mse_grad_f32(p, t)
     if dtype == "bf16":
