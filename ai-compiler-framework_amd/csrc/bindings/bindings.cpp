@@ -54,6 +54,7 @@ enum class OpKind : int {
   GeluBwd = AICF_OP_GELU_BWD,
   EltwiseGelu = AICF_OP_ELTWISE_GELU,
   Transpose = AICF_OP_TRANSPOSE,
+  GemmAdamW = AICF_OP_GEMM_ADAMW,
 };
 
 std::string tensor_brief(const torch::Tensor& t) {
@@ -226,6 +227,7 @@ PYBIND11_MODULE(_C, m) {
       .value("GeluBwd", OpKind::GeluBwd)
       .value("EltwiseGelu", OpKind::EltwiseGelu)
       .value("Transpose", OpKind::Transpose)
+      .value("GemmAdamW", OpKind::GemmAdamW)
       .export_values();
 
   m.def(

@@ -63,6 +63,7 @@ enum class OpKind : int {
   GeluBwd = AICF_OP_GELU_BWD,
   EltwiseGelu = AICF_OP_ELTWISE_GELU,
   Transpose = AICF_OP_TRANSPOSE,
+  GemmAdamW = AICF_OP_GEMM_ADAMW,
   _Count = AICF_OP_COUNT,
 };
 

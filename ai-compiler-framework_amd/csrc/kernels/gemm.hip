@@ -31,6 +31,7 @@
 #include <type_traits>
 #include <utility>
 
+#include "../common/adamw.hpp"
 #include "../common/hip_util.hpp"
 
 namespace aicf::hip {
@@ -43,7 +44,20 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 enum InKind { IN_F32 = 0, IN_F16 = 1, IN_BF16 = 2 };
 enum OutKind { OUT_F32 = 0, OUT_F16 = 1, OUT_BF16 = 2 };
-enum Act { ACT_NONE = 0, ACT_RELU = 1, ACT_GELU = 2, ACT_DGELU = 3 };
+// ACT_ADAMW (fp32 accumulators only): the tile is the gradient of a weight
+// matrix; the epilogue applies AdamW to that weight instead of storing it.
+enum Act { ACT_NONE = 0, ACT_RELU = 1, ACT_GELU = 2, ACT_DGELU = 3, ACT_ADAMW = 4 };
+
+// Optimizer state a fused weight-gradient GEMM updates in place ([M, N]
+// row-major like the output, leading dimension ldc).
+struct GemmAdamW {
+  float* P;             // fp32 master weights
+  float* M;             // first moment
+  float* V;             // second moment
+  uint16_t* Wb;         // bf16 shadow of P
+  const int32_t* step;  // device step counter (already incremented)
+  AdamWArgs args;
+};
 enum LoadMode { LD_KCONTIG = 0, LD_MNCONTIG = 1, LD_GATHER = 2 };
 
 struct GemmParams {
@@ -62,6 +76,7 @@ struct GemmParams {
   int act;
   int bias_f32;  // bias stored as fp32 (else in the output type)
   int tiles_m, tiles_n;
+  GemmAdamW adam;  // ACT_ADAMW only
 };
 
 template <int IN>
@@ -446,6 +461,7 @@ struct NTParams {
   int M, N, K;
   int bias_f32;
   int tiles_m, tiles_n;
+  GemmAdamW adam;  // ACT_ADAMW only
 };
 
 // Epilogue of the NT kernels.  Block (i, j) of the accumulators holds D[n][m];
@@ -479,7 +495,7 @@ __device__ __forceinline__ void nt_epilogue_staged(const NTParams& p,
   static_assert((CPR & (CPR - 1)) == 0 && (ROWS_PASS * CPR) % NT == 0, "chunk split");
   uint8_t* const tile = smem;
 
-  if constexpr (ACT != ACT_DGELU) {
+  if constexpr (ACT != ACT_DGELU && ACT != ACT_ADAMW) {
     if (p.bias) {
 #pragma unroll
       for (int i = 0; i < TN; ++i)
@@ -572,6 +588,39 @@ __device__ __forceinline__ void nt_epilogue_staged(const NTParams& p,
     __builtin_amdgcn_s_waitcnt(0);
   };
 
+  // ACT_ADAMW: the staged rows of this pass are the weight gradient; each
+  // 16-byte chunk updates 4 weights (P, M, V read and written, bf16 shadow
+  // written), row-contiguous like copy_out.
+  auto adam_out = [&](int pass) {
+    if constexpr (ACT == ACT_ADAMW) {
+      const AdamWScalars sc = adamw_scalars(p.adam.step, p.adam.args);
+#pragma unroll 4
+      for (int k = 0; k < ROWS_PASS * CPR / NT; ++k) {
+        const int idx = threadIdx.x + k * NT;
+        const int pr = idx / CPR, c = idx % CPR;
+        const f32x4 g = *reinterpret_cast<const f32x4*>(tile + pr * ROWB + ((c ^ (pr & (CPR - 1))) * 16));
+        const int64_t e = grow(pass, pr) * p.ldc + n0 + c * 4;
+        f32x4 pp = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p.adam.P + e));
+        f32x4 mm = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p.adam.M + e));
+        f32x4 vv = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p.adam.V + e));
+        u16x4 w;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float pj = pp[j], mj = mm[j], vj = vv[j];
+          adamw_elem(pj, g[j], mj, vj, sc, p.adam.args);
+          pp[j] = pj;
+          mm[j] = mj;
+          vv[j] = vj;
+          w[j] = f32_to_bf16(pj);
+        }
+        __builtin_nontemporal_store(pp, reinterpret_cast<f32x4*>(p.adam.P + e));
+        __builtin_nontemporal_store(mm, reinterpret_cast<f32x4*>(p.adam.M + e));
+        __builtin_nontemporal_store(vv, reinterpret_cast<f32x4*>(p.adam.V + e));
+        __builtin_nontemporal_store(w, reinterpret_cast<u16x4*>(p.adam.Wb + e));
+      }
+    }
+  };
+
 #pragma unroll
   for (int pass = 0; pass < NPASS; ++pass) {
     if constexpr (ACT == ACT_DGELU) {
@@ -621,7 +670,10 @@ __device__ __forceinline__ void nt_epilogue_staged(const NTParams& p,
           put4(off, v);
         }
     __syncthreads();
-    copy_out(pass, p.C, p.ldc);
+    if constexpr (ACT == ACT_ADAMW)
+      adam_out(pass);
+    else
+      copy_out(pass, p.C, p.ldc);
     if (pass + 1 < NPASS) __syncthreads();
   }
 }
@@ -1071,6 +1123,7 @@ Status run_nt_act(const GemmParams& g, hipStream_t s) {
   p.bias_f32 = g.bias_f32;
   p.tiles_m = p.M / BM;
   p.tiles_n = p.N / BN;
+  p.adam = g.adam;
   // 256 x 256 tiles hold one workgroup per CU: with more tiles than CUs, the
   // persistent configuration launches one workgroup per CU (a multiple of 8,
   // one per XCD slot) that loops over its tiles.
@@ -1089,6 +1142,10 @@ Status run_nt_layout(const GemmParams& g, hipStream_t s) {
     case ACT_RELU: return run_nt_act<IN, OUT, ACT_RELU, BM, BN, WM, WN, AKC, BKC>(g, s);
     case ACT_GELU: return run_nt_act<IN, OUT, ACT_GELU, BM, BN, WM, WN, AKC, BKC>(g, s);
     case ACT_DGELU: return run_nt_act<IN, OUT, ACT_DGELU, BM, BN, WM, WN, AKC, BKC>(g, s);
+    case ACT_ADAMW:
+      if constexpr (OUT == OUT_F32 && BM == 256 && BN == 256)
+        return run_nt_act<IN, OUT, ACT_ADAMW, BM, BN, WM, WN, AKC, BKC>(g, s);
+      return Status::Internal;  // fused AdamW runs on the 256 x 256 fp32-output tiles only
     default: return run_nt_act<IN, OUT, ACT_NONE, BM, BN, WM, WN, AKC, BKC>(g, s);
   }
 }
@@ -1153,6 +1210,12 @@ bool nt_eligible(const GemmParams& p, int BM, int BN, bool mn_ok) {
 
 template <int IN, int OUT>
 Status run_gemm(GemmParams& p, hipStream_t s) {
+  if (p.act == ACT_ADAMW) {  // the fused optimizer epilogue exists on the 256 x 256 NT path only
+    if constexpr (OUT == OUT_F32 && IN == IN_BF16) {
+      if (nt_eligible<IN, OUT>(p, 256, 256, true)) return run_nt256<IN, OUT>(p, s);
+    }
+    return Status::NotImplemented;
+  }
   {
     constexpr bool MN = IN != IN_F32;
     const int64_t tiles256 = (p.M / 256) * (p.N / 256);
@@ -1320,6 +1383,71 @@ EPI_VARIANT(epi_f16, DType::kF16, DType::kF16, true)
 EPI_VARIANT(epi_bf16, DType::kBF16, DType::kBF16, false)
 EPI_VARIANT(epi_bf16_f32out, DType::kBF16, DType::kF32, false)
 
+// ---------------------------------------------------------------------------
+// GemmAdamW (no reference counterpart): the weight-gradient GEMM of a Linear
+// layer with AdamW applied in its epilogue, so the fp32 gradient never goes
+// to memory.  inputs (A bf16, B bf16, P f32, M f32, V f32, step i32 scalar),
+// outputs (P, M, V in place, Wb bf16 shadow of P); P, M, V, Wb are [M, N]
+// row-major views; grad = op(A) . op(B).  Attr schema GADW
+// <ii fffff>: transA, transB, lr, beta1, beta2, eps, weight_decay.  Only the
+// 256 x 256-tile path carries this epilogue (bf16 operands, M and N
+// multiples of 256, K of 64, 16-byte aligned rows); other shapes are not
+// supported.
+// ---------------------------------------------------------------------------
+struct GadwAttr {
+  bool ta = false, tb = false;
+  AdamWArgs args{};
+  bool ok = false;
+};
+GadwAttr read_gadw(const void* attr) {
+  GadwAttr g;
+  const AttrBlob& a = blob(attr);
+  if (!attr || a.schema_id != AICF_SCHEMA_GADW || !payload_ok(a, 28)) return g;
+  g.ta = field<int32_t>(a, 0) != 0;
+  g.tb = field<int32_t>(a, 4) != 0;
+  const float lr = field<float>(a, 8), b1 = field<float>(a, 12), b2 = field<float>(a, 16);
+  const float eps = field<float>(a, 20), wd = field<float>(a, 24);
+  if (lr != lr || b1 != b1 || b2 != b2 || eps != eps || wd != wd) return g;
+  g.args = AdamWArgs{lr, b1, b2, eps, wd, 1.0f - b1, 1.0f - b2, 1.0f - lr * wd};
+  g.ok = true;
+  return g;
+}
+
+bool gadw_fill(const TensorDesc* in, int ni, const TensorDesc* out, int no, const void* attr,
+               GemmParams* pp) {
+  if (!in || !out || ni != 6 || no != 4) return false;
+  const GadwAttr at = read_gadw(attr);
+  if (!at.ok) return false;
+  if (dt(in[0]) != DType::kBF16 || dt(in[1]) != DType::kBF16) return false;
+  for (int k = 2; k < 5; ++k)
+    if (dt(in[k]) != DType::kF32 || !is_contig_2d_rowmajor(in[k])) return false;
+  if (dt(in[5]) != DType::kI32 || !in[5].contiguous || numel_of(in[5]) != 1) return false;
+  for (int k = 0; k < 3; ++k)  // P, M, V updated in place
+    if (dt(out[k]) != DType::kF32 || out[k].data != in[k + 2].data || !same_shape(out[k], in[k + 2]))
+      return false;
+  if (dt(out[3]) != DType::kBF16 || !is_contig_2d_rowmajor(out[3]) || !same_shape(out[3], in[2])) return false;
+  if (!same_shape(in[2], in[3]) || !same_shape(in[2], in[4])) return false;
+  if (!gemm_views_ok(in[0], in[1], in[2], at.ta, at.tb)) return false;
+  GemmParams p{};
+  fill_operands(p, in[0], in[1], in[2], at.ta, at.tb);
+  p.act = ACT_ADAMW;
+  p.adam = GemmAdamW{(float*)in[2].data, (float*)in[3].data, (float*)in[4].data, (uint16_t*)out[3].data,
+                     (const int32_t*)in[5].data, at.args};
+  if ((uintptr_t)p.adam.M % 16 || (uintptr_t)p.adam.V % 16 || (uintptr_t)p.adam.Wb % 8) return false;
+  if (!nt_eligible<IN_BF16, OUT_F32>(p, 256, 256, true)) return false;
+  if (pp) *pp = p;
+  return true;
+}
+bool gadw_sup(const TensorDesc* i, int ni, const TensorDesc* o, int no, const void* a) {
+  return gadw_fill(i, ni, o, no, a, nullptr);
+}
+Status gadw_launch(const TensorDesc* i, int ni, TensorDesc* o, int no, const void* a, void*, size_t,
+                   void* s) {
+  GemmParams p{};
+  if (!gadw_fill(i, ni, o, no, a, &p)) return Status::InvalidArgument;
+  return run_gemm<IN_BF16, OUT_F32>(p, as_stream(s));
+}
+
 size_t no_workspace(const TensorDesc*, int, const void*) { return 0; }
 
 KernelVariant make(const char* name, LaunchFn l, SupportedFn s) {
@@ -1356,6 +1484,11 @@ KernelVariant make_gemm_epilogue_bf16_variant() {
 }
 KernelVariant make_gemm_epilogue_bf16_f32out_variant() {
   return make("gemm_epilogue_bf16_mfma_f32out", epi_bf16_f32out_launch, epi_bf16_f32out_sup);
+}
+KernelVariant make_gemm_adamw_bf16_variant() {
+  KernelVariant v = make("gemm_adamw_bf16_mfma", gadw_launch, gadw_sup);
+  v.expected_attr_schema_id = AICF_SCHEMA_GADW;
+  return v;
 }
 
 }  // namespace aicf::hip

@@ -14,6 +14,7 @@
 // loop, so the whole array is covered by one wave of workgroups that the
 // dispatcher spreads over all 8 XCDs.  Out-of-place Adam reads P and writes
 // Pout in the same pass instead of copying P first.
+#include "../common/adamw.hpp"
 #include "../common/hip_util.hpp"
 
 namespace aicf::hip {
@@ -103,36 +104,6 @@ __global__ __launch_bounds__(256) void adam_ref_scalar_kernel(
 // step = lr / bc1 and ibc2 = 1 / bc2 (both rounded to fp32 once per thread).
 // Optionally writes bf16(p) into a shadow copy used by bf16 GEMMs.
 // ---------------------------------------------------------------------------
-struct AdamWArgs {
-  float lr, beta1, beta2, eps, wd, omb1, omb2, decay;  // decay = 1 - lr*wd
-};
-
-struct AdamWScalars {
-  float step, ibc2;
-};
-
-__device__ __forceinline__ AdamWScalars adamw_scalars(const int32_t* stepp, const AdamWArgs& a) {
-  int t = stepp[0];
-  if (t < 1) t = 1;
-  const float bc1 = (float)(1.0 - pow((double)a.beta1, (double)t));
-  const float bc2 = (float)(1.0 - pow((double)a.beta2, (double)t));
-  AdamWScalars s;
-  s.step = a.lr / bc1;
-  s.ibc2 = 1.0f / bc2;
-  return s;
-}
-
-__device__ __forceinline__ void adamw_elem(float& p, float g, float& m, float& v,
-                                           const AdamWScalars& s, const AdamWArgs& a) {
-  p = p * a.decay;
-  const float m_new = fmaf(a.beta1, m, a.omb1 * g);
-  const float v_new = fmaf(a.beta2, v, a.omb2 * (g * g));
-  const float denom = sqrtf(v_new * s.ibc2) + a.eps;
-  p = fmaf(-s.step, m_new / denom, p);
-  m = m_new;
-  v = v_new;
-}
-
 template <int UNROLL, bool SHADOW>
 __global__ __launch_bounds__(256) void adamw_vec4_kernel(
     const float* __restrict__ P, const float* __restrict__ G, const float* __restrict__ M,

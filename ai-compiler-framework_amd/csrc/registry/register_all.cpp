@@ -66,6 +66,7 @@ KernelVariant make_gemm_bias_relu_f32_naive_variant();
 KernelVariant make_gemm_bias_relu_f16_tc_wmma_out_f16_variant();
 KernelVariant make_gemm_epilogue_bf16_variant();
 KernelVariant make_gemm_epilogue_bf16_f32out_variant();
+KernelVariant make_gemm_adamw_bf16_variant();
 
 void register_all_kernels_into(KernelRegistry& R) {
   if (std::getenv("AICF_VERBOSE")) std::fprintf(stderr, "[aicf] register_all: gfx950 backend\n");
@@ -162,6 +163,7 @@ void register_all_kernels_into(KernelRegistry& R) {
   reg(OpKind::EltwiseGelu, make_gelu_bf16_variant(), 10, "gelu_bf16_v0");
   reg(OpKind::EltwiseGelu, make_gelu_f32_variant(), 0, "gelu_f32_v0");
   reg(OpKind::Transpose, make_transpose_variant(), 0, "transpose2d_v0");
+  reg(OpKind::GemmAdamW, make_gemm_adamw_bf16_variant(), 0, "gemm_adamw_bf16_v0");
 }
 
 }  // namespace aicf::hip

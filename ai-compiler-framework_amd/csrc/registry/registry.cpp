@@ -157,6 +157,7 @@ const char* opkind_name(OpKind k) {
     case OpKind::GeluBwd: return "gelu_bwd";
     case OpKind::EltwiseGelu: return "gelu";
     case OpKind::Transpose: return "transpose";
+    case OpKind::GemmAdamW: return "gemm_adamw";
     case OpKind::_Count: break;
   }
   return "unknown";

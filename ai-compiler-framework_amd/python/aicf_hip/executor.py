@@ -60,6 +60,7 @@ OPNAME_TO_KIND: Dict[str, int] = {
     "row_softmax": int(_C.OpKind.RowSoftmax), "row_reduce": int(_C.OpKind.RowReduce),
     "softmax_xent": int(_C.OpKind.SoftmaxXent), "gelu_bwd": int(_C.OpKind.GeluBwd),
     "gelu": int(_C.OpKind.EltwiseGelu), "transpose": int(_C.OpKind.Transpose),
+    "gemm_adamw": int(_C.OpKind.GemmAdamW),
 }
 
 
@@ -73,6 +74,7 @@ SCHEMA_BCOR = _fourcc_le(b"BCOR")
 SCHEMA_SGDS = _fourcc_le(b"SGDS")
 SCHEMA_MSEG = _fourcc_le(b"MSEG")
 SCHEMA_RRED = _fourcc_le(b"RRED")
+SCHEMA_GADW = _fourcc_le(b"GADW")
 SCHEMA_GEMM = int.from_bytes(b"GEMM", "big")
 SCHEMA_RSUM = int.from_bytes(b"RSUM", "big")
 
@@ -106,6 +108,11 @@ def pack_attrs(op: str, attrs: Dict[str, Any]) -> Tuple[int, bytes]:
     if op == "gemm_epilogue":
         return SCHEMA_GEPI, struct.pack("<iii", int(bool(a.get("transA", False))),
                                         int(bool(a.get("transB", False))), epilogue_kind(a))
+    if op == "gemm_adamw":
+        return SCHEMA_GADW, struct.pack("<iifffff", int(bool(a.get("transA", False))),
+                                        int(bool(a.get("transB", False))), float(a.get("lr", 1e-3)),
+                                        float(a.get("beta1", 0.9)), float(a.get("beta2", 0.999)),
+                                        float(a.get("eps", 1e-8)), float(a.get("weight_decay", 0.0)))
     if op in ("adam_step", "adamw_step"):
         vals = [float(a.get("lr", 1e-3)), float(a.get("beta1", 0.9)), float(a.get("beta2", 0.999)),
                 float(a.get("eps", 1e-8))]
@@ -236,7 +243,7 @@ class PlannedExecutor:
             if warmup and op == "step_inc":
                 outs_t[0].copy_(ins_t[0])
                 continue
-            if warmup and op in ("adam_step", "adamw_step"):
+            if warmup and op in ("adam_step", "adamw_step", "gemm_adamw"):
                 attrs = dict(attrs, lr=0.0)
             schema, payload = pack_attrs(op, attrs)
             if kid is not None:

@@ -12,6 +12,10 @@ compile-time rewrites of the reference pipeline:
   extended with gemm -> bias_add -> gelu (==> bias_gelu, keeping the
   pre-activation when a later gelu_bwd needs it) and gemm -> gelu_bwd
   (==> dgelu epilogue).
+* StageE  fuse_optimizer_into_gemms (not in the reference; opt-in): a
+  weight-gradient GEMM whose output only feeds the flat AdamW step becomes
+  gemm_adamw (AdamW applied in the GEMM's epilogue, no fp32 gradient in
+  memory); the flat step keeps the remaining ranges.
 * StageB  apply_kernel_selection (reference kernel_select.py:22-142 and the
   vec2/half2 upgrades of plan.py:371-444): pins a kernel_id on every op.
 
@@ -31,7 +35,7 @@ _PRIMITIVES = {
     "copy", "copy_saved", "copy_aux", "grad_zero", "adam_step", "step_inc", "bias_corr",
     "sgd_step", "gelu", "gelu_bwd", "softmax_xent", "row_softmax", "row_reduce", "mse_loss",
     "adamw_step", "layernorm_fwd", "layernorm_bwd", "batchnorm_fwd", "batchnorm_bwd",
-    "transpose",
+    "transpose", "gemm_adamw",
 }
 
 _ALIASES = {"adamstep": "adam_step", "stepinc": "step_inc", "biascorr": "bias_corr",
@@ -317,6 +321,8 @@ def pick_kernel_id(ir: IRGraph, it: Dict[str, Any]) -> Optional[str]:
         return "adam_step_f32_v0"
     if op == "adamw_step":
         return "adamw_step_f32_v1"
+    if op == "gemm_adamw":
+        return "gemm_adamw_bf16_v0"
     if op == "step_inc":
         return "step_inc_v0"
     if op == "bias_corr":
@@ -353,17 +359,142 @@ def apply_kernel_selection(ir: IRGraph, lowered: Lowered) -> Lowered:
     return out
 
 
+def _base_and_offset(ir: IRGraph, vid: int):
+    v = ir.values[vid]
+    return (v.view_of[0], v.view_of[1]) if v.view_of else (vid, 0)
+
+
+def _view(ir: IRGraph, base: int, off: int, shape, dtype: str) -> int:
+    """A view of `base` at element offset `off` with this shape and dtype:
+    an existing IR value if one matches, else a new one."""
+    shape = tuple(int(s) for s in shape)
+    for v in ir.values.values():
+        if v.view_of == (base, off) and v.shape == shape and v.dtype == dtype:
+            return v.id
+    b = ir.values[base]
+    return ir.new_value(name=f"{b.name}[{off}:{off + _numel_shape(shape)}]", shape=shape, dtype=dtype,
+                        device=b.device, view_of=(base, off)).id
+
+
+def _numel_shape(shape) -> int:
+    n = 1
+    for s in shape:
+        n *= int(s)
+    return n
+
+
+def gemm_adamw_eligible(M: int, N: int, K: int) -> bool:
+    """Shapes the fused kernel (256 x 256 tiles) covers."""
+    return M % 256 == 0 and N % 256 == 0 and K % 64 == 0 and M > 0 and N > 0 and K > 0
+
+
+def fuse_optimizer_into_gemms(ir: IRGraph, lowered: Lowered) -> Lowered:
+    """StageE (not in the reference): for the flat AdamW step
+    adamw_step(P, G, M, V, step) -> (P, M, V, Wb), every bf16 GEMM that writes
+    a 2-D view of G read by no other op becomes
+        gemm_adamw(A, B, P', M', V', step) -> (P', M', V', Wb')
+    with P', M', V', Wb' the views of P, M, V, Wb at the same offset: AdamW
+    runs in the GEMM's epilogue and the fp32 gradient never goes to memory.
+    The flat step is replaced by steps over the ranges no GEMM covered (one
+    per contiguous range), and step_inc moves in front of the first fused GEMM
+    (the fused kernels read the incremented counter, as the flat step does).
+    The updates are bit-identical to the unfused plan: the epilogue applies
+    the same AdamW expression to the same fp32 accumulators the GEMM would
+    have stored."""
+    kind = lambda it: str(it.get("op", "")).strip().lower()  # noqa: E731
+    ad = [i for i, it in enumerate(lowered) if kind(it) == "adamw_step"]
+    if len(ad) != 1 or len(lowered[ad[0]]["outputs"]) != 4:
+        return lowered
+    adam = lowered[ad[0]]
+    P, G, M, V, step = (int(x) for x in adam["inputs"])
+    Wb = int(adam["outputs"][3])
+    if any(ir.values[x].view_of for x in (P, G, M, V, Wb)):
+        return lowered
+    hyper = {k: adam.get("attrs", {}).get(k) for k in ("lr", "beta1", "beta2", "eps", "weight_decay")}
+    hyper = {k: v for k, v in hyper.items() if v is not None}
+
+    def readers(vid: int) -> int:
+        return sum(1 for it in lowered if vid in it.get("inputs", []))
+
+    def touched_later(idx: int, lo: int, hi: int) -> bool:
+        """Whether an item after `idx` (before the flat step) reads or writes
+        P, M, V or Wb in [lo, hi): the fused kernel updates that range where
+        the GEMM stood, the unfused plan only at the flat step."""
+        for it in lowered[idx + 1:ad[0]]:
+            for x in list(it.get("inputs", [])) + list(it.get("outputs", [])):
+                b, o = _base_and_offset(ir, int(x))
+                if b in (P, M, V, Wb) and o < hi and lo < o + _numel(ir, int(x)):
+                    return True
+        return False
+
+    out: Lowered = []
+    covered = []
+    first_fused = None
+    for idx, it in enumerate(lowered):
+        if kind(it) == "gemm" and len(it["outputs"]) == 1 and idx < ad[0]:
+            o = int(it["outputs"][0])
+            base, off = _base_and_offset(ir, o)
+            a, b = (int(x) for x in it["inputs"])
+            attrs = dict(it.get("attrs", {}))
+            ta, tb = bool(attrs.get("transA", False)), bool(attrs.get("transB", False))
+            sa, sb = ir.values[a].shape, ir.values[b].shape
+            if base == G and len(ir.values[o].shape) == 2 and readers(o) == 0 \
+                    and "bfloat16" in str(ir.values[a].dtype) and "bfloat16" in str(ir.values[b].dtype) \
+                    and len(sa) == 2 and len(sb) == 2:
+                Mg = sa[1] if ta else sa[0]
+                Kg = sa[0] if ta else sa[1]
+                Ng = sb[0] if tb else sb[1]
+                if tuple(ir.values[o].shape) == (Mg, Ng) and gemm_adamw_eligible(Mg, Ng, Kg) \
+                        and not touched_later(idx, off, off + Mg * Ng):
+                    shp = ir.values[o].shape
+                    pv = _view(ir, P, off, shp, ir.values[P].dtype)
+                    mv = _view(ir, M, off, shp, ir.values[M].dtype)
+                    vv = _view(ir, V, off, shp, ir.values[V].dtype)
+                    wv = _view(ir, Wb, off, shp, ir.values[Wb].dtype)
+                    if first_fused is None:
+                        first_fused = len(out)
+                    out.append(_item("gemm_adamw", [a, b, pv, mv, vv, step], [pv, mv, vv, wv],
+                                     dict(transA=ta, transB=tb, **hyper)))
+                    covered.append((off, off + _numel(ir, o)))
+                    continue
+        if idx == ad[0] and covered:
+            total = _numel(ir, P)
+            gaps, pos = [], 0
+            for s, e in sorted(covered):
+                if s > pos:
+                    gaps.append((pos, s))
+                pos = max(pos, e)
+            if pos < total:
+                gaps.append((pos, total))
+            for s, e in gaps:
+                views = [_view(ir, x, s, (e - s,), ir.values[x].dtype) for x in (P, G, M, V, Wb)]
+                out.append(_item("adamw_step", [views[0], views[1], views[2], views[3], step],
+                                 [views[0], views[2], views[3], views[4]], dict(adam.get("attrs", {}))))
+            continue
+        out.append(it)
+    if first_fused is not None:
+        si = [i for i, it in enumerate(out) if kind(it) == "step_inc" and int(it["inputs"][0]) == step]
+        if len(si) == 1 and si[0] > first_fused:
+            inc = out.pop(si[0])
+            out.insert(first_fused, inc)
+    return out
+
+
 def compile_lowered(ir: IRGraph, *, fuse: bool = True, fuse_bias: bool = False,
-                    nt_layout: Any = False, nt_min_flops: float = 2.0 ** 30) -> Lowered:
-    """StageA -> StageC -> (StageD) -> StageB.  nt_layout: False (no StageD),
-    True / "all" (transpose every M/N-contiguous 16-bit operand) or "cost"
-    (transpose only where that is cheaper than reading it in place)."""
+                    nt_layout: Any = False, nt_min_flops: float = 2.0 ** 30,
+                    fuse_optimizer: bool = False) -> Lowered:
+    """StageA -> StageC -> (StageD) -> (StageE) -> StageB.  nt_layout: False
+    (no StageD), True / "all" (transpose every M/N-contiguous 16-bit operand)
+    or "cost" (transpose only where that is cheaper than reading it in
+    place); fuse_optimizer: StageE."""
     low = lower_to_backend_ops(ir)
     if fuse:
         low = fuse_gemm_epilogue(ir, low, fuse_bias=fuse_bias)
     if nt_layout:
         policy = "all" if nt_layout is True else str(nt_layout)
         low = normalize_gemm_layout(ir, low, min_flops=nt_min_flops, policy=policy)
+    if fuse_optimizer:
+        low = fuse_optimizer_into_gemms(ir, low)
     return apply_kernel_selection(ir, low)
 
 

@@ -92,6 +92,11 @@ def init_mlp_xent(B=64, din=784, dh=256, dout=10, seed=0):
 # ============================================================ bf16 MSE MLP
 @dataclass
 class FlatLayout:
+    """Element offsets in the flat parameter buffer (and in the gradient,
+    moment and bf16-shadow buffers laid out alike): the L weight matrices
+    first, then the L biases, so that once the weight ranges are updated by
+    fused GEMM epilogues the biases are one contiguous range for one AdamW
+    launch."""
     D: int
     L: int
 
@@ -104,22 +109,25 @@ class FlatLayout:
         return self.per_layer * self.L
 
     def w_off(self, i: int) -> int:  # layer i in 1..L
-        return (i - 1) * self.per_layer
+        return (i - 1) * self.D * self.D
 
     def b_off(self, i: int) -> int:
-        return (i - 1) * self.per_layer + self.D * self.D
+        return self.L * self.D * self.D + (i - 1) * self.D
 
 
 def build_mlp_mse(B: int = 8192, D: int = 4096, L: int = 4, *, lr: float = 1e-3,
                   beta1: float = 0.9, beta2: float = 0.999, eps: float = 1e-8,
                   weight_decay: float = 0.0, dead_dx: bool = True, nt_layout="cost",
-                  nt_min_flops: float = 2.0 ** 30, device: str = "cuda:0"):
+                  nt_min_flops: float = 2.0 ** 30, fuse_optimizer: bool = False,
+                  device: str = "cuda:0"):
     """bf16 activations/weights, fp32 master parameters in one flat buffer.
     The GEMM kernel reads M/N-contiguous operands in place; StageD
     (nt_layout) may still insert explicit transposes: "cost" where a
     transpose is cheaper than the in-place read (none at the measured
     in-place cost of this kernel), True for every such operand, False for
-    none."""
+    none.  fuse_optimizer: each weight-gradient GEMM applies AdamW to its
+    layer's weights in its epilogue (StageE); the flat step then covers the
+    biases only."""
     ir = IRGraph(name=f"mlp_mse_{B}x{D}x{L}")
     lay = FlatLayout(D, L)
     nv = lambda n, s, dt=F32, view=None: ir.new_value(name=n, shape=s, dtype=dt,  # noqa: E731
@@ -169,7 +177,8 @@ def build_mlp_mse(B: int = 8192, D: int = 4096, L: int = 4, *, lr: float = 1e-3,
     ir.emit(op="AdamWStep", inputs=[P, Gf, Mf, Vf, step], outputs=[P, Mf, Vf, Wb],
             attrs={"lr": lr, "beta1": beta1, "beta2": beta2, "eps": eps,
                    "weight_decay": weight_decay})
-    lowered = compile_lowered(ir, fuse_bias=True, nt_layout=nt_layout, nt_min_flops=nt_min_flops)
+    lowered = compile_lowered(ir, fuse_bias=True, nt_layout=nt_layout, nt_min_flops=nt_min_flops,
+                              fuse_optimizer=fuse_optimizer)
     plan = build_binding_plan(ir, opts=PlanOptions(param_names={"flat.params"}))
     return ir, lowered, plan
 

@@ -324,12 +324,12 @@ def bench_adam(C, n=1 << 28, steps=10):
 
 
 # ------------------------------------------------------------------ MLP
-def bench_mlp(B, D, L, steps, warmup, dead_dx=True):
+def bench_mlp(B, D, L, steps, warmup, dead_dx=True, fuse_optimizer=False):
     import torch
 
     from aicf_hip import mlp
 
-    ir, lowered, plan = mlp.build_mlp_mse(B, D, L, dead_dx=dead_dx)
+    ir, lowered, plan = mlp.build_mlp_mse(B, D, L, dead_dx=dead_dx, fuse_optimizer=fuse_optimizer)
     ex = mlp.make_executor(ir, lowered, plan)
     inputs, params = mlp.init_mlp_mse(B, D, L)
     ex.build_env(inputs=inputs, params=params, reuse_static=False)
@@ -352,7 +352,7 @@ def bench_mlp(B, D, L, steps, warmup, dead_dx=True):
     ms = e0.elapsed_time(e1) / steps
     losses.append(float(ex.value("loss").item()))
     finite = all(math.isfinite(v) for v in losses)
-    ngemm = sum(1 for it in lowered if it["op"] in ("gemm", "gemm_epilogue"))
+    ngemm = sum(1 for it in lowered if it["op"] in ("gemm", "gemm_epilogue", "gemm_adamw"))
     ex.reset_graph()
     return {"ms": ms, "wall_ms": wall * 1e3 / steps, "steps_per_s": 1e3 / ms, "losses": losses,
             "finite": finite, "ops": len(lowered), "gemms": ngemm}
@@ -878,7 +878,7 @@ def main():
         vendor_compare(C)
         return
 
-    res = bench_mlp(B, D, L, args.steps, args.warmup)
+    res = bench_mlp(B, D, L, args.steps, args.warmup, fuse_optimizer=True)
     log(f"[bench] mlp {res}")
 
     # dominant kernel: forward GEMM of the step (bias + GELU epilogue)
@@ -939,7 +939,13 @@ def main():
                 "frac": round(tm["tflops"] / PEAK_BF16_TFLOPS, 4), "ms": round(tm["ms"], 4),
                 "note": "torch.matmul (hipBLASLt) in the same process, reference line only"}
             log(f"[bench] torch.matmul {M_}x{N_}x{K_} {tm}")
-        nd = bench_mlp(B, D, L, args.steps, args.warmup, dead_dx=False)
+        uf = bench_mlp(B, D, L, args.steps, args.warmup, fuse_optimizer=False)
+        comps["mlp_step_unfused_optimizer"] = {
+            "value": round(uf["steps_per_s"], 3), "unit": "steps/s", "ms": round(uf["ms"], 4),
+            "note": "same step with the reference's op split: dW GEMMs write the fp32 gradient, "
+                    "one streaming AdamW launch over all parameters; bit-identical results"}
+        log(f"[bench] mlp unfused optimizer {uf}")
+        nd = bench_mlp(B, D, L, args.steps, args.warmup, dead_dx=False, fuse_optimizer=True)
         comps["mlp_step_without_dead_input_dx"] = {
             "value": round(nd["steps_per_s"], 3), "unit": "steps/s", "ms": round(nd["ms"], 4),
             "gemms_per_step": nd["gemms"],
@@ -975,6 +981,7 @@ def main():
         "config": {"workload": "mlp_mse_bf16_train_step_hipgraph", "global_batch": B,
                    "hidden": D, "layers": L, "activation": "gelu_tanh", "loss": "mse",
                    "optimizer": "adamw(lr=1e-3, b=(0.9,0.999), eps=1e-8)",
+                   "optimizer_in_dw_gemm_epilogue": True,
                    "gemms_per_step": res["gemms"], "ops_per_step": res["ops"],
                    "parallelism": "single_gpu"},
         "roofline": roofline,

@@ -70,7 +70,8 @@ extern "C" {
 #define AICF_OP_GELU_BWD 21     /* dOut, Z -> dOut * gelu_tanh'(Z) */
 #define AICF_OP_ELTWISE_GELU 22 /* X -> gelu_tanh(X) */
 #define AICF_OP_TRANSPOSE 23    /* X[R,C] -> X^T[C,R] (2-D, row-major) */
-#define AICF_OP_COUNT 24
+#define AICF_OP_GEMM_ADAMW 24   /* A, B, P, M, V, step -> P, M, V, Wb: AdamW on P with grad op(A).op(B) (schema GADW) */
+#define AICF_OP_COUNT 25
 
 /*
  * Attribute schema ids (numeric ABI).  The reference mixes big-endian fourccs
@@ -88,6 +89,7 @@ extern "C" {
 #define AICF_SCHEMA_LNEP 0x50454E4Cu /* layernorm/launcher.cu:41      <f>   eps (default 1e-5) */
 #define AICF_SCHEMA_BNEP 0x50454E42u /* batchnorm/launcher.cu:51      <fI>  eps, flags (bit0 use_running_stats) */
 #define AICF_SCHEMA_RRED 0x44455252u /* appended: b"RRED" little-endian, <i> 0=sum 1=max */
+#define AICF_SCHEMA_GADW 0x57444147u /* appended: b"GADW" little-endian, <ii fffff> transA, transB, lr, b1, b2, eps, wd */
 
 /* GEPI epilogue kinds.  0..2 are the values core_v2/exec.py:223-252 packs;
  * 3..5 are appended. */

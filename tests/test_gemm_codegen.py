@@ -20,12 +20,13 @@ import pytest
 REPO = Path(__file__).resolve().parents[1]
 SRC = REPO / "ai-compiler-framework_amd" / "csrc" / "kernels" / "gemm.hip"
 
-# bf16 in; OUT 2 bf16 / 0 fp32; ACT 0 none, 2 GELU, 3 dGELU; waves; AKC, BKC
+# bf16 in; OUT 2 bf16 / 0 fp32; ACT 0 none, 2 GELU, 3 dGELU, 4 AdamW; waves; AKC, BKC
 KERNELS = [
     "gemm_nt_kernelILi2ELi2ELi0ELi256ELi256ELi2ELi2ELb1ELb1E",  # 4-wave, K-contiguous (8192^3)
     "gemm_nt_kernelILi2ELi2ELi2ELi256ELi256ELi2ELi4ELb1ELb1E",  # forward bias+GELU(+Z)
     "gemm_nt_kernelILi2ELi2ELi3ELi256ELi256ELi2ELi4ELb1ELb0E",  # dX dGELU, W read in place
     "gemm_nt_kernelILi2ELi0ELi0ELi256ELi256ELi2ELi4ELb0ELb0E",  # dW, both M/N-contiguous, fp32 out
+    "gemm_nt_kernelILi2ELi0ELi4ELi256ELi256ELi2ELi4ELb0ELb0E",  # dW with the AdamW epilogue
 ]
 
 

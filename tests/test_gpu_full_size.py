@@ -174,3 +174,31 @@ def test_c5_mlp_step_full_shape_forward_rows_and_adamw_bit_exact(C):
     assert np.array_equal(ex.value("wb.flat").cpu().view(torch.int16).numpy().view(np.uint16), Wr)
     assert np.isfinite(G).all() and np.abs(G).max() > 0
     ex.reset_graph()
+
+
+def test_c5_fused_optimizer_plan_bit_identical_at_full_shape(C):
+    """C5 at its full shape with AdamW fused into the four weight-gradient
+    GEMMs against the unfused plan (pinned to the oracle above), one replay
+    each from the same start: loss, all 67,125,248 parameters, both moments
+    and the bf16 shadow bit for bit."""
+    from aicf_hip import mlp
+
+    B, D, L = 8192, 4096, 4
+    outs = []
+    for fuse in (True, False):
+        ir, lowered, plan = mlp.build_mlp_mse(B, D, L, fuse_optimizer=fuse)
+        assert sum(it["op"] == "gemm_adamw" for it in lowered) == (L if fuse else 0)
+        ex = mlp.make_executor(ir, lowered, plan)
+        inputs, params = mlp.init_mlp_mse(B, D, L)
+        ex.build_env(inputs=inputs, params=params, reuse_static=False)
+        mlp.refresh_shadow(ex)
+        ex.capture(inputs=inputs, params=params, reuse_static=True)
+        ex.replay(1)
+        torch.cuda.synchronize()
+        outs.append({k: ex.value(k).cpu().clone() for k in ("loss", "flat.params", "opt.m.flat", "opt.v.flat",
+                                                             "wb.flat")})
+        ex.reset_graph()
+        del ex
+        torch.cuda.empty_cache()
+    for k in outs[0]:
+        assert torch.equal(outs[0][k], outs[1][k]), k

@@ -27,6 +27,47 @@ def test_mlp_mse_bf16_graph(C, B, D, L, nt):
     assert res["ok"], res
 
 
+def _run_plan(B, D, L, steps, **kw):
+    import torch
+
+    from aicf_hip import mlp
+
+    ir, lowered, plan = mlp.build_mlp_mse(B, D, L, **kw)
+    ex = mlp.make_executor(ir, lowered, plan)
+    inputs, params = mlp.init_mlp_mse(B, D, L, seed=3)
+    ex.build_env(inputs=inputs, params=params, reuse_static=False)
+    mlp.refresh_shadow(ex)
+    ex.capture(inputs=inputs, params=params, reuse_static=True)
+    losses = []
+    for _ in range(steps):
+        ex.replay(1)
+        torch.cuda.synchronize()
+        losses.append(float(ex.value("loss").item()))
+    out = {k: ex.value(k).cpu().clone() for k in ("flat.params", "opt.m.flat", "opt.v.flat", "wb.flat", "opt.step")}
+    ex.reset_graph()
+    return lowered, losses, out
+
+
+@pytest.mark.parametrize("B,D,L", [(256, 3072, 3), (512, 4096, 2)])
+def test_mlp_mse_fused_optimizer_plan_bit_identical(C, B, D, L):
+    """The plan with AdamW fused into the weight-gradient GEMMs (StageE)
+    against the unfused plan, three graph replays each from the same start:
+    every loss, parameter, moment and shadow element bit for bit (the
+    unfused plan is itself checked against the oracle above).  D >= 3072
+    puts the unfused fp32-output dW GEMM on the same 256 x 256 tiles."""
+    import torch
+
+    low_f, loss_f, out_f = _run_plan(B, D, L, 3, fuse_optimizer=True)
+    assert sum(it["op"] == "gemm_adamw" for it in low_f) == L
+    assert sum(it["op"] == "adamw_step" for it in low_f) == 1
+    low_u, loss_u, out_u = _run_plan(B, D, L, 3, fuse_optimizer=False)
+    assert not any(it["op"] == "gemm_adamw" for it in low_u)
+    assert loss_f == loss_u
+    for k in out_f:
+        assert torch.equal(out_f[k], out_u[k]), k
+    assert int(out_f["opt.step"].item()) == 3
+
+
 def test_mlp_mse_benchmark_shape_runs_finite(C):
     """Full benchmark shape (8192 x 4096, 4 layers): two replays, finite and
     decreasing loss, Adam moments populated (size-independent properties)."""

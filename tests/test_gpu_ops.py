@@ -30,6 +30,7 @@ GEMM = int.from_bytes(b"GEMM", "big")
 GPEL = int.from_bytes(b"GPEL", "big")
 GEPI = int.from_bytes(b"GEPI", "little")
 RRED = int.from_bytes(b"RRED", "little")
+GADW = int.from_bytes(b"GADW", "little")
 
 
 def g(a, dtype=None):
@@ -622,6 +623,81 @@ def test_gemm_neg_cases_raise(C):
                        [torch.empty((64, 81), device="cuda")])
     with pytest.raises(RuntimeError):
         C.op_call(int(C.OpKind.Gemm), [A.cpu(), B], [torch.empty((64, 80), device="cuda")])
+
+
+# (M, N, K, transA, transB): both operand layouts per side; 4096 x 2048 is the
+# smallest shape on which the plain fp32-output GEMM also takes 256 x 256
+# tiles; 17 x 16 tiles exceed the CU count (persistent workgroups).
+GADW_CASES = [(4096, 4096, 64, 1, 0), (4096, 4096, 192, 0, 1), (4096, 2048, 128, 0, 0),
+              (4096, 2048, 128, 1, 1), (17 * 256, 16 * 256, 128, 1, 0)]
+
+
+@pytest.mark.parametrize("M,N,K,ta,tb", GADW_CASES)
+def test_gemm_adamw_matches_gemm_then_adamw_bit_exact(C, M, N, K, ta, tb):
+    """gemm_adamw (weight-gradient GEMM with AdamW in its epilogue) against
+    the fp32-output GEMM followed by the streaming AdamW with bf16 shadow,
+    over two steps with different gradients and weight decay: parameters,
+    both moments and the shadow bit for bit.  The unfused gradient run
+    through the oracle's AdamW gives the same bits."""
+    r = rng(M + N + K + 2 * ta + tb)
+    s = 1.0 / np.sqrt(K)
+    As = [orc.bf16_bits_from_f32(r.uniform(-1, 1, (K, M) if ta else (M, K)).astype(np.float32)) for _ in range(2)]
+    Bs = [orc.bf16_bits_from_f32(r.uniform(-s, s, (N, K) if tb else (K, N)).astype(np.float32)) for _ in range(2)]
+    P0 = (0.02 * r.standard_normal((M, N))).astype(np.float32)
+    Pf, Mf, Vf = g(P0), torch.zeros((M, N), device="cuda"), torch.zeros((M, N), device="cuda")
+    Pu, Mu, Vu = g(P0), torch.zeros((M, N), device="cuda"), torch.zeros((M, N), device="cuda")
+    Wf = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    Wu = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    G = torch.empty((M, N), device="cuda")
+    sf = torch.zeros((), dtype=torch.int32, device="cuda")
+    su = torch.zeros((), dtype=torch.int32, device="cuda")
+    hp = (1e-3, 0.9, 0.999, 1e-8, 0.01)
+    Pc, Mc, Vc = P0.ravel().copy(), np.zeros(M * N, np.float32), np.zeros(M * N, np.float32)
+    for t in range(1, 3):
+        ga, gb = g(As[t - 1], torch.bfloat16), g(Bs[t - 1], torch.bfloat16)
+        C.launch_by_id("step_inc_v0", C.OpKind.StepInc, [sf], [sf])
+        C.launch_by_id("gemm_adamw_bf16_v0", C.OpKind.GemmAdamW, [ga, gb, Pf, Mf, Vf, sf], [Pf, Mf, Vf, Wf],
+                       GADW, struct.pack("<iifffff", ta, tb, *hp))
+        C.launch_by_id("step_inc_v0", C.OpKind.StepInc, [su], [su])
+        C.launch_by_id("gemm_bf16_mfma_f32out_v0", C.OpKind.Gemm, [ga, gb], [G], 0, struct.pack("<ii", ta, tb))
+        C.launch_by_id("adamw_step_f32_v1", C.OpKind.AdamStep, [Pu, G, Mu, Vu, su], [Pu, Mu, Vu, Wu], ADAM,
+                       struct.pack("<fffff", *hp))
+        Pc, Mc, Vc, Wc = orc.adamw(Pc, h(G).ravel(), Mc, Vc, t, *hp, shadow=True)
+        assert_bits_equal(h(Pf), h(Pu))
+        assert_bits_equal(h(Mf), h(Mu))
+        assert_bits_equal(h(Vf), h(Vu))
+        assert_bits_equal(h(Wf), h(Wu))
+        assert_bits_equal(h(Pf), Pc)
+        assert_bits_equal(h(Wf), Wc)
+    assert int(sf.item()) == 2
+
+
+def test_gemm_adamw_rejects_what_it_does_not_cover(C):
+    """Shapes off the 256 x 256 tiles, P/M/V outputs not aliasing the inputs,
+    and a NaN hyper-parameter are rejected on the host."""
+    def args(M, N, K):
+        A = torch.zeros((M, K), dtype=torch.bfloat16, device="cuda")
+        B = torch.zeros((K, N), dtype=torch.bfloat16, device="cuda")
+        P, Mm, V = (torch.zeros((M, N), device="cuda") for _ in range(3))
+        W = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+        st = torch.ones((), dtype=torch.int32, device="cuda")
+        return [A, B, P, Mm, V, st], [P, Mm, V, W]
+    pay = struct.pack("<iifffff", 0, 0, 1e-3, 0.9, 0.999, 1e-8, 0.0)
+    ins, outs = args(384, 256, 64)
+    with pytest.raises(RuntimeError):
+        C.launch_by_id("gemm_adamw_bf16_v0", C.OpKind.GemmAdamW, ins, outs, GADW, pay)
+    ins, outs = args(256, 256, 96)
+    with pytest.raises(RuntimeError):
+        C.launch_by_id("gemm_adamw_bf16_v0", C.OpKind.GemmAdamW, ins, outs, GADW, pay)
+    ins, outs = args(256, 256, 64)
+    with pytest.raises(RuntimeError):
+        C.launch_by_id("gemm_adamw_bf16_v0", C.OpKind.GemmAdamW, ins, [outs[0].clone()] + outs[1:], GADW, pay)
+    with pytest.raises(RuntimeError):
+        C.launch_by_id("gemm_adamw_bf16_v0", C.OpKind.GemmAdamW, ins, outs, GADW,
+                       struct.pack("<iifffff", 0, 0, float("nan"), 0.9, 0.999, 1e-8, 0.0))
+    C.launch_by_id("gemm_adamw_bf16_v0", C.OpKind.GemmAdamW, ins, outs, GADW, pay)
+    torch.cuda.synchronize()
+    assert float(outs[0].abs().max().item()) == 0.0  # zero gradient, zero decay: P stays 0
 
 
 @pytest.mark.parametrize("R,Ccols,dtype", [(64, 64, "bf16"), (4096, 8192, "bf16"), (100, 37, "f32"),
