@@ -560,11 +560,23 @@ __device__ __forceinline__ void nt_epilogue_staged(const NTParams& p,
   auto grow = [&](int pass, int pr) -> int64_t {
     return (int64_t)m0 + (pr / WROWS) * WTM + pass * WROWS + (pr % WROWS);
   };
+  // The thread index as a value the compiler cannot see through: the
+  // per-chunk offsets below are then computed here, in the epilogue.
+  // Otherwise they are loop-invariant for the persistent tile loop, get
+  // hoisted to the kernel start and spilled across the K loop, and each
+  // reload's vmcnt(0) wait also waits for the memory operation issued just
+  // before it, which serialises the epilogue's loads.
+  auto opaque_tid = [&]() -> int {
+    int t = threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
+  };
   // tile rows of this pass -> global matrix (row stride ld elements)
   auto copy_out = [&](int pass, void* dst, int64_t ld) {
+    const int tid = opaque_tid();
 #pragma unroll
     for (int k = 0; k < ROWS_PASS * CPR / NT; ++k) {
-      const int idx = threadIdx.x + k * NT;
+      const int idx = tid + k * NT;
       const int pr = idx / CPR, c = idx % CPR;
       const u16x8 x = *reinterpret_cast<const u16x8*>(tile + pr * ROWB + ((c ^ (pr & (CPR - 1))) * 16));
       *reinterpret_cast<u16x8*>((uint8_t*)dst + (grow(pass, pr) * ld + n0) * OB + c * 16) = x;
@@ -575,11 +587,12 @@ __device__ __forceinline__ void nt_epilogue_staged(const NTParams& p,
   // tile + 1024 q, i.e. physical chunks idx = 64 q + lane; the lane fetches
   // the logical chunk stored there.
   auto copy_in = [&](int pass, const void* src, int64_t ld) {
-    const int wave_id = threadIdx.x >> 6;
+    const int tid = opaque_tid();
+    const int wave_id = __builtin_amdgcn_readfirstlane(tid >> 6), ln = tid & 63;
 #pragma unroll
     for (int k = 0; k < ROWS_PASS * CPR / NT; ++k) {
       const int q = wave_id + k * NW;
-      const int idx = q * 64 + lane;
+      const int idx = q * 64 + ln;
       const int pr = idx / CPR, c = (idx % CPR) ^ (pr & (CPR - 1));
       __builtin_amdgcn_global_load_lds(
           (glb_void_t*)((const uint8_t*)src + (grow(pass, pr) * ld + n0) * OB + c * 16),
@@ -594,9 +607,10 @@ __device__ __forceinline__ void nt_epilogue_staged(const NTParams& p,
   auto adam_out = [&](int pass) {
     if constexpr (ACT == ACT_ADAMW) {
       const AdamWScalars sc = adamw_scalars(p.adam.step, p.adam.args);
+      const int tid = opaque_tid();
 #pragma unroll 4
       for (int k = 0; k < ROWS_PASS * CPR / NT; ++k) {
-        const int idx = threadIdx.x + k * NT;
+        const int idx = tid + k * NT;
         const int pr = idx / CPR, c = idx % CPR;
         const f32x4 g = *reinterpret_cast<const f32x4*>(tile + pr * ROWB + ((c ^ (pr & (CPR - 1))) * 16));
         const int64_t e = grow(pass, pr) * p.ldc + n0 + c * 4;

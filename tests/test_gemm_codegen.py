@@ -81,3 +81,15 @@ def test_k_loop_waits_for_its_loads_once_per_k_step(asm, kernel):
     assert any("s_barrier" in l for l in loop)
     loads = [l for l in loop if re.search(r"(buffer|global)_load\w*.*\blds\b", l)]
     assert loads, "the K loop issues the next stage's direct-to-LDS loads"
+
+
+# The 8-wave kernels: no scratch (spill) traffic at all.  A spilled value
+# reloaded in the epilogue comes with an `s_waitcnt vmcnt(0)` that also
+# waits for the epilogue's own loads and stores, one at a time (the dGELU
+# pre-activation load ran 16 round trips in series that way, +26 us per
+# 8192x4096x4096 GEMM).
+@pytest.mark.parametrize("kernel", [k for k in KERNELS if "ELi2ELi4E" in k])
+def test_eight_wave_kernels_do_not_spill(asm, kernel):
+    body = kernel_body(asm, kernel)
+    spills = [l.strip() for l in body if "scratch_" in l]
+    assert not spills, spills[:4]
