@@ -234,24 +234,34 @@ class PlannedExecutor:
     @torch.no_grad()
     def _execute_lowered(self, *, stream: int) -> None:
         warmup = os.getenv("AICF_WARMUP", "0") == "1"
+        for i in range(len(self._ops)):
+            self.launch_op(i, stream=stream, warmup=warmup)
+
+    @property
+    def ops(self) -> List[Tuple[str, int, Optional[str], List[int], List[int], Dict[str, Any]]]:
+        """The lowered ops as (op, kind, kernel_id, input vids, output vids, attrs)."""
+        return list(self._ops)
+
+    def launch_op(self, i: int, *, stream: int = 0, warmup: bool = False) -> None:
+        """Launches lowered op i on the bound tensors (one step of run())."""
+        op, kind, kid, ins, outs, attrs = self._ops[i]
         env = self.env
-        for i, (op, kind, kid, ins, outs, attrs) in enumerate(self._ops):
-            ins_t = [env[v] for v in ins]
-            outs_t = [env[v] for v in outs]
-            if self.opts.debug and i < self.opts.debug_limit:
-                print(f"[exec][#{i:03d}] {op} kind={kind} kernel_id={kid} attrs={attrs}")
-            if warmup and op == "step_inc":
-                outs_t[0].copy_(ins_t[0])
-                continue
-            if warmup and op in ("adam_step", "adamw_step", "gemm_adamw"):
-                attrs = dict(attrs, lr=0.0)
-            schema, payload = pack_attrs(op, attrs)
-            if kid is not None:
-                _C.launch_by_id(str(kid), _C.OpKind(kind), ins_t, outs_t, schema, payload, int(stream))
-            else:
-                if self.opts.require_kernel_id:
-                    raise RuntimeError(f"[exec] require_kernel_id=True but lowered op #{i} '{op}' has no kernel_id")
-                _C.op_call(kind, ins_t, outs_t, schema, payload, int(stream))
+        ins_t = [env[v] for v in ins]
+        outs_t = [env[v] for v in outs]
+        if self.opts.debug and i < self.opts.debug_limit:
+            print(f"[exec][#{i:03d}] {op} kind={kind} kernel_id={kid} attrs={attrs}")
+        if warmup and op == "step_inc":
+            outs_t[0].copy_(ins_t[0])
+            return
+        if warmup and op in ("adam_step", "adamw_step", "gemm_adamw"):
+            attrs = dict(attrs, lr=0.0)
+        schema, payload = pack_attrs(op, attrs)
+        if kid is not None:
+            _C.launch_by_id(str(kid), _C.OpKind(kind), ins_t, outs_t, schema, payload, int(stream))
+        else:
+            if self.opts.require_kernel_id:
+                raise RuntimeError(f"[exec] require_kernel_id=True but lowered op #{i} '{op}' has no kernel_id")
+            _C.op_call(kind, ins_t, outs_t, schema, payload, int(stream))
 
     @torch.no_grad()
     def run(self, *, inputs: Dict[str, Any], params: Dict[str, Any],

@@ -358,6 +358,63 @@ def bench_mlp(B, D, L, steps, warmup, dead_dx=True, fuse_optimizer=False):
             "finite": finite, "ops": len(lowered), "gemms": ngemm}
 
 
+STEP_GEMM_OPS = ("gemm", "gemm_epilogue", "gemm_adamw")
+# The step's GEMM launches by kernel instantiation (the template arguments in
+# the kernel name): role, launches per step (B=8192, D=4096, L=4) and
+# algorithmic MiB moved per launch.
+STEP_GEMM_ROLES = [
+    ("<2, 2, 2, 256, 256, 2, 4, true, true>", "fwd bias+GELU (+Z)", 3, 64 + 32 + 64 + 64),
+    ("<2, 2, 0, 256, 256, 2, 2, true, true>", "fwd bias (last layer)", 1, 64 + 32 + 64),
+    ("<2, 2, 3, 256, 256, 2, 4, true, false>", "dX with dGELU", 3, 64 + 32 + 64 + 64),
+    ("<2, 2, 0, 256, 256, 2, 4, true, false>", "dX (first layer)", 1, 64 + 32 + 64),
+    ("<2, 0, 4, 256, 256, 2, 4, false, false>", "dW + AdamW", 4, 64 + 64 + 3 * 64 * 2 + 32),
+]
+
+
+def gemm_role(op, attrs, n_out):
+    from aicf_hip.executor import epilogue_kind
+
+    if op == "gemm_adamw":
+        return "dW + AdamW"
+    if op == "gemm":
+        return "dX (first layer)"
+    kind = epilogue_kind(attrs)  # GEPI kinds: 5 dGELU, 3 bias+GELU, 1 bias
+    return {5: "dX with dGELU", 3: "fwd bias+GELU (+Z)"}.get(kind, "fwd bias (last layer)")
+
+
+def build_step(B, D, L, fuse_optimizer=True):
+    from aicf_hip import mlp
+
+    ir, lowered, plan = mlp.build_mlp_mse(B, D, L, fuse_optimizer=fuse_optimizer)
+    ex = mlp.make_executor(ir, lowered, plan)
+    inputs, params = mlp.init_mlp_mse(B, D, L)
+    ex.build_env(inputs=inputs, params=params, reuse_static=False)
+    mlp.refresh_shadow(ex)
+    return ex
+
+
+def step_gemm_times(ex, iters, warmup=2):
+    """Average ms per launch of each GEMM op of the step, HIP events on
+    torch's current stream around `iters` launches of the op on the step's own
+    tensors, after one eager pass over the step (so every activation holds
+    this step's values; the flat AdamW over the biases, which no GEMM reads,
+    is left out)."""
+    import torch
+
+    s = torch.cuda.current_stream()
+    for i, o in enumerate(ex.ops):
+        if o[0] != "adamw_step":
+            ex.launch_op(i, stream=s.cuda_stream)
+    torch.cuda.synchronize()
+    res = []
+    for i, (op, _kind, kid, _ins, outs, attrs) in enumerate(ex.ops):
+        if op not in STEP_GEMM_OPS:
+            continue
+        ms = time_launches(lambda i=i: ex.launch_op(i, stream=s.cuda_stream), iters, warmup, s)
+        res.append({"op": i, "kernel_id": kid, "role": gemm_role(op, attrs, len(outs)), "ms": ms})
+    return res
+
+
 def ex_stream():
     from aicf_cuda import _C
 
@@ -408,24 +465,26 @@ def cpu_baseline_mlp(B, D, L, sample_rows):
 
 # ------------------------------------------------------------------ main
 # ------------------------------------------------------------------ HBM traffic (rocprofv3 --pmc)
-TRAFFIC_FILE = REPO / "profiles" / "gemm_bias_gelu_8192x4096x4096_traffic.md"
+TRAFFIC_FILE = REPO / "profiles" / "step_gemms_8192x4096x4096_traffic.md"
 CALIB_ELEMS = 1 << 27          # calibration copy: 2^27 bf16 = 256 MiB read + 256 MiB written
 CALIB_KIB = CALIB_ELEMS * 2 / 1024
 
 
-def roofline_only(C, B, D, launches):
-    """The roofline kernel alone (launches x the step's bias+GELU GEMM with
-    saved pre-activation), then 3 calibration copies of known size; the
-    program profiled by the FETCH_SIZE / WRITE_SIZE passes."""
+def roofline_only(C, B, D, L, launches):
+    """The roofline kernel family alone: one eager pass over the step, then
+    `launches` launches of each of the step's GEMM ops on its own tensors,
+    then 3 calibration copies of known size; the program profiled by the
+    FETCH_SIZE / WRITE_SIZE passes."""
     import torch
 
-    g = bench_gemm(C, B, D, D, act_kind=3, iters=launches, warmup=1, save_preact=True)
+    ex = build_step(B, D, L)
+    t = step_gemm_times(ex, iters=launches, warmup=0)
     x = torch.ones(CALIB_ELEMS, device="cuda", dtype=torch.bfloat16)
     y = torch.empty_like(x)
     for _ in range(3):
         C.launch_by_id("copy_bf16_v0", C.OpKind.Copy, [x], [y], 0, b"")
     torch.cuda.synchronize()
-    log(f"[bench] roofline-only: {launches + 1} gemm launches, 3 calibration copies; {g}")
+    log(f"[bench] roofline-only: {len(t)} GEMM ops x ({launches} + 1) launches, 3 calibration copies; {t}")
 
 
 def mfma_report(counter_csv, trace_csv, pattern):
@@ -566,31 +625,33 @@ def pmc_mfma_compare_report(counter_csv, trace_csv):
 
 def pmc_report(fetch_csv, write_csv, mfma_csv=None, trace_csv=None):
     """Markdown summary of two rocprofv3 --pmc runs of --roofline-only
-    (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch).  Each counter is scaled
-    by calibration copy's expected/measured ratio.  With the MFMA counter run
+    (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch), per GEMM role of the step
+    and weighted by the role's launches per step.  Each counter is scaled by
+    the calibration copy's expected/measured ratio.  With the MFMA counter run
     and its kernel trace, also the MFMA utilisation and clock per dispatch."""
     import csv
     from statistics import mean
 
     def per_kernel(path, counter):
-        vals = {"gemm": [], "copy": []}
+        vals = {"copy": []}
         with open(path, newline="") as f:
             for row in csv.DictReader(f):
                 if row.get("Counter_Name") != counter:
                     continue
                 name = row.get("Kernel_Name", "")
-                key = "gemm" if "gemm_nt" in name else "copy" if "map1" in name else None
-                if key:
-                    vals[key].append(float(row["Counter_Value"]))
+                if "map1" in name:
+                    vals["copy"].append(float(row["Counter_Value"]))
+                    continue
+                for sig, role, _n, _mib in STEP_GEMM_ROLES:
+                    if "gemm_nt_kernel" in name and sig in name:
+                        vals.setdefault(role, []).append(float(row["Counter_Value"]))
         return vals
 
     fe, wr = per_kernel(fetch_csv, "FETCH_SIZE"), per_kernel(write_csv, "WRITE_SIZE")
     f_r = CALIB_KIB / mean(fe["copy"])
     f_w = CALIB_KIB / mean(wr["copy"])
-    fetch_b = mean(fe["gemm"]) * f_r * 1024
-    write_b = mean(wr["gemm"]) * f_w * 1024
     lines = [
-        "# HBM traffic of the step's bias+GELU GEMM (8192x4096x4096, bf16, Z saved)",
+        "# HBM traffic of the step's GEMM launches (bf16, B=8192, D=4096, L=4)",
         "",
         "Commands (GPU box, repo root):",
         "```",
@@ -602,20 +663,45 @@ def pmc_report(fetch_csv, write_csv, mfma_csv=None, trace_csv=None):
         "<mfma counter_collection.csv> <mfma kernel_trace.csv>",
         "```",
         "",
+        "`--roofline-only` builds the step, runs it once eagerly, launches each of its 12 GEMM ops 5 "
+        "more times on the step's own tensors, then 3 calibration copies.",
+        "",
         f"calibration copy (copy_bf16_v0, {CALIB_KIB:.0f} KiB read + written): "
         f"FETCH_SIZE {mean(fe['copy']):.0f} KiB -> factor {f_r:.4f}; "
         f"WRITE_SIZE {mean(wr['copy']):.0f} KiB -> factor {f_w:.4f}",
-        f"gemm dispatches: {len(fe['gemm'])} (fetch run), {len(wr['gemm'])} (write run)",
-        f"gemm FETCH_SIZE {mean(fe['gemm']):.0f} KiB/dispatch -> {fetch_b / 1e6:.1f} MB",
-        f"gemm WRITE_SIZE {mean(wr['gemm']):.0f} KiB/dispatch -> {write_b / 1e6:.1f} MB",
-        "algorithmic bytes: X 64 MiB + W 32 MiB read, Y 64 MiB + Z 64 MiB written = 224 MiB",
         "",
-        f"traffic_bytes_per_launch: {int(round(fetch_b + write_b))}",
+        "| role | launches/step | dispatches (fetch, write) | HBM read MB | HBM write MB | "
+        "algorithmic MB | ratio |",
+        "|---|---:|---:|---:|---:|---:|---:|",
+    ]
+    tot_b = tot_alg = 0.0
+    n_step = 0
+    for _sig, role, n, mib in STEP_GEMM_ROLES:
+        if role not in fe or role not in wr:
+            continue
+        rb = mean(fe[role]) * f_r * 1024
+        wb = mean(wr[role]) * f_w * 1024
+        alg = mib * 2.0 ** 20
+        lines.append(f"| {role} | {n} | {len(fe[role])}, {len(wr[role])} | {rb / 1e6:.1f} | {wb / 1e6:.1f} | "
+                     f"{alg / 1e6:.1f} | {(rb + wb) / alg:.3f} |")
+        tot_b += n * (rb + wb)
+        tot_alg += n * alg
+        n_step += n
+    lines += [
+        "",
+        "Algorithmic bytes per launch: operands read once and outputs written once (bf16 activations "
+        "64 MiB, weights 32 MiB; dW+AdamW: dY and h 64 MiB each, P/M/V fp32 64 MiB each read and "
+        "written, bf16 shadow 32 MiB).",
+        "",
+        f"step mean over {n_step} launches: {tot_b / n_step / 1e6:.1f} MB measured, "
+        f"{tot_alg / n_step / 1e6:.1f} MB algorithmic",
+        "",
+        f"traffic_bytes_per_launch: {int(round(tot_b / max(n_step, 1)))}",
         "",
     ]
     if mfma_csv and trace_csv:
         lines += [
-            "## MFMA utilisation and clock of the same GEMM",
+            "## MFMA utilisation and clock of the same GEMM launches",
             "",
             "```",
             "rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE SQ_INSTS_VALU_MFMA_MOPS_BF16 "
@@ -626,7 +712,9 @@ def pmc_report(fetch_csv, write_csv, mfma_csv=None, trace_csv=None):
             "MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE per XCD x 1024 SIMDs); clock = "
             "GRBM_GUI_ACTIVE per XCD / kernel duration; TFLOP/s from SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512.",
             "",
-        ] + mfma_report(mfma_csv, trace_csv, "gemm_nt") + [""]
+        ]
+        for sig, role, _n, _mib in STEP_GEMM_ROLES:
+            lines += [f"### {role}", ""] + mfma_report(mfma_csv, trace_csv, sig) + [""]
     print("\n".join(lines))
 
 
@@ -777,9 +865,10 @@ def stats_report(stats_csv, trace_csv, steps):
         "```",
         "",
         f"Process contents: warmup + {steps} timed replays of the captured step (batch 8192, 4 x 4096^2, "
-        "GELU, MSE, AdamW), then 23 launches of the forward bias+GELU GEMM for the roofline figure.",
+        "GELU, MSE, AdamW in the dW GEMMs' epilogue), then the roofline measurement: one eager pass "
+        "over the step and 12 launches of each of its 12 GEMM ops.",
         "`gemm_nt_kernel<IN, OUT, ACT, BM, BN, WM, WN, AKC, BKC>`: IN 2 = bf16; OUT 2 = bf16, 0 = fp32; "
-        "ACT 0 none, 2 GELU (+ pre-activation store), 3 dGELU; WM x WN waves; AKC/BKC operand "
+        "ACT 0 none, 2 GELU (+ pre-activation store), 3 dGELU, 4 AdamW; WM x WN waves; AKC/BKC operand "
         "K-contiguous (false: M/N-contiguous, read in place through transposing LDS reads).",
         "",
         "| kernel | calls | avg us | % time |",
@@ -802,6 +891,16 @@ def stats_report(stats_csv, trace_csv, steps):
         for i, r in enumerate(step):
             lines.append(f"| {i} | `{short(r['Kernel_Name'])}` | "
                          f"{(int(r['End_Timestamp']) - int(r['Start_Timestamp'])) / 1e3:.1f} |")
+        dur = lambda rs: [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3  # noqa: E731
+                          for rs_ in [rs] for r in rs_ if "gemm_nt_kernel" in r["Kernel_Name"]]
+        g_step, g_roof = dur(step), dur(trace[b:])
+        if g_step:
+            lines += ["", f"GEMM launches of the last replayed step: {len(g_step)}, mean "
+                      f"{sum(g_step) / len(g_step):.1f} us (the roofline's avg_ms is the same mean over "
+                      "the eager launches)."]
+        if g_roof:
+            lines.append(f"GEMM launches after the replays (roofline measurement): {len(g_roof)}, mean "
+                         f"{sum(g_roof) / len(g_roof):.1f} us.")
     lines.append("")
     print("\n".join(lines))
 
@@ -869,7 +968,7 @@ def main():
     B, D, L = args.batch, args.hidden, args.layers
     log(f"[bench] device={torch.cuda.get_device_name(0)} mlp B={B} D={D} L={L}")
     if args.roofline_only:
-        roofline_only(C, B, D, 5)
+        roofline_only(C, B, D, L, 5)
         return
     if args.streaming_only:
         streaming_only(C)
@@ -881,16 +980,28 @@ def main():
     res = bench_mlp(B, D, L, args.steps, args.warmup, fuse_optimizer=True)
     log(f"[bench] mlp {res}")
 
-    # dominant kernel: forward GEMM of the step (bias + GELU epilogue)
-    g = bench_gemm(C, B, D, D, act_kind=3, iters=20, warmup=3, save_preact=True)
+    # dominant kernel: gemm_nt_kernel, the step's 12 GEMM launches (~88% of
+    # the step), each 2*B*D*D flop; timed on the step's own tensors
+    ex = build_step(B, D, L)
+    times = step_gemm_times(ex, iters=10)
+    del ex
+    avg_ms = sum(t["ms"] for t in times) / len(times)
     flops = 2.0 * B * D * D
-    traffic = read_traffic() if (B, D) == (8192, 4096) else None
-    roofline = {"bound": "mfma", "achieved": round(g["tflops"], 2), "peak": PEAK_BF16_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(g["tflops"] / PEAK_BF16_TFLOPS, 4),
-                "traffic": traffic, "traffic_unit": "bytes/launch",
-                "kernel": "gemm_epilogue_bf16_mfma_v0 (bias+gelu, pre-activation saved)",
-                "shape": [B, D, D], "flops_per_launch": flops, "avg_ms": round(g["ms"], 4)}
-    log(f"[bench] roofline gemm {g}")
+    achieved = flops / (avg_ms * 1e-3) / 1e12
+    per_role = {}
+    for t in times:
+        per_role.setdefault(t["role"], []).append(t["ms"])
+    traffic = read_traffic() if (B, D, L) == (8192, 4096, 4) else None
+    roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                "traffic": traffic, "traffic_unit": "bytes/launch (mean over the step's GEMM launches)",
+                "kernel": f"gemm_nt_kernel: the step's {len(times)} GEMM launches "
+                          "(bias+GELU+Z, bias, dX+dGELU, dX, dW+AdamW epilogues)",
+                "shape": [B, D, D], "flops_per_launch": flops, "avg_ms": round(avg_ms, 4),
+                "per_role_avg_ms": {k: round(sum(v) / len(v), 4) for k, v in per_role.items()},
+                "measured": "HIP events around 10 launches of each GEMM op of the step on the step's "
+                            "own tensors (torch's current stream), after the timed replays"}
+    log(f"[bench] roofline step gemms {times}")
 
     comps = {}
     if not args.no_components:
