@@ -447,11 +447,14 @@ def test_gemm_bf16(C, M, N, K, ta, tb):
     assert orc.rel_err(h(of), ref) < 1e-5  # fp32 out: only accumulation-order error
 
 
-@pytest.mark.parametrize("K", [64, 192])
+@pytest.mark.parametrize("K", [64, 192, 576, 640])
 @pytest.mark.parametrize("ta,tb", [(False, True), (False, False), (True, True), (True, False)])
 def test_gemm_bf16_256_tiles_all_operand_layouts(C, ta, tb, K):
     """256x256-tile path with each operand K-contiguous or MN-contiguous
-    (the latter read through the transposing LDS loads)."""
+    (the latter read through the transposing LDS loads).  Both operands
+    K-contiguous with K <= 512 and a one-output epilogue take the 128x128
+    tiles instead; K = 576 and 640 (odd and even K-step counts) keep that
+    layout on the 256x256 tiles."""
     M = N = 4096
     r = rng(K + 2 * ta + tb)
     s = 1.0 / np.sqrt(K)
@@ -488,13 +491,15 @@ def test_gemm_bf16_dgelu_with_mn_contiguous_weight_256_tiles(C):
 
 
 @pytest.mark.parametrize("ta,tb,K", [(0, 1, 128), (1, 0, 128), (0, 0, 128), (1, 1, 128), (0, 1, 192),
-                                     (0, 0, 192)])
+                                     (0, 0, 192), (0, 1, 576), (0, 1, 640)])
 def test_gemm_bf16_persistent_tiles(C, ta, tb, K):
     """More 256x256 tiles (17 x 16 = 272) than CUs: one persistent workgroup
     per CU loops over its tiles, 16 of them take a second tile.  All operand
     layouts (fp32 output at 1e-5), bias+GELU with the pre-activation, and
     dGELU epilogues.  K = 128 and 192 (2 and 3 K-steps) put the pre-activation
-    rows loaded during the last K-step in either stage buffer."""
+    rows loaded during the last K-step in either stage buffer; with both
+    operands K-contiguous the fp32-output GEMM takes the 128x128 tiles up to
+    K = 512, so that layout also runs at K = 576 and 640 (9 and 10 K-steps)."""
     M, N = 17 * 256, 16 * 256
     r = rng(300 + 2 * ta + tb)
     s = 1.0 / np.sqrt(K)
