@@ -27,6 +27,11 @@ inline Status hip_status(hipError_t e, const char* what) {
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+// out[col] = sum over p < P of partial[p * N + col], fixed order (reduce.hip;
+// the second pass of the column sums, shared with the GEMM epilogue that
+// writes one partial row per 256-row tile).
+Status colsum_finish(const float* partial, float* out, int64_t P, int64_t N, void* stream);
+
 // Grid size for a 1-D launch: enough blocks to cover n items, at most cap.
 inline unsigned grid_1d(int64_t n, int threads, int64_t cap) {
   int64_t b = (n + threads - 1) / threads;

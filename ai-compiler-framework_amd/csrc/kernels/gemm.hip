@@ -77,6 +77,7 @@ struct GemmParams {
   int bias_f32;  // bias stored as fp32 (else in the output type)
   int tiles_m, tiles_n;
   GemmAdamW adam;  // ACT_ADAMW only
+  float* colsum;   // ACT_DGELU, bf16 out: per-tile column sums of C, row m0/256 of [M/256, N]
 };
 
 template <int IN>
@@ -462,6 +463,7 @@ struct NTParams {
   int bias_f32;
   int tiles_m, tiles_n;
   GemmAdamW adam;  // ACT_ADAMW only
+  float* colsum;   // see GemmParams::colsum
 };
 
 // Epilogue of the NT kernels.  Block (i, j) of the accumulators holds D[n][m];
@@ -582,6 +584,43 @@ __device__ __forceinline__ void nt_epilogue_staged(const NTParams& p,
       *reinterpret_cast<u16x8*>((uint8_t*)dst + (grow(pass, pr) * ld + n0) * OB + c * 16) = x;
     }
   };
+  // copy_out of the whole tile (bf16, 256 x 256, 8 waves) that also writes
+  // the tile's column sums of the stored (bf16-rounded) values to row m0/256
+  // of p.colsum.  A lane always handles the same 8-column chunk c = tid % 32,
+  // rows tid / 32 + 16 k (k = 0..15, summed in that order); lanes l and l + 32
+  // of a wave hold the same chunk and are added, then the 8 waves in order
+  // through LDS.
+  auto copy_out_colsum = [&]() {
+    const int tid = opaque_tid();
+    float cs[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) cs[e] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < ROWS_PASS * CPR / NT; ++k) {
+      const int idx = tid + k * NT;
+      const int pr = idx / CPR, c = idx % CPR;
+      const u16x8 x = *reinterpret_cast<const u16x8*>(tile + pr * ROWB + ((c ^ (pr & (CPR - 1))) * 16));
+      *reinterpret_cast<u16x8*>((uint8_t*)p.C + (grow(0, pr) * p.ldc + n0) * OB + c * 16) = x;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) cs[e] += bf16_to_f32(x[e]);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) cs[e] += __shfl_xor(cs[e], 32, 64);
+    __syncthreads();  // every lane has read its rows of the tile
+    float* red = reinterpret_cast<float*>(tile);  // [8 waves][256 columns]
+    const int w = tid >> 6, l = tid & 63;
+    if (l < 32) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) red[w * BN + l * 8 + e] = cs[e];
+    }
+    __syncthreads();
+    if (tid < BN) {
+      float s = red[tid];
+#pragma unroll
+      for (int ww = 1; ww < NW; ++ww) s += red[ww * BN + tid];
+      p.colsum[(int64_t)(m0 / BM) * p.N + n0 + tid] = s;
+    }
+  };
   // global matrix -> tile rows of this pass, straight into LDS (no VGPRs:
   // the accumulators are live).  Wave instruction q fills the 1 KB at
   // tile + 1024 q, i.e. physical chunks idx = 64 q + lane; the lane fetches
@@ -684,10 +723,16 @@ __device__ __forceinline__ void nt_epilogue_staged(const NTParams& p,
           put4(off, v);
         }
     __syncthreads();
-    if constexpr (ACT == ACT_ADAMW)
+    if constexpr (ACT == ACT_ADAMW) {
       adam_out(pass);
-    else
+    } else if constexpr (ACT == ACT_DGELU && OUT == OUT_BF16 && NPASS == 1 && CPR == 32 && NT == 512) {
+      if (p.colsum)
+        copy_out_colsum();
+      else
+        copy_out(pass, p.C, p.ldc);
+    } else {
       copy_out(pass, p.C, p.ldc);
+    }
     if (pass + 1 < NPASS) __syncthreads();
   }
 }
@@ -1075,7 +1120,7 @@ EpiAttr read_epi_attr(const void* attr) {
   return e;
 }
 
-bool epi_kind_valid(int k) { return k >= AICF_EPI_BIAS_RELU && k <= AICF_EPI_DGELU; }
+bool epi_kind_valid(int k) { return k >= AICF_EPI_BIAS_RELU && k <= AICF_EPI_DGELU_COLSUM; }
 
 // gemm/launcher.cu:116-148: A[M,K] . B[K,N] -> C[M,N] with positive strides.
 bool gemm_views_ok(const TensorDesc& A0, const TensorDesc& B0, const TensorDesc& C0, bool ta,
@@ -1138,6 +1183,7 @@ Status run_nt_act(const GemmParams& g, hipStream_t s) {
   p.tiles_m = p.M / BM;
   p.tiles_n = p.N / BN;
   p.adam = g.adam;
+  p.colsum = g.colsum;
   // 256 x 256 tiles hold one workgroup per CU: with more tiles than CUs, the
   // persistent configuration launches one workgroup per CU (a multiple of 8,
   // one per XCD slot) that loops over its tiles.
@@ -1224,6 +1270,12 @@ bool nt_eligible(const GemmParams& p, int BM, int BN, bool mn_ok) {
 
 template <int IN, int OUT>
 Status run_gemm(GemmParams& p, hipStream_t s) {
+  if (p.colsum) {  // dGELU with column sums: the 8-wave 256 x 256 bf16-output path only
+    if constexpr (OUT == OUT_BF16 && IN != IN_F32) {
+      if (p.act == ACT_DGELU && nt_eligible<IN, OUT>(p, 256, 256, true)) return run_nt256<IN, OUT>(p, s);
+    }
+    return Status::NotImplemented;
+  }
   if (p.act == ACT_ADAMW) {  // the fused optimizer epilogue exists on the 256 x 256 NT path only
     if constexpr (OUT == OUT_F32 && IN == IN_BF16) {
       if (nt_eligible<IN, OUT>(p, 256, 256, true)) return run_nt256<IN, OUT>(p, s);
@@ -1333,7 +1385,7 @@ GEMM_VARIANT(gemm_bf16_f32out, DType::kBF16, DType::kF32, false)
 // outputs (C) or (C, Zaux) for BIAS_GELU.
 bool epi_check(const TensorDesc* in, int ni, const TensorDesc* out, int no, const void* attr,
                DType din, DType dout, bool c_rowmajor) {
-  if (!in || !out || ni != 3 || (no != 1 && no != 2)) return false;
+  if (!in || !out || ni != 3 || no < 1 || no > 3) return false;
   if (dt(in[0]) != din || dt(in[1]) != din || dt(out[0]) != dout) return false;
   const EpiAttr e = read_epi_attr(attr);
   if (!epi_kind_valid(e.kind)) return false;
@@ -1341,6 +1393,19 @@ bool epi_check(const TensorDesc* in, int ni, const TensorDesc* out, int no, cons
   if (c_rowmajor && !is_contig_2d_rowmajor(out[0])) return false;
   const View2D C = view2d(out[0], false);
   const TensorDesc& X = in[2];
+  if (e.kind == AICF_EPI_DGELU_COLSUM) {
+    // outputs (C, db [N] f32, workspace [P >= M/256, N] f32), bf16 output
+    if (no != 3 || dout != DType::kBF16 || !is_contig_2d_rowmajor(out[0])) return false;
+    if (dt(X) != dout || X.rank != 2 || X.shape[0] != C.rows || X.shape[1] != C.cols) return false;
+    if (X.stride[1] != 1 || X.stride[0] <= 0) return false;
+    const TensorDesc &D = out[1], &W = out[2];
+    if (dt(D) != DType::kF32 || !D.contiguous || D.rank != 1 || D.shape[0] != C.cols) return false;
+    if (dt(W) != DType::kF32 || !W.contiguous || W.rank != 2 || W.shape[1] != C.cols ||
+        W.shape[0] < C.rows / 256)
+      return false;
+    return true;
+  }
+  if (no > 2) return false;
   if (e.kind == AICF_EPI_DGELU) {
     if (no != 1) return false;
     if (dt(X) != dout || X.rank != 2 || X.shape[0] != C.rows || X.shape[1] != C.cols) return false;
@@ -1373,6 +1438,7 @@ Status epi_launch_common(const TensorDesc* in, int no, TensorDesc* out, const vo
     case AICF_EPI_BIAS_GELU: p.act = ACT_GELU; break;
     case AICF_EPI_GELU: p.act = ACT_GELU; break;
     case AICF_EPI_DGELU: p.act = ACT_DGELU; break;
+    case AICF_EPI_DGELU_COLSUM: p.act = ACT_DGELU; break;
   }
   const bool with_bias = e.kind == AICF_EPI_BIAS_RELU || e.kind == AICF_EPI_BIAS ||
                          e.kind == AICF_EPI_BIAS_GELU;
@@ -1381,12 +1447,18 @@ Status epi_launch_common(const TensorDesc* in, int no, TensorDesc* out, const vo
     p.bias_s = X.stride[0];
     p.bias_f32 = dt(X) == DType::kF32 ? 1 : 0;
   }
-  if (e.kind == AICF_EPI_DGELU) {
+  if (e.kind == AICF_EPI_DGELU || e.kind == AICF_EPI_DGELU_COLSUM) {
     p.aux = const_cast<void*>(X.data);
     p.aux_rs = X.stride[0];
   } else if (no == 2) {
     p.aux = out[1].data;
     p.aux_rs = out[1].stride[0];
+  }
+  if (e.kind == AICF_EPI_DGELU_COLSUM) {
+    p.colsum = (float*)out[2].data;
+    const Status st = dispatch_gemm(p, din, dout, as_stream(stream));
+    if (st != Status::Ok) return st;
+    return colsum_finish(p.colsum, (float*)out[1].data, p.M / 256, p.N, stream);
   }
   return dispatch_gemm(p, din, dout, as_stream(stream));
 }

@@ -712,6 +712,12 @@ Status xent_launch(const TensorDesc* in, int ni, TensorDesc* out, int no, const 
 
 }  // namespace
 
+Status colsum_finish(const float* partial, float* out, int64_t P, int64_t N, void* stream) {
+  if (P < 1 || N < 1) return Status::InvalidArgument;
+  colsum_finish_kernel<<<(unsigned)((N + 63) / 64), 256, 0, as_stream(stream)>>>(partial, out, P, N);
+  return launch_status("colsum_finish");
+}
+
 // Direct C++ API counterpart of reduce_sum/api.hpp:6.
 Status reduce_sum_lastdim_f32(const float* dY, float* dB, int M, int N, void* stream) {
   if (!dY || !dB || M <= 0 || N <= 0) return Status::InvalidArgument;

@@ -92,7 +92,7 @@ def epilogue_kind(attrs: Dict[str, Any]) -> int:
     act = str(attrs.get("epilogue_act", "relu")).lower()
     bias = bool(attrs.get("epilogue_bias", True))
     if act == "dgelu":
-        return 5
+        return 6 if attrs.get("epilogue_colsum", False) else 5
     if act == "gelu":
         return 3 if bias else 4
     if act in ("none", ""):

@@ -12,6 +12,9 @@ compile-time rewrites of the reference pipeline:
   extended with gemm -> bias_add -> gelu (==> bias_gelu, keeping the
   pre-activation when a later gelu_bwd needs it) and gemm -> gelu_bwd
   (==> dgelu epilogue).
+* StageC' fuse_colsum_into_dgelu (not in the reference; opt-in): the column
+  sum (bias gradient) of a dGELU GEMM's output is taken in that GEMM's
+  epilogue (GEPI kind 6) instead of by a reduce_sum over the stored tensor.
 * StageE  fuse_optimizer_into_gemms (not in the reference; opt-in): a
   weight-gradient GEMM whose output only feeds the flat AdamW step becomes
   gemm_adamw (AdamW applied in the GEMM's epilogue, no fp32 gradient in
@@ -480,16 +483,64 @@ def fuse_optimizer_into_gemms(ir: IRGraph, lowered: Lowered) -> Lowered:
     return out
 
 
+def fuse_colsum_into_dgelu(ir: IRGraph, lowered: Lowered) -> Lowered:
+    """StageC' (not in the reference): reduce_sum(dz) -> (db, workspace) over
+    the output of a bf16 dGELU gemm_epilogue becomes part of that GEMM (GEPI
+    kind 6: outputs dz, db, workspace).  Only where the GEMM runs on the
+    256 x 256 tiles that carry the column sums (bf16 2-D operands, M and N
+    multiples of 256, K of 64) and the reduce_sum has a [P >= M/256, N] fp32
+    workspace; db then sums one partial per 256-row tile instead of the
+    two-pass column sum's order (equal to fp32 rounding)."""
+    kind = lambda it: str(it.get("op", "")).strip().lower()  # noqa: E731
+    producer = {}
+    for i, it in enumerate(lowered):
+        if kind(it) == "gemm_epilogue" and len(it["outputs"]) == 1 and \
+                str(it.get("attrs", {}).get("epilogue_act", "")).lower() == "dgelu":
+            producer[int(it["outputs"][0])] = i
+    out = [dict(it, inputs=list(it["inputs"]), outputs=list(it["outputs"]), attrs=dict(it.get("attrs", {})))
+           for it in lowered]
+    drop = set()
+    for j, it in enumerate(out):
+        if kind(it) != "reduce_sum" or len(it["inputs"]) != 1 or len(it["outputs"]) != 2:
+            continue
+        if int(it.get("attrs", {}).get("axis", 0)) != 0:
+            continue
+        dz = int(it["inputs"][0])
+        i = producer.get(dz)
+        if i is None or i > j:
+            continue
+        g = out[i]
+        a, b = (int(x) for x in g["inputs"][:2])
+        ta, tb = bool(g["attrs"].get("transA", False)), bool(g["attrs"].get("transB", False))
+        sa, sb = ir.values[a].shape, ir.values[b].shape
+        if len(sa) != 2 or len(sb) != 2 or not all("bfloat16" in str(ir.values[v].dtype) for v in (a, b, dz)):
+            continue
+        M, K = (sa[1], sa[0]) if ta else (sa[0], sa[1])
+        N = sb[0] if tb else sb[1]
+        db, ws = (int(x) for x in it["outputs"])
+        wsh = ir.values[ws].shape
+        if M % 256 or N % 256 or K % 64 or len(wsh) != 2 or wsh[1] != N or wsh[0] < M // 256:
+            continue
+        if tuple(ir.values[db].shape) != (N,) or "float32" not in str(ir.values[db].dtype):
+            continue
+        g["outputs"] = [dz, db, ws]
+        g["attrs"]["epilogue_colsum"] = True
+        drop.add(j)
+    return [it for j, it in enumerate(out) if j not in drop]
+
+
 def compile_lowered(ir: IRGraph, *, fuse: bool = True, fuse_bias: bool = False,
                     nt_layout: Any = False, nt_min_flops: float = 2.0 ** 30,
-                    fuse_optimizer: bool = False) -> Lowered:
-    """StageA -> StageC -> (StageD) -> (StageE) -> StageB.  nt_layout: False
-    (no StageD), True / "all" (transpose every M/N-contiguous 16-bit operand)
-    or "cost" (transpose only where that is cheaper than reading it in
-    place); fuse_optimizer: StageE."""
+                    fuse_optimizer: bool = False, fuse_colsum: bool = False) -> Lowered:
+    """StageA -> StageC -> (StageC') -> (StageD) -> (StageE) -> StageB.
+    nt_layout: False (no StageD), True / "all" (transpose every M/N-contiguous
+    16-bit operand) or "cost" (transpose only where that is cheaper than
+    reading it in place); fuse_colsum: StageC'; fuse_optimizer: StageE."""
     low = lower_to_backend_ops(ir)
     if fuse:
         low = fuse_gemm_epilogue(ir, low, fuse_bias=fuse_bias)
+    if fuse and fuse_colsum:
+        low = fuse_colsum_into_dgelu(ir, low)
     if nt_layout:
         policy = "all" if nt_layout is True else str(nt_layout)
         low = normalize_gemm_layout(ir, low, min_flops=nt_min_flops, policy=policy)

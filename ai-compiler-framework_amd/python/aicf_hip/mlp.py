@@ -119,7 +119,7 @@ def build_mlp_mse(B: int = 8192, D: int = 4096, L: int = 4, *, lr: float = 1e-3,
                   beta1: float = 0.9, beta2: float = 0.999, eps: float = 1e-8,
                   weight_decay: float = 0.0, dead_dx: bool = True, nt_layout="cost",
                   nt_min_flops: float = 2.0 ** 30, fuse_optimizer: bool = False,
-                  device: str = "cuda:0"):
+                  fuse_colsum: bool = False, device: str = "cuda:0"):
     """bf16 activations/weights, fp32 master parameters in one flat buffer.
     The GEMM kernel reads M/N-contiguous operands in place; StageD
     (nt_layout) may still insert explicit transposes: "cost" where a
@@ -127,7 +127,9 @@ def build_mlp_mse(B: int = 8192, D: int = 4096, L: int = 4, *, lr: float = 1e-3,
     in-place cost of this kernel), True for every such operand, False for
     none.  fuse_optimizer: each weight-gradient GEMM applies AdamW to its
     layer's weights in its epilogue (StageE); the flat step then covers the
-    biases only."""
+    biases only.  fuse_colsum: the bias gradients of the hidden layers are
+    column-summed in the epilogue of the dGELU GEMM that produces their
+    input (StageC')."""
     ir = IRGraph(name=f"mlp_mse_{B}x{D}x{L}")
     lay = FlatLayout(D, L)
     nv = lambda n, s, dt=F32, view=None: ir.new_value(name=n, shape=s, dtype=dt,  # noqa: E731
@@ -178,7 +180,7 @@ def build_mlp_mse(B: int = 8192, D: int = 4096, L: int = 4, *, lr: float = 1e-3,
             attrs={"lr": lr, "beta1": beta1, "beta2": beta2, "eps": eps,
                    "weight_decay": weight_decay})
     lowered = compile_lowered(ir, fuse_bias=True, nt_layout=nt_layout, nt_min_flops=nt_min_flops,
-                              fuse_optimizer=fuse_optimizer)
+                              fuse_optimizer=fuse_optimizer, fuse_colsum=fuse_colsum)
     plan = build_binding_plan(ir, opts=PlanOptions(param_names={"flat.params"}))
     return ir, lowered, plan
 
@@ -290,7 +292,7 @@ def check_mlp_small(device: str = "cuda:0", verbose: bool = False, B=64, din=784
 
 
 def check_mlp_mse_small(B: int = 256, D: int = 256, L: int = 4, device: str = "cuda:0",
-                        steps: int = 3, nt_layout=False) -> Dict[str, object]:
+                        steps: int = 3, nt_layout=False, fuse_colsum: bool = False) -> Dict[str, object]:
     """Runs the bf16 MSE MLP (same graph and kernels as the benchmark, smaller
     shape) eagerly for one step and as a captured graph for `steps`-1 more,
     and checks each step against the CPU oracle: an fp64 chain that rounds
@@ -301,7 +303,8 @@ def check_mlp_mse_small(B: int = 256, D: int = 256, L: int = 4, device: str = "c
 
     # nt_min_flops=0: with nt_layout, take the transpose + NT-kernel route at
     # every size
-    ir, lowered, plan = build_mlp_mse(B, D, L, device=device, nt_layout=nt_layout, nt_min_flops=0)
+    ir, lowered, plan = build_mlp_mse(B, D, L, device=device, nt_layout=nt_layout, nt_min_flops=0,
+                                      fuse_colsum=fuse_colsum)
     lay = FlatLayout(D, L)
     ex = make_executor(ir, lowered, plan, device)
     inputs, params = init_mlp_mse(B, D, L, seed=1, device=device)

@@ -324,12 +324,13 @@ def bench_adam(C, n=1 << 28, steps=10):
 
 
 # ------------------------------------------------------------------ MLP
-def bench_mlp(B, D, L, steps, warmup, dead_dx=True, fuse_optimizer=False):
+def bench_mlp(B, D, L, steps, warmup, dead_dx=True, fuse_optimizer=False, fuse_colsum=False):
     import torch
 
     from aicf_hip import mlp
 
-    ir, lowered, plan = mlp.build_mlp_mse(B, D, L, dead_dx=dead_dx, fuse_optimizer=fuse_optimizer)
+    ir, lowered, plan = mlp.build_mlp_mse(B, D, L, dead_dx=dead_dx, fuse_optimizer=fuse_optimizer,
+                                          fuse_colsum=fuse_colsum)
     ex = mlp.make_executor(ir, lowered, plan)
     inputs, params = mlp.init_mlp_mse(B, D, L)
     ex.build_env(inputs=inputs, params=params, reuse_static=False)
@@ -378,14 +379,14 @@ def gemm_role(op, attrs, n_out):
         return "dW + AdamW"
     if op == "gemm":
         return "dX (first layer)"
-    kind = epilogue_kind(attrs)  # GEPI kinds: 5 dGELU, 3 bias+GELU, 1 bias
-    return {5: "dX with dGELU", 3: "fwd bias+GELU (+Z)"}.get(kind, "fwd bias (last layer)")
+    kind = epilogue_kind(attrs)  # GEPI kinds: 5 dGELU, 6 dGELU + column sums, 3 bias+GELU, 1 bias
+    return {5: "dX with dGELU", 6: "dX with dGELU", 3: "fwd bias+GELU (+Z)"}.get(kind, "fwd bias (last layer)")
 
 
-def build_step(B, D, L, fuse_optimizer=True):
+def build_step(B, D, L, fuse_optimizer=True, fuse_colsum=True):
     from aicf_hip import mlp
 
-    ir, lowered, plan = mlp.build_mlp_mse(B, D, L, fuse_optimizer=fuse_optimizer)
+    ir, lowered, plan = mlp.build_mlp_mse(B, D, L, fuse_optimizer=fuse_optimizer, fuse_colsum=fuse_colsum)
     ex = mlp.make_executor(ir, lowered, plan)
     inputs, params = mlp.init_mlp_mse(B, D, L)
     ex.build_env(inputs=inputs, params=params, reuse_static=False)
@@ -977,7 +978,7 @@ def main():
         vendor_compare(C)
         return
 
-    res = bench_mlp(B, D, L, args.steps, args.warmup, fuse_optimizer=True)
+    res = bench_mlp(B, D, L, args.steps, args.warmup, fuse_optimizer=True, fuse_colsum=True)
     log(f"[bench] mlp {res}")
 
     # dominant kernel: gemm_nt_kernel, the step's 12 GEMM launches (~88% of
@@ -1050,13 +1051,13 @@ def main():
                 "frac": round(tm["tflops"] / PEAK_BF16_TFLOPS, 4), "ms": round(tm["ms"], 4),
                 "note": "torch.matmul (hipBLASLt) in the same process, reference line only"}
             log(f"[bench] torch.matmul {M_}x{N_}x{K_} {tm}")
-        uf = bench_mlp(B, D, L, args.steps, args.warmup, fuse_optimizer=False)
-        comps["mlp_step_unfused_optimizer"] = {
+        uf = bench_mlp(B, D, L, args.steps, args.warmup, fuse_optimizer=False, fuse_colsum=False)
+        comps["mlp_step_reference_op_split"] = {
             "value": round(uf["steps_per_s"], 3), "unit": "steps/s", "ms": round(uf["ms"], 4),
-            "note": "same step with the reference's op split: dW GEMMs write the fp32 gradient, "
-                    "one streaming AdamW launch over all parameters; bit-identical results"}
-        log(f"[bench] mlp unfused optimizer {uf}")
-        nd = bench_mlp(B, D, L, args.steps, args.warmup, dead_dx=False, fuse_optimizer=True)
+            "note": "same step with the reference's op split: dW GEMMs write the fp32 gradient, one "
+                    "streaming AdamW over all parameters, bias gradients by separate column sums"}
+        log(f"[bench] mlp reference op split {uf}")
+        nd = bench_mlp(B, D, L, args.steps, args.warmup, dead_dx=False, fuse_optimizer=True, fuse_colsum=True)
         comps["mlp_step_without_dead_input_dx"] = {
             "value": round(nd["steps_per_s"], 3), "unit": "steps/s", "ms": round(nd["ms"], 4),
             "gemms_per_step": nd["gemms"],
@@ -1093,6 +1094,7 @@ def main():
                    "hidden": D, "layers": L, "activation": "gelu_tanh", "loss": "mse",
                    "optimizer": "adamw(lr=1e-3, b=(0.9,0.999), eps=1e-8)",
                    "optimizer_in_dw_gemm_epilogue": True,
+                   "bias_grads_in_dgelu_gemm_epilogue": True,
                    "gemms_per_step": res["gemms"], "ops_per_step": res["ops"],
                    "parallelism": "single_gpu"},
         "roofline": roofline,

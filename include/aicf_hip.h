@@ -99,6 +99,8 @@ extern "C" {
 #define AICF_EPI_BIAS_GELU 3  /* bias then gelu_tanh; optional 2nd output keeps the pre-activation */
 #define AICF_EPI_GELU 4       /* gelu_tanh, input 2 ignored */
 #define AICF_EPI_DGELU 5      /* out = acc * gelu_tanh'(Z), input 2 is Z[M,N] */
+#define AICF_EPI_DGELU_COLSUM 6 /* as 5, plus outputs db[N] f32 = column sums of out, and a f32
+                                   workspace [P, N] with P >= M/256 (no reference counterpart) */
 
 /*
  * Replaces tensor_desc.hpp:88-158 (struct TensorDesc).  Field order, types

@@ -128,18 +128,21 @@ def test_c4_gemm_epilogue_full_size_sampled_rows(C, dt, M, N, K, act):
     assert orc.rel_err(_host(Y[rows]), ref) < tol
 
 
-def test_c5_mlp_step_full_shape_forward_rows_and_adamw_bit_exact(C):
+@pytest.mark.parametrize("colsum", [False, True])
+def test_c5_mlp_step_full_shape_forward_rows_and_adamw_bit_exact(C, colsum):
     """C5 at its full shape (batch 8192, 4 x 4096^2, GELU, MSE, AdamW) replayed
     once from its captured graph.  Forward rows are independent: 16 sampled
     rows of every stored activation (z_i, h_i, y) against an fp64 chain from
     the same bf16 inputs and weights that rounds each stored tensor to bf16.
     The optimizer is elementwise: the oracle's AdamW applied to the GPU's own
     gradients over all 67,125,248 parameters must reproduce the updated fp32
-    parameters, both moments and the bf16 shadow bit for bit."""
+    parameters, both moments and the bf16 shadow bit for bit.  Every bias
+    gradient matches the fp64 column sum of the stored output gradient it
+    comes from (with colsum: taken in the dGELU GEMMs' epilogue)."""
     from aicf_hip import mlp
 
     B, D, L = 8192, 4096, 4
-    ir, lowered, plan = mlp.build_mlp_mse(B, D, L)
+    ir, lowered, plan = mlp.build_mlp_mse(B, D, L, fuse_colsum=colsum)
     ex = mlp.make_executor(ir, lowered, plan)
     inputs, params = mlp.init_mlp_mse(B, D, L)
     ex.build_env(inputs=inputs, params=params, reuse_static=False)
@@ -173,6 +176,10 @@ def test_c5_mlp_step_full_shape_forward_rows_and_adamw_bit_exact(C):
     assert np.array_equal(ex.value("opt.v.flat").cpu().numpy(), Vr)
     assert np.array_equal(ex.value("wb.flat").cpu().view(torch.int16).numpy().view(np.uint16), Wr)
     assert np.isfinite(G).all() and np.abs(G).max() > 0
+    # bias gradients: column sums of the stored (bf16) output gradient of each layer
+    for i in range(1, L + 1):
+        dz = _host(ex.value("dY" if i == L else f"d_z{i}")).astype(np.float64).sum(axis=0)
+        assert orc.rel_err(G[lay.b_off(i):lay.b_off(i) + D], dz) < 1e-5, i
     ex.reset_graph()
 
 

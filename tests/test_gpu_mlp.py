@@ -17,13 +17,20 @@ def test_mlp_xent_fp32_reference_config(C):
     assert res["ok"], res
 
 
-@pytest.mark.parametrize("B,D,L,nt", [(256, 256, 4, True), (512, 384, 3, True), (256, 256, 2, False)])
-def test_mlp_mse_bf16_graph(C, B, D, L, nt):
+@pytest.mark.parametrize("B,D,L,nt,colsum", [(256, 256, 4, True, False), (512, 384, 3, True, False),
+                                             (256, 256, 2, False, False), (256, 256, 4, False, True),
+                                             (512, 512, 3, False, True)])
+def test_mlp_mse_bf16_graph(C, B, D, L, nt, colsum):
     """The benchmark's bf16 GELU/MSE/AdamW graph at a reduced shape, with the
-    transpose + NT-GEMM lowering (nt) and with the general GEMM kernel."""
+    transpose + NT-GEMM lowering (nt) and with the general GEMM kernel; with
+    colsum the hidden layers' bias gradients come from the dGELU GEMMs'
+    epilogue (GEPI kind 6)."""
     from aicf_hip import mlp
 
-    res = mlp.check_mlp_mse_small(B, D, L, nt_layout=nt)
+    if colsum:
+        ir, lowered, _ = mlp.build_mlp_mse(B, D, L, fuse_colsum=True)
+        assert sum(bool(it["attrs"].get("epilogue_colsum")) for it in lowered) == L - 1
+    res = mlp.check_mlp_mse_small(B, D, L, nt_layout=nt, fuse_colsum=colsum)
     assert res["ok"], res
 
 

@@ -618,6 +618,51 @@ def test_gemm_epilogue_bf16_gelu_aux_and_dgelu(C, M, N, K):
     assert orc.rel_err(orc.bf16_bits_to_f32(h(dz)).reshape(M, K), ref) < 1e-2
 
 
+@pytest.mark.parametrize("M,N,K,ta,tb", [(512, 768, 128, 0, 0), (4096, 4096, 64, 0, 1),
+                                         (17 * 256, 16 * 256, 128, 0, 0), (1024, 512, 320, 1, 0)])
+def test_gemm_dgelu_with_column_sums(C, M, N, K, ta, tb):
+    """GEPI kind 6: the dGELU GEMM that also column-sums its stored output
+    (one partial per 256-row tile, then a fixed-order finish).  The output is
+    the same bits as kind 5; db against the fp64 column sum of that stored
+    bf16 output; the workspace may have more rows than M/256."""
+    r = rng(M + N + K)
+    A = orc.bf16_bits_from_f32(r.standard_normal((K, M) if ta else (M, K)).astype(np.float32))
+    B = orc.bf16_bits_from_f32(r.uniform(-0.1, 0.1, (N, K) if tb else (K, N)).astype(np.float32))
+    Z = orc.bf16_bits_from_f32(r.standard_normal((M, N)).astype(np.float32))
+    ga, gb, gz = g(A, torch.bfloat16), g(B, torch.bfloat16), g(Z, torch.bfloat16)
+    d5 = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    C.launch_by_id("gemm_epilogue_bf16_mfma_v0", C.OpKind.GemmEpilogue, [ga, gb, gz], [d5], GEPI,
+                   struct.pack("<iii", ta, tb, 5))
+    d6 = torch.empty_like(d5)
+    db = torch.empty(N, device="cuda")
+    ws = torch.full((M // 256 + 3, N), float("nan"), device="cuda")
+    C.launch_by_id("gemm_epilogue_bf16_mfma_v0", C.OpKind.GemmEpilogue, [ga, gb, gz], [d6, db, ws], GEPI,
+                   struct.pack("<iii", ta, tb, 6))
+    assert torch.equal(d5, d6)
+    ref = orc.bf16_bits_to_f32(h(d6)).reshape(M, N).astype(np.float64).sum(axis=0)
+    assert orc.rel_err(h(db), ref) < 1e-5
+    assert np.isnan(h(ws)[M // 256:]).all()  # rows past M/256 untouched
+
+
+def test_gemm_dgelu_column_sums_rejects(C):
+    """Kind 6 needs the bf16 256 x 256 path and a [>= M/256, N] fp32 workspace."""
+    def call(M, N, K, P):
+        A = torch.zeros((M, K), dtype=torch.bfloat16, device="cuda")
+        B = torch.zeros((K, N), dtype=torch.bfloat16, device="cuda")
+        Z = torch.zeros((M, N), dtype=torch.bfloat16, device="cuda")
+        C.launch_by_id("gemm_epilogue_bf16_mfma_v0", C.OpKind.GemmEpilogue, [A, B, Z],
+                       [torch.empty((M, N), dtype=torch.bfloat16, device="cuda"), torch.empty(N, device="cuda"),
+                        torch.empty((P, N), device="cuda")], GEPI, struct.pack("<iii", 0, 0, 6))
+    with pytest.raises(RuntimeError):
+        call(512, 256, 64, 1)      # workspace rows < M/256
+    with pytest.raises(RuntimeError):
+        call(384, 256, 64, 2)      # M not a multiple of 256
+    with pytest.raises(RuntimeError):
+        call(512, 256, 96, 2)      # K not a multiple of 64
+    call(512, 256, 64, 2)
+    torch.cuda.synchronize()
+
+
 def test_gemm_neg_cases_raise(C):
     A = torch.zeros((64, 48), device="cuda")
     B = torch.zeros((48, 80), device="cuda")
