@@ -108,8 +108,12 @@ template <int UNROLL, bool SHADOW>
 __global__ __launch_bounds__(256) void adamw_vec4_kernel(
     const float* __restrict__ P, const float* __restrict__ G, const float* __restrict__ M,
     const float* __restrict__ V, float* __restrict__ Pout, float* __restrict__ Mout,
-    float* __restrict__ Vout, uint16_t* __restrict__ Wb, int64_t n4, AdamWArgs a,
+    float* __restrict__ Vout, uint16_t* __restrict__ Wb, int64_t n, AdamWArgs a,
     const int32_t* __restrict__ stepp) {
+  // vectors 0 .. n4-1; the thread that would take vector n4 updates the
+  // n % 4 remaining elements one by one (the same expression), so one launch
+  // covers any length
+  const int64_t n4 = n / 4;
   // the bias corrections (two fp64 pow) are computed by one wave per block
   __shared__ float sh[2];
   if (threadIdx.x < 64) {
@@ -151,6 +155,15 @@ __global__ __launch_bounds__(256) void adamw_vec4_kernel(
       __builtin_nontemporal_store(m[u], reinterpret_cast<f32x4*>(Mout) + i);
       __builtin_nontemporal_store(v[u], reinterpret_cast<f32x4*>(Vout) + i);
       if (SHADOW) __builtin_nontemporal_store(w, reinterpret_cast<u16x4*>(Wb) + i);
+    } else if (i == n4) {
+      for (int64_t e = 4 * n4; e < n; ++e) {
+        float pp = P[e], mm = M[e], vv = V[e];
+        adamw_elem(pp, G[e], mm, vv, s, a);
+        Pout[e] = pp;
+        Mout[e] = mm;
+        Vout[e] = vv;
+        if (SHADOW) Wb[e] = f32_to_bf16(pp);
+      }
     }
   }
 }
@@ -307,17 +320,15 @@ Status adamw_launch(const TensorDesc* in, int ni, TensorDesc* out, int no, const
   hipStream_t s = as_stream(stream);
   int64_t done = 0;
   if (all_aligned16({P, G, M, V, Po, Mo, Vo}) && (!Wb || aligned(Wb, 8))) {
-    const int64_t n4 = n / 4;
-    if (n4 > 0) {
-      const unsigned blocks = (unsigned)((n4 + 256 * kAdamUnroll - 1) / (256 * kAdamUnroll));
-      if (Wb)
-        adamw_vec4_kernel<kAdamUnroll, true><<<blocks, 256, 0, s>>>(P, G, M, V, Po, Mo, Vo, Wb, n4,
-                                                                     a, step);
-      else
-        adamw_vec4_kernel<kAdamUnroll, false><<<blocks, 256, 0, s>>>(P, G, M, V, Po, Mo, Vo,
-                                                                      nullptr, n4, a, step);
-    }
-    done = n4 * 4;
+    const int64_t slots = n / 4 + (n % 4 ? 1 : 0);  // vectors, plus the tail's thread
+    const unsigned blocks = (unsigned)((slots + 256 * kAdamUnroll - 1) / (256 * kAdamUnroll));
+    if (Wb)
+      adamw_vec4_kernel<kAdamUnroll, true><<<blocks, 256, 0, s>>>(P, G, M, V, Po, Mo, Vo, Wb, n, a,
+                                                                   step);
+    else
+      adamw_vec4_kernel<kAdamUnroll, false><<<blocks, 256, 0, s>>>(P, G, M, V, Po, Mo, Vo, nullptr,
+                                                                    n, a, step);
+    done = n;
   }
   if (done < n) {
     const unsigned blocks = (unsigned)((n - done + 255) / 256);
