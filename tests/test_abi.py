@@ -217,6 +217,34 @@ def test_dispatch_neg_cases(lib):
     assert _call(lib, 7, [Pp, Gp], [Gp]) == INV
 
 
+def test_zero_size_inputs_follow_the_reference(lib):
+    """Zero-element tensors get the reference's statuses, decided on the host:
+    copy, grad_zero and Adam accept n = 0 and return Ok without a launch
+    (copy/launcher.cu:81,110; grad_zero/launcher.cu:79,107;
+    adam_step/launcher.cu:174-175,211-212); the other ops require a positive
+    size, so no variant supports the call (relu/launcher.cu:131-132,
+    add/launcher.cu:108, bias_add/launcher.cu:142-150,
+    reduce_sum/launcher.cu:44-53, mse_grad/launcher.cu:131,
+    relu_bwd/launcher.cu:110, sgd_step/launcher.cu:66-70,
+    step_inc/launcher.cu:105, gemm/launcher.cu:141)."""
+    adam = int.from_bytes(b"ADAM", "little")
+    pay = struct.pack("<ffff", 1e-3, 0.9, 0.999, 1e-8)
+    sc = d((), F32)
+    z = lambda k=0, dt=F32: d((0,), dt, FAKE + k * 4096)  # noqa: E731
+    assert _call(lib, 8, [z(0)], [z(1)]) == OK                                   # copy
+    assert _call(lib, 9, [z(0)], [z(0)]) == OK                                   # grad_zero
+    assert _call(lib, 10, [z(0), z(1), z(2), z(3), sc, sc], [z(0), z(2), z(3)], adam, pay) == OK
+    assert _call(lib, 1, [z()], [z()]) == NOTIMPL                                # relu
+    assert _call(lib, 0, [z(), z(1)], [z(2)]) == NOTIMPL                         # add
+    assert _call(lib, 3, [d((0, 8)), d((8,))], [d((0, 8))]) == NOTIMPL          # bias_add
+    assert _call(lib, 4, [d((0, 8))], [d((8,))]) == NOTIMPL                     # reduce_sum
+    assert _call(lib, 5, [z(), z(1)], [z(2)]) == NOTIMPL                         # mse_grad
+    assert _call(lib, 6, [z(), z(1)], [z(2)]) == NOTIMPL                         # relu_bwd
+    assert _call(lib, 7, [z(), z(1)], [z()]) == NOTIMPL                          # sgd
+    assert _call(lib, 11, [z(0, I32)], [z(0, I32)]) == NOTIMPL                  # step_inc
+    assert _call(lib, 2, [d((0, 8)), d((8, 8))], [d((0, 8))]) == NOTIMPL        # gemm
+
+
 def test_by_id_status_rules(lib):
     P = d((128,))
     # empty id -> InvalidArgument; unknown id -> NotImplemented
