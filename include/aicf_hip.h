@@ -92,7 +92,7 @@ extern "C" {
 #define AICF_SCHEMA_GADW 0x57444147u /* appended: b"GADW" little-endian, <ii fffff> transA, transB, lr, b1, b2, eps, wd */
 
 /* GEPI epilogue kinds.  0..2 are the values core_v2/exec.py:223-252 packs;
- * 3..5 are appended. */
+ * 3..6 are appended (no counterpart in the reference). */
 #define AICF_EPI_BIAS_RELU 0
 #define AICF_EPI_BIAS 1
 #define AICF_EPI_RELU 2
