@@ -44,6 +44,8 @@ SIGNATURES = {
     "aicf_cuda_register_all_kernels": (None, []),
     "aicf_reduce_sum_lastdim_f32": (ctypes.c_int32, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32,
                                                      ctypes.c_int32, ctypes.c_void_p]),
+    "aicf_diag_mfma_loop": (ctypes.c_int32, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_uint32,
+                                             ctypes.c_void_p]),
     "aicf_registry_count": (ctypes.c_int32, [ctypes.c_int32]),
     "aicf_registry_kernel_id": (ctypes.c_char_p, [ctypes.c_int32, ctypes.c_int32]),
     "aicf_registry_priority": (ctypes.c_int32, [ctypes.c_int32, ctypes.c_int32]),

@@ -416,6 +416,40 @@ def step_gemm_times(ex, iters, warmup=2):
     return res
 
 
+def bench_mfma_ceiling(waves_per_simd=4, iters=20000, launches=8, warm=4):
+    """Sustained rate of the register-only MFMA loop (aicf_diag_mfma_loop:
+    v_mfma_f32_32x32x16_bf16 on random operands, no memory traffic): the
+    power-limited MFMA ceiling of this part, the practical upper bound of any
+    bf16 GEMM on it.  `warm` launches (~14 ms each) bring the board to its
+    power-limited steady state before the timed ones."""
+    import ctypes
+
+    import torch
+
+    from aicf_cuda import abi
+
+    lib = abi.load()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    blocks = cus * waves_per_simd  # 4 waves per workgroup, one per SIMD
+    out = torch.zeros(1, device="cuda")
+    s = torch.cuda.current_stream()
+    flops = blocks * 4.0 * iters * 8 * 2 * 32 * 32 * 16
+    times = []
+    for k in range(warm + launches):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        st = lib.aicf_diag_mfma_loop(ctypes.c_void_p(out.data_ptr()), blocks, iters, k + 1,
+                                     ctypes.c_void_p(s.cuda_stream))
+        e1.record(s)
+        torch.cuda.synchronize()
+        if st != 0:
+            raise RuntimeError(f"aicf_diag_mfma_loop failed: status {st}")
+        if k >= warm:
+            times.append(e0.elapsed_time(e1))
+    ms = sum(times) / len(times)
+    return {"tflops": flops / (ms * 1e-3) / 1e12, "ms": ms}
+
+
 def ex_stream():
     from aicf_cuda import _C
 
@@ -1003,8 +1037,15 @@ def main():
                 "measured": "HIP events around 10 launches of each GEMM op of the step on the step's "
                             "own tensors (torch's current stream), after the timed replays"}
     log(f"[bench] roofline step gemms {times}")
+    ceil = bench_mfma_ceiling()
+    roofline["power_limited_mfma_ceiling"] = round(ceil["tflops"], 1)
+    roofline["frac_of_ceiling"] = round(achieved / ceil["tflops"], 4)
+    log(f"[bench] register-only MFMA loop {ceil}")
 
-    comps = {}
+    comps = {"mfma_register_loop_bf16": {
+        "value": round(ceil["tflops"], 1), "unit": "TFLOP/s", "frac": round(ceil["tflops"] / PEAK_BF16_TFLOPS, 4),
+        "note": "v_mfma_f32_32x32x16_bf16 on random register operands, no memory traffic: the "
+                "power-limited MFMA ceiling of this part, measured in this run"}}
     if not args.no_components:
         gg = bench_gemm(C, 8192, 8192, 8192)
         comps["gemm_bf16_8192^3"] = {"value": round(gg["tflops"], 2), "unit": "TFLOP/s",

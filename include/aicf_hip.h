@@ -159,6 +159,14 @@ void aicf_cuda_register_all_kernels(void);
  * dB[n] = sum_m dY[m, n] over a row-major [M, N] fp32 matrix. */
 int32_t aicf_reduce_sum_lastdim_f32(const float* dY, float* dB, int32_t M, int32_t N, void* stream);
 
+/* Measurement aid, no counterpart in the reference: launches `blocks`
+ * workgroups of 4 waves, each running `iters` rounds of 8 independent
+ * v_mfma_f32_32x32x16_bf16 on random register operands (no memory traffic),
+ * 2 * 32 * 32 * 16 * 8 * iters flop per wave.  Its sustained rate is the
+ * power-limited MFMA ceiling of the part; `out` (one float) is written only
+ * to keep the loop.  Returns AICF_STATUS_*. */
+int32_t aicf_diag_mfma_loop(float* out, int32_t blocks, int32_t iters, uint32_t seed, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Registry introspection (replaces KernelRegistry::variants_snapshot and    */
 /* find_by_id, registry/registry.hpp:39-42)                                  */

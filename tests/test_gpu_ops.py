@@ -817,3 +817,28 @@ def test_trace_api(C):
     C.trace_enable(True)
     C.trace_reset()
     assert C.trace_get() == []
+
+
+def test_diag_mfma_loop_runs_and_rate_is_plausible(C):
+    """The measurement aid behind bench.py's MFMA ceiling: returns Ok, rejects
+    bad arguments, and its rate lies between a fraction of and the dense bf16
+    peak (2.5 PFLOP/s)."""
+    import ctypes
+
+    from aicf_cuda import abi
+
+    lib = abi.load()
+    out = torch.zeros(1, device="cuda")
+    s = torch.cuda.current_stream()
+    assert lib.aicf_diag_mfma_loop(None, 256, 10, 1, None) == abi.STATUS_INVALID_ARGUMENT
+    assert lib.aicf_diag_mfma_loop(ctypes.c_void_p(out.data_ptr()), 0, 10, 1, None) == abi.STATUS_INVALID_ARGUMENT
+    blocks, iters = 1024, 2000
+    for k in range(3):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        assert lib.aicf_diag_mfma_loop(ctypes.c_void_p(out.data_ptr()), blocks, iters, k + 1,
+                                       ctypes.c_void_p(s.cuda_stream)) == abi.STATUS_OK
+        e1.record(s)
+        torch.cuda.synchronize()
+    tflops = blocks * 4.0 * iters * 8 * 32768 / (e0.elapsed_time(e1) * 1e-3) / 1e12
+    assert 300.0 < tflops < 2600.0, tflops
