@@ -416,6 +416,19 @@ def step_gemm_times(ex, iters, warmup=2):
     return res
 
 
+def bench_copy_ceiling(C, elems=1 << 29, iters=10, warmup=2):
+    """HBM read+write ceiling of this part for a plain stream: copy_bf16_v0
+    (16-byte nontemporal vector per lane) over 1 GiB, 2 bytes read and 2
+    written per element; the reference point for the kernels that read and
+    write a stream (softmax, xent, MSE, AdamW)."""
+    import torch
+
+    x = torch.ones(elems, device="cuda", dtype=torch.bfloat16)
+    y = torch.empty_like(x)
+    ms = time_launches(lambda: C.launch_by_id("copy_bf16_v0", C.OpKind.Copy, [x], [y], 0, b""), iters, warmup)
+    return {"gbs": 4.0 * elems / (ms * 1e-3) / 1e9, "ms": ms}
+
+
 def bench_mfma_ceiling(waves_per_simd=4, iters=20000, launches=8, warm=4):
     """Sustained rate of the register-only MFMA loop (aicf_diag_mfma_loop:
     v_mfma_f32_32x32x16_bf16 on random operands, no memory traffic): the
@@ -1066,6 +1079,12 @@ def main():
                                                  "frac": round(rr["gbs"] / PEAK_HBM_GBS, 4),
                                                  "ms": round(rr["ms"], 5), "buffer_sets": rr["buffer_sets"]}
                 log(f"[bench] {name} {cols} {rr}")
+        cp = bench_copy_ceiling(C)
+        comps["hbm_copy_1GiB"] = {"value": round(cp["gbs"], 1), "unit": "GB/s",
+                                  "frac": round(cp["gbs"] / PEAK_HBM_GBS, 4), "ms": round(cp["ms"], 4),
+                                  "note": "plain read+write stream (copy_bf16_v0): the ceiling of the "
+                                          "read-and-write kernels on this part, measured in this run"}
+        log(f"[bench] copy ceiling {cp}")
         xe = bench_xent(C, 16384, 8192)
         comps["softmax_xent_fwd_bwd_16384x8192"] = {"value": round(xe["gbs"], 1), "unit": "GB/s",
                                                     "frac": round(xe["gbs"] / PEAK_HBM_GBS, 4),
