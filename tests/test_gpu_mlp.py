@@ -11,9 +11,9 @@ def test_mlp_xent_fp32_reference_config(C):
     """Batch 64, 784 -> 256 (ReLU) -> 10, softmax cross-entropy, Adam: loss,
     argmax, all gradients and all updated parameters (eager step, then two
     replays of the captured step)."""
-    from aicf_hip import mlp
+    import mlp_checks
 
-    res = mlp.check_mlp_small()
+    res = mlp_checks.check_mlp_small()
     assert res["ok"], res
 
 
@@ -25,12 +25,13 @@ def test_mlp_mse_bf16_graph(C, B, D, L, nt, colsum):
     transpose + NT-GEMM lowering (nt) and with the general GEMM kernel; with
     colsum the hidden layers' bias gradients come from the dGELU GEMMs'
     epilogue (GEPI kind 6)."""
+    import mlp_checks
     from aicf_hip import mlp
 
     if colsum:
         ir, lowered, _ = mlp.build_mlp_mse(B, D, L, fuse_colsum=True)
         assert sum(bool(it["attrs"].get("epilogue_colsum")) for it in lowered) == L - 1
-    res = mlp.check_mlp_mse_small(B, D, L, nt_layout=nt, fuse_colsum=colsum)
+    res = mlp_checks.check_mlp_mse_small(B, D, L, nt_layout=nt, fuse_colsum=colsum)
     assert res["ok"], res
 
 
