@@ -1403,7 +1403,16 @@ bool epi_check(const TensorDesc* in, int ni, const TensorDesc* out, int no, cons
     if (dt(W) != DType::kF32 || !W.contiguous || W.rank != 2 || W.shape[1] != C.cols ||
         W.shape[0] < C.rows / 256)
       return false;
-    return true;
+    // only the bf16 256 x 256-tile path carries the column sums: accept
+    // exactly the calls it runs (M, N multiples of 256, so the workspace
+    // has at least one row; K of 64; aligned operands)
+    if (din != DType::kBF16) return false;
+    GemmParams p{};
+    fill_operands(p, in[0], in[1], out[0], e.ta, e.tb);
+    p.act = ACT_DGELU;
+    p.aux = const_cast<void*>(X.data);
+    p.aux_rs = X.stride[0];
+    return nt_eligible<IN_BF16, OUT_BF16>(p, 256, 256, true);
   }
   if (no > 2) return false;
   if (e.kind == AICF_EPI_DGELU) {

@@ -13,9 +13,14 @@
 // same topology - the usual case when a plan is captured again with other
 // buffers bound - and instantiates afresh only when the update is refused.
 //
-// Launch can first wait on an event recorded on the caller's stream, so
-// device-scalar updates queued there are ordered before the replay (the
-// reference replays with no such edge).
+// Launch orders the replay between the caller's work on both sides: the
+// graph stream first waits on an event recorded on the caller's stream (so
+// input copies and device-scalar updates queued there run before the
+// replay), and the caller's stream then waits on an event recorded after the
+// replay (so what it queues next reads the replay's results).  A NULL caller
+// stream is the null stream, torch's default; the graph stream is created
+// non-blocking and would not otherwise synchronise with it.  The reference
+// replays with no such edges.
 #include <hip/hip_runtime_api.h>
 
 #include <map>
@@ -33,13 +38,15 @@ struct GraphState {
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
   hipStream_t stream = nullptr;
-  hipEvent_t edge = nullptr;
+  hipEvent_t edge = nullptr;  // caller's queued work -> replay
+  hipEvent_t done = nullptr;  // replay -> caller's later work
   uint64_t updates = 0;  // re-captures applied through hipGraphExecUpdate
 
   hipError_t ensure_stream() {
     hipError_t e = hipSuccess;
     if (!stream) e = hipStreamCreateWithFlags(&stream, hipStreamNonBlocking);
     if (e == hipSuccess && !edge) e = hipEventCreateWithFlags(&edge, hipEventDisableTiming);
+    if (e == hipSuccess && !done) e = hipEventCreateWithFlags(&done, hipEventDisableTiming);
     return e;
   }
 
@@ -70,8 +77,10 @@ struct GraphState {
   void release() {
     reset_full();
     if (edge) (void)hipEventDestroy(edge);
+    if (done) (void)hipEventDestroy(done);
     if (stream) (void)hipStreamDestroy(stream);
     edge = nullptr;
+    done = nullptr;
     stream = nullptr;
   }
 };
@@ -158,8 +167,10 @@ int32_t launch_on(GraphState& g, void* caller_stream) {
   }
   hipError_t e = g.ensure_stream();
   if (e != hipSuccess) return fail(e, "hipStreamCreateWithFlags");
+  // NULL is the null stream (torch's default stream), not "no caller"
   hipStream_t caller = reinterpret_cast<hipStream_t>(caller_stream);
-  if (caller && caller != g.stream) {
+  const bool edges = caller != g.stream;
+  if (edges) {
     e = hipEventRecord(g.edge, caller);
     if (e != hipSuccess) return fail(e, "hipEventRecord");
     e = hipStreamWaitEvent(g.stream, g.edge, 0);
@@ -167,6 +178,12 @@ int32_t launch_on(GraphState& g, void* caller_stream) {
   }
   e = hipGraphLaunch(g.exec, g.stream);
   if (e != hipSuccess) return fail(e, "hipGraphLaunch");
+  if (edges) {
+    e = hipEventRecord(g.done, g.stream);
+    if (e != hipSuccess) return fail(e, "hipEventRecord");
+    e = hipStreamWaitEvent(caller, g.done, 0);
+    if (e != hipSuccess) return fail(e, "hipStreamWaitEvent");
+  }
   return AICF_STATUS_OK;
 }
 

@@ -498,10 +498,13 @@ def cpu_baseline_mlp(B, D, L, sample_rows):
             dy = (dx * orc.gelu_grad_f64(zs[i - 1].astype(np.float64))).astype(np.float32)
     t_batch = time.perf_counter() - t0
     n = L * (D * D + D)
-    P = np.zeros(n, np.float32)
+    # separate P, G, M, V: the update reads four streams and writes three
+    P = np.full(n, 0.01, np.float32)
     G = np.full(n, 1e-3, np.float32)
+    M = np.zeros(n, np.float32)
+    V = np.zeros(n, np.float32)
     t1 = time.perf_counter()
-    orc.adamw(P, G, P, P, 1, wd=0.01)
+    orc.adamw(P, G, M, V, 1, wd=0.01)
     t_adam = time.perf_counter() - t1
     per_step = t_batch * (B / b) + t_adam
     return {"value": 1.0 / per_step, "unit": "steps/s", "cores": orc.threads(), "kind": "port",
@@ -509,6 +512,116 @@ def cpu_baseline_mlp(B, D, L, sample_rows):
                       f"fp32 algorithm + GELU/MSE/colsum) scaled by {B // b}, plus AdamW over all "
                       f"{n} parameters; measured {t_batch:.2f}s + {t_adam:.2f}s",
             "modelled_seconds_per_step": per_step}
+
+
+def _cpu(value, unit, sample, **extra):
+    import oracle as orc
+
+    d = {"value": value, "unit": unit, "cores": orc.threads(), "kind": "port", "sample": sample}
+    d.update(extra)
+    return d
+
+
+def cpu_baseline_c1(iters=20):
+    """C1 on the host: the whole fp32 step of the reference MLP (64 x 784 ->
+    256 ReLU -> 10, softmax cross-entropy, Adam) through the oracle: the six
+    GEMMs of the reference lowering with its per-output sequential-k
+    algorithm (gemm/launcher.cu:155-172), bias add, ReLU and its backward,
+    the loss and its gradient, the column sums and the AdamW update of every
+    parameter; microseconds per step."""
+    import numpy as np
+
+    import oracle as orc
+    from aicf_hip import mlp
+
+    d = mlp.init_mlp_xent()
+    x, lab = d["x"], d["t"]
+    P = {k: d[k].copy() for k in ("0.W", "0.b", "2.W", "2.b")}
+    Ms = {k: np.zeros(v.size, np.float32) for k, v in P.items()}
+    Vs = {k: np.zeros(v.size, np.float32) for k, v in P.items()}
+    t0 = time.perf_counter()
+    for it in range(iters):
+        z = orc.gemm_ref_f32(x, P["0.W"], False, True) + P["0.b"][None, :]
+        h = orc.relu_f32(z).reshape(z.shape)
+        logits = orc.gemm_ref_f32(h, P["2.W"], False, True) + P["2.b"][None, :]
+        _, dz, _, _ = orc.softmax_xent_f64(logits, lab)
+        dz = dz.astype(np.float32)
+        g = {"2.W": orc.gemm_ref_f32(dz, h, True, False), "2.b": orc.colsum_f64(dz).astype(np.float32)}
+        dh = orc.gemm_ref_f32(dz, P["2.W"], False, False)
+        dzz = orc.relu_bwd_f32(dh, h).reshape(dh.shape)
+        g["0.W"] = orc.gemm_ref_f32(dzz, x, True, False)
+        g["0.b"] = orc.colsum_f64(dzz).astype(np.float32)
+        orc.gemm_ref_f32(dzz, P["0.W"], False, False)  # the input gradient the lowering emits
+        for k in P:
+            p, Ms[k], Vs[k] = orc.adamw(P[k], g[k], Ms[k], Vs[k], it + 1)
+            P[k] = p.reshape(P[k].shape)
+    us = (time.perf_counter() - t0) / iters * 1e6
+    return _cpu(round(us, 1), "us/step", f"{iters} full steps at the configuration's own size")
+
+
+def cpu_baseline_c2(rows=1024):
+    """C2 on the host: row softmax with row max and row sum (the oracle's
+    per-row pass, fp64 accumulation and output, OpenMP over rows) on the
+    first `rows` rows of each width; GB/s at the GPU metric's algorithmic
+    bytes (fp32 in and out, 8 B per element + 8 B per row)."""
+    import numpy as np
+
+    import oracle as orc
+
+    out = {}
+    r = np.random.default_rng(2)
+    for cols in (128, 1024, 8192, 32768):
+        x = (r.standard_normal((rows, cols)) * 2.0).astype(np.float32)
+        orc.softmax_rows_f64(x[:8])
+        t0 = time.perf_counter()
+        orc.softmax_rows_f64(x)
+        dt = time.perf_counter() - t0
+        nbytes = 8.0 * rows * cols + 8.0 * rows
+        out[cols] = _cpu(round(nbytes / dt / 1e9, 2), "GB/s",
+                         f"{rows} of 16384 rows x {cols}; fp64 accumulation and output")
+    return out
+
+
+def cpu_baseline_c3(n=1 << 26):
+    """C3 on the host: the oracle's AdamW (OpenMP over elements) over `n`
+    parameters with separate P, G, M, V arrays, one step; GB/s at 28 B per
+    parameter (4 streams read, 3 written)."""
+    import numpy as np
+
+    import oracle as orc
+
+    r = np.random.default_rng(3)
+    P = (r.standard_normal(n, dtype=np.float32) * 0.02)
+    G = (r.standard_normal(n, dtype=np.float32) * 1e-3)
+    M = np.zeros(n, np.float32)
+    V = np.zeros(n, np.float32)
+    orc.adamw(P[:1024], G[:1024], M[:1024], V[:1024], 1, wd=0.01)
+    t0 = time.perf_counter()
+    orc.adamw(P, G, M, V, 1, wd=0.01)
+    dt = time.perf_counter() - t0
+    return _cpu(round(28.0 * n / dt / 1e9, 2), "GB/s", f"2^{int(math.log2(n))} of 2^28 parameters, one step")
+
+
+def cpu_baseline_c4(rows=8):
+    """C4 on the host: the reference's fp32 GEMM algorithm (one sequential-k
+    dot per output, gemm/launcher.cu:155-172; OpenMP over outputs) on the
+    first `rows` rows of X at each shape, extrapolated to TFLOP/s (the
+    epilogue is not timed: it is negligible beside the dots)."""
+    import numpy as np
+
+    import oracle as orc
+
+    out = {}
+    for (M, N, K) in C4_SHAPES:
+        x = np.linspace(-1.0, 1.0, rows * K, dtype=np.float32).reshape(rows, K) / math.sqrt(K)
+        w = np.linspace(-1.0, 1.0, N * K, dtype=np.float32).reshape(N, K)[:, ::-1].copy() / math.sqrt(K)
+        orc.gemm_ref_f32(x[:1, :64], w[:8, :64], False, True)
+        t0 = time.perf_counter()
+        orc.gemm_ref_f32(x, w, False, True)
+        dt = time.perf_counter() - t0
+        out[(M, N, K)] = _cpu(round(2.0 * rows * N * K / dt / 1e12, 6), "TFLOP/s",
+                              f"{rows} of {M} rows, fp32 sequential-k dots, extrapolated by rate")
+    return out
 
 
 # ------------------------------------------------------------------ main
@@ -1129,7 +1242,7 @@ def main():
         c1 = bench_c1()
         comps["c1_mlp_fp32_64x784x256x10_step"] = c1
         log(f"[bench] c1 {c1}")
-        for dt, shapes in (("bf16", C4_SHAPES), ("fp32", C4_SHAPES[:3])):
+        for dt, shapes in (("bf16", C4_SHAPES), ("fp32", C4_SHAPES)):
             c4 = bench_c4(C, dt, shapes)
             comps.update(c4)
             log(f"[bench] c4 {dt} {c4}")
@@ -1138,6 +1251,17 @@ def main():
     if not args.no_cpu:
         cpu = cpu_baseline_mlp(B, D, L, args.cpu_rows)
         log(f"[bench] cpu {cpu}")
+        if not args.no_components:
+            # the oracle on the host beside each configuration's GPU line
+            comps["c1_mlp_fp32_64x784x256x10_step"]["cpu_baseline"] = cpu_baseline_c1()
+            for cols, v in cpu_baseline_c2().items():
+                comps[f"softmax_16384x{cols}"]["cpu_baseline"] = v
+            comps["adamw_2^28"]["cpu_baseline"] = cpu_baseline_c3()
+            for (M_, N_, K_), v in cpu_baseline_c4().items():
+                for key in [k for k in comps if k.startswith("c4_") and k.split("_")[2] == f"{M_}x{N_}x{K_}"]:
+                    comps[key]["cpu_baseline"] = v
+            log(f"[bench] cpu per config: c1 {comps['c1_mlp_fp32_64x784x256x10_step']['cpu_baseline']}, "
+                f"c3 {comps['adamw_2^28']['cpu_baseline']}")
 
     out = {
         "metric": METRIC,

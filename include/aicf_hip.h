@@ -198,11 +198,14 @@ int32_t aicf_graph_begin(uint64_t* out_stream);
 /* Ends the capture and instantiates the executable graph.  INVALID_ARGUMENT
  * when no capture is in progress. */
 int32_t aicf_graph_end(void);
-/* Launches the instantiated graph on the dedicated stream.  When
- * `caller_stream` is non-NULL, the launch first waits on an event recorded
- * on it, so work queued on the caller's stream (e.g. host-side updates of
- * device scalars) is ordered before the replay.  INVALID_ARGUMENT when no
- * graph was captured. */
+/* Launches the instantiated graph on the dedicated stream, ordered after the
+ * work already queued on `caller_stream` (input copies, host-side updates of
+ * device scalars) and before the work queued there afterwards (reads of the
+ * replay's results): an event recorded on the caller's stream is waited on
+ * by the graph stream, and one recorded after the replay by the caller's
+ * stream.  NULL is the null stream (torch's default stream), which the
+ * non-blocking graph stream does not otherwise synchronise with.
+ * INVALID_ARGUMENT when no graph was captured. */
 int32_t aicf_graph_launch(void* caller_stream);
 /* Ends a dangling capture and destroys the graph objects. */
 int32_t aicf_graph_reset(void);

@@ -217,6 +217,32 @@ def test_dispatch_neg_cases(lib):
     assert _call(lib, 7, [Pp, Gp], [Gp]) == INV
 
 
+def test_dgelu_colsum_supported_only_where_it_runs(lib):
+    """GEPI kind 6 (dGELU + column sums) is supported exactly where its
+    bf16 256 x 256-tile path runs: M and N multiples of 256, K of 64, a
+    workspace of at least M/256 rows.  Everything else is refused by
+    supported() (no variant for op_call; INVALID_ARGUMENT by id), on the
+    host, before any launch."""
+    gepi = int.from_bytes(b"GEPI", "little")
+    pay = struct.pack("<iii", 0, 0, 6)
+    kid = "gemm_epilogue_bf16_mfma_v0"
+
+    def call(M, N, K, P, by_id):
+        ins = [d((M, K), BF16, FAKE), d((K, N), BF16, FAKE + (1 << 24)), d((M, N), BF16, FAKE + (2 << 24))]
+        outs = [d((M, N), BF16, FAKE + (3 << 24)), d((N,), F32, FAKE + (4 << 24)),
+                d((P, N), F32, FAKE + (5 << 24))]
+        return _call(lib, 17, ins, outs, gepi, pay, kid=kid if by_id else None)
+
+    for M, N, K, P in ((384, 256, 64, 2), (512, 320, 64, 2), (512, 256, 96, 2), (512, 256, 64, 1),
+                       (128, 256, 64, 1), (128, 256, 64, 0)):
+        assert call(M, N, K, P, True) == INV, (M, N, K, P)
+        assert call(M, N, K, P, False) == NOTIMPL, (M, N, K, P)
+    # an f16 call with kind 6 has no supporting variant either
+    ins = [d((512, 64), F16), d((64, 256), F16), d((512, 256), F16)]
+    outs = [d((512, 256), F16), d((256,), F32), d((2, 256), F32)]
+    assert _call(lib, 17, ins, outs, gepi, pay) == NOTIMPL
+
+
 def test_zero_size_inputs_follow_the_reference(lib):
     """Zero-element tensors get the reference's statuses, decided on the host:
     copy, grad_zero and Adam accept n = 0 and return Ok without a launch

@@ -93,3 +93,120 @@ def test_eight_wave_kernels_do_not_spill(asm, kernel):
     body = kernel_body(asm, kernel)
     spills = [l.strip() for l in body if "scratch_" in l]
     assert not spills, spills[:4]
+
+
+# The M/N-contiguous operand loads are inline asm (`buffer_load_dwordx4 v,
+# s[..], s offen lds`), hidden from the compiler's hazard tracking: nothing
+# stops it from reusing the lane-offset VGPR of such a load while the load
+# is still in flight.  Every one of them must keep that VGPR unwritten until
+# a `s_waitcnt vmcnt(0)`, on the fall-through path and, past a backward
+# branch, from the loop header on.
+_DST_OPS = re.compile(r"^(v_|ds_read|ds_load|buffer_load|global_load|flat_load|scratch_load)")
+_REG = re.compile(r"^v(\d+)$|^v\[(\d+):(\d+)\]$")
+
+
+def _vgprs(operand: str) -> set[int]:
+    m = _REG.match(operand.strip())
+    if not m:
+        return set()
+    if m.group(1) is not None:
+        return {int(m.group(1))}
+    return set(range(int(m.group(2)), int(m.group(3)) + 1))
+
+
+def _instr(line: str):
+    s = line.split(";")[0].strip()
+    if not s or s.startswith(".") or s.endswith(":"):
+        return None, []
+    parts = s.split(None, 1)
+    ops = [o.strip() for o in parts[1].split(",")] if len(parts) > 1 else []
+    return parts[0], ops
+
+
+def _written_vgprs(line: str) -> set[int]:
+    mnem, ops = _instr(line)
+    if not mnem or not ops or not _DST_OPS.match(mnem):
+        return set()
+    if mnem.startswith(("v_cmp", "v_readlane", "v_readfirstlane")):
+        return set()
+    return _vgprs(ops[0])
+
+
+def _is_vm_drain(line: str) -> bool:
+    s = line.split(";")[0]
+    return "s_waitcnt" in s and ("vmcnt(0)" in s or re.search(r"s_waitcnt\s+0\b", s) is not None)
+
+
+def asm_lds_loads(body: list[str]) -> list[tuple[int, int]]:
+    """(line index after the asm block, voffset VGPR) of each inline-asm
+    direct-to-LDS buffer load."""
+    out = []
+    in_asm = False
+    pending = []
+    for i, ln in enumerate(body):
+        if "ASMSTART" in ln:
+            in_asm, pending = True, []
+            continue
+        if "ASMEND" in ln:
+            out += [(i + 1, r) for r in pending]
+            in_asm = False
+            continue
+        m = re.search(r"buffer_load_dwordx4\s+v(\d+),\s*s\[\d+:\d+\],\s*s\d+\s+offen\s+lds", ln)
+        if in_asm and m:
+            pending.append(int(m.group(1)))
+    return out
+
+
+def _first_write_before_drain(body, start, reg, labels):
+    seen = set()
+    todo = [start]
+    while todo:
+        i = todo.pop()
+        while i < len(body):
+            if i in seen:
+                break
+            seen.add(i)
+            ln = body[i]
+            if _is_vm_drain(ln):
+                break
+            if reg in _written_vgprs(ln):
+                return i
+            m = re.search(r"s_(?:cbranch_\w+|branch)\s+(\.LBB\w+)", ln.split(";")[0])
+            if m and m.group(1) in labels and labels[m.group(1)] < i:
+                todo.append(labels[m.group(1)] + 1)
+                if "s_branch" in ln:
+                    break
+            i += 1
+    return None
+
+
+def test_asm_lds_loads_keep_their_offset_vgpr_until_drained(asm):
+    names = re.findall(r"^(_Z\S*gemm_nt_kernel\S*):", asm, re.M)
+    assert names
+    checked = 0
+    for name in names:
+        body = kernel_body(asm, name[name.index("gemm_nt_kernel"):])
+        labels = {ln.split(":")[0]: i for i, ln in enumerate(body) if ln.startswith(".LBB")}
+        for start, reg in asm_lds_loads(body):
+            hit = _first_write_before_drain(body, start, reg, labels)
+            assert hit is None, f"{name}: v{reg} of the asm load before line {start} is written at " \
+                                f"'{body[hit].strip()}' before a vmcnt(0) wait"
+            checked += 1
+    assert checked > 100, checked
+
+
+def test_asm_offset_guard_flags_a_planted_write(asm):
+    """The guard itself: a write of the offset VGPR planted (in the text)
+    right after one asm load, or behind the loop's backward branch, is
+    reported."""
+    name = re.findall(r"^(_Z\S*gemm_nt_kernel\S*ELb0ELb0E\S*):", asm, re.M)[0]
+    body = kernel_body(asm, name[name.index("gemm_nt_kernel"):])
+    labels = {ln.split(":")[0]: i for i, ln in enumerate(body) if ln.startswith(".LBB")}
+    start, reg = asm_lds_loads(body)[0]
+    assert _first_write_before_drain(body, start, reg, labels) is None
+    planted = body[:start] + [f"\tv_mov_b32_e32 v{reg}, 0"] + body[start:]
+    labels2 = {ln.split(":")[0]: i for i, ln in enumerate(planted) if ln.startswith(".LBB")}
+    assert _first_write_before_drain(planted, start, reg, labels2) == start
+    assert _written_vgprs("\tds_read_b128 v[4:7], v1 offset:16") == {4, 5, 6, 7}
+    assert _written_vgprs("\tds_write_b128 v1, v[4:7]") == set()
+    assert _is_vm_drain("\ts_waitcnt vmcnt(0) lgkmcnt(0)") and not _is_vm_drain("\ts_waitcnt vmcnt(3)")

@@ -102,7 +102,8 @@ C4_CASES = [
     ("bf16", 4096, 4096, 4096, "relu"), ("bf16", 1024, 1024, 1024, "gelu"),
     ("bf16", 8192, 4096, 256, "relu"), ("bf16", 8192, 4096, 11008, "gelu"),
     ("fp32", 8192, 8192, 8192, "gelu"), ("fp32", 4096, 4096, 4096, "relu"),
-    ("fp32", 1024, 1024, 1024, "none"),
+    ("fp32", 1024, 1024, 1024, "none"), ("fp32", 8192, 4096, 256, "gelu"),
+    ("fp32", 8192, 4096, 11008, "relu"),
 ]
 ACT_KIND = {"none": 1, "relu": 0, "gelu": 3}
 
@@ -138,7 +139,10 @@ def test_c5_mlp_step_full_shape_forward_rows_and_adamw_bit_exact(C, colsum):
     gradients over all 67,125,248 parameters must reproduce the updated fp32
     parameters, both moments and the bf16 shadow bit for bit.  Every bias
     gradient matches the fp64 column sum of the stored output gradient it
-    comes from (with colsum: taken in the dGELU GEMMs' epilogue)."""
+    comes from (with colsum: taken in the dGELU GEMMs' epilogue), 4096
+    sampled weight-gradient entries per layer match fp64 dots over the 8192
+    stored rows, and 16 sampled rows of every input gradient match the fp64
+    chain through the dGELU epilogue."""
     from aicf_hip import mlp
 
     B, D, L = 8192, 4096, 4
@@ -180,6 +184,29 @@ def test_c5_mlp_step_full_shape_forward_rows_and_adamw_bit_exact(C, colsum):
     for i in range(1, L + 1):
         dz = _host(ex.value("dY" if i == L else f"d_z{i}")).astype(np.float64).sum(axis=0)
         assert orc.rel_err(G[lay.b_off(i):lay.b_off(i) + D], dz) < 1e-5, i
+    # weight gradients dW_i = dz_i^T . h_{i-1} (core_v2/lower.py:100-104): a
+    # 64 x 64 block of sampled (output, input) pairs per layer, 4096 entries,
+    # each an fp64 dot over all 8192 stored bf16 rows of both operands
+    r = np.random.default_rng(9)
+    for i in range(1, L + 1):
+        o_idx = np.sort(r.choice(D, 64, replace=False))
+        j_idx = np.sort(r.choice(D, 64, replace=False))
+        dz = ex.value("dY" if i == L else f"d_z{i}")[:, torch.from_numpy(o_idx).cuda()]
+        hp = ex.value("x" if i == 1 else f"h{i - 1}")[:, torch.from_numpy(j_idx).cuda()]
+        ref = _host(dz).astype(np.float64).T @ _host(hp).astype(np.float64)
+        got = G[lay.w_off(i):lay.w_off(i) + D * D].reshape(D, D)[np.ix_(o_idx, j_idx)]
+        assert orc.rel_err(got, ref) < 1e-4, f"dW{i}"
+    # input gradients of 16 sampled rows: d_z{i-1} = bf16((dz_i . Wb_i) *
+    # gelu'(z_{i-1})) through the dGELU epilogue, d_x = bf16(dz_1 . Wb_1)
+    for i in range(L, 0, -1):
+        W = wb0[lay.w_off(i):lay.w_off(i) + D * D].reshape(D, D).astype(np.float64)
+        dzr = _host(ex.value("dY" if i == L else f"d_z{i}")[rows]).astype(np.float64)
+        v = dzr @ W
+        if i > 1:
+            v = bf(v * orc.gelu_grad_f64(_host(ex.value(f"z{i - 1}")[rows]).astype(np.float64)))
+            assert orc.rel_err(_host(ex.value(f"d_z{i - 1}")[rows]), v) < 1e-2, f"d_z{i - 1}"
+        else:
+            assert orc.rel_err(_host(ex.value("d_x")[rows]), bf(v)) < 1e-2, "d_x"
     ex.reset_graph()
 
 

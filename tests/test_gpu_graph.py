@@ -2,11 +2,13 @@
 holding an instantiated graph of their own, replayed interleaved, and
 re-capture with other input buffers updating the executable in place.
 
-Each graph replay is compared bit for bit with eager execution of the same
-plan on separately allocated copies of the same data (all kernels on the
-path are deterministic, so graph and eager runs agree exactly).  The
-process-wide graph (handle 0, the reference's singleton,
-src/python_bindings/bindings.cpp:137-187,475-547) keeps working alongside.
+Each graph replay is checked against the CPU oracle (loss and argmax, all
+gradients <= 1e-4, the AdamW update bit-exact on the GPU's gradients; the
+oracle follows each executor's own sequence of batches) and compared bit
+for bit with eager execution of the same plan on separately allocated
+copies of the same data.  The process-wide graph (handle 0, the reference's
+singleton, src/python_bindings/bindings.cpp:137-187,475-547) keeps working
+alongside.
 """
 from __future__ import annotations
 
@@ -19,15 +21,19 @@ pytestmark = pytest.mark.gpu
 KEYS = ("loss", "pred", "d_0.W", "d_2.b")
 
 
-def _xent_setup(seed, own_graph, B=64, din=784, dh=256, dout=10):
+def _xent_setup(seed, own_graph):
+    import mlp_checks
+
+    ex, inputs, params, _, _ = mlp_checks.xent_setup(seed, own_graph=own_graph)
+    return ex, inputs, params
+
+
+def _oracle(seed):
+    import mlp_checks
     from aicf_hip import mlp
 
-    ir, lowered, plan = mlp.build_mlp_xent(B, din, dh, dout)
-    data = mlp.init_mlp_xent(B, din, dh, dout, seed=seed)
-    params = {k: torch.from_numpy(v.copy()).cuda() for k, v in data.items() if "." in k}
-    inputs = {"x": torch.from_numpy(data["x"]).cuda(), "t": torch.from_numpy(data["t"]).cuda()}
-    ex = mlp.make_executor(ir, lowered, plan, own_graph=own_graph)
-    return ex, inputs, params
+    data = mlp.init_mlp_xent(seed=seed)
+    return mlp_checks.XentOracle(data), data
 
 
 def _snap(ex, params):
@@ -60,6 +66,8 @@ def test_executors_with_own_graphs_replay_interleaved(C):
     plus a third on the process-wide graph; replays alternate between them
     and each matches its own eager run bit for bit."""
     want = {seed: _eager_steps(seed, 3) for seed in (1, 2, 3)}
+    oracles = {seed: _oracle(seed) for seed in (1, 2, 3)}
+    res = {"ok": True}
     exs = {}
     for seed in (1, 2, 3):
         ex, inputs, params = _xent_setup(seed, own_graph=(seed != 3))
@@ -75,6 +83,8 @@ def test_executors_with_own_graphs_replay_interleaved(C):
             ex, params = exs[seed]
             ex.replay(1)
             torch.cuda.synchronize()
+            o, data = oracles[seed]
+            assert o.check(ex, params, data["x"], data["t"], f"s{seed}_{step}", res), res
             _assert_same(_snap(ex, params), want[seed][step], f"seed {seed} step {step}")
     for seed, (ex, _) in exs.items():
         if seed == 3:
@@ -96,6 +106,8 @@ def test_recapture_with_new_inputs_updates_in_place(C):
     batch2 = {"x": x2.clone(), "t": t2.clone()}
     want = _eager_steps(5, 4, feed=lambda i: batch2 if i == 2 else None)
 
+    o, data = _oracle(5)
+    res = {"ok": True}
     ex, inputs, params = _xent_setup(5, own_graph=True)
     ex.build_env(inputs=inputs, params=params, reuse_static=False)
     ex.capture(inputs=inputs, params=params, reuse_static=True)
@@ -103,14 +115,17 @@ def test_recapture_with_new_inputs_updates_in_place(C):
     for step in range(2):
         ex.replay(1)
         torch.cuda.synchronize()
+        assert o.check(ex, params, data["x"], data["t"], f"step{step}", res), res
         _assert_same(_snap(ex, params), want[step], f"step {step}")
     old_x = ex.value("x").data_ptr()
     ex.recapture(inputs={"x": x2, "t": t2})
     assert ex.value("x").data_ptr() == x2.data_ptr() != old_x
     assert ex.graph_updates == 1
+    xb, tb = x2.cpu().numpy(), t2.cpu().numpy()
     for step in range(2, 4):
         ex.replay(1)
         torch.cuda.synchronize()
+        assert o.check(ex, params, xb, tb, f"step{step}", res), res
         _assert_same(_snap(ex, params), want[step], f"step {step}")
     ex.close()
 
@@ -122,8 +137,10 @@ def _env_snapshot(ex):
 def test_recapture_of_a_different_plan_reinstantiates(C):
     """A capture whose op sequence differs from the executable's (another
     plan captured on the same handle) cannot be an update: the handle builds
-    a new executable and replays the new plan exactly as eager execution
-    does (every value of the plan compared)."""
+    a new executable; each replay matches the oracle (the xent and the bf16
+    MSE steps, gradients and the AdamW update) and equals eager execution
+    (every value of the plan compared)."""
+    import mlp_checks
     from aicf_hip import mlp
 
     def xent():
@@ -131,19 +148,22 @@ def test_recapture_of_a_different_plan_reinstantiates(C):
         data = mlp.init_mlp_xent(seed=7)
         params = {k: torch.from_numpy(v.copy()).cuda() for k, v in data.items() if "." in k}
         inputs = {"x": torch.from_numpy(data["x"]).cuda(), "t": torch.from_numpy(data["t"]).cuda()}
-        return ir, lowered, plan, inputs, params, None
+        o = mlp_checks.XentOracle(data)
+        check = lambda ex, res: o.check(ex, params, data["x"], data["t"], "xent", res)  # noqa: E731
+        return ir, lowered, plan, inputs, params, None, check
 
     def mse():
         ir, lowered, plan = mlp.build_mlp_mse(256, 256, 2)
         inputs, params = mlp.init_mlp_mse(256, 256, 2, seed=8)
-        return ir, lowered, plan, inputs, params, mlp.refresh_shadow
+        o = mlp_checks.MseOracle(inputs, params, 256, 256, 2)
+        return ir, lowered, plan, inputs, params, mlp.refresh_shadow, lambda ex, res: o.check(ex, "mse", res)
 
     h = C.graph_create()
     try:
         for make in (xent, mse):
             snaps = []
             for graph in (False, True):
-                ir, lowered, plan, inputs, params, prep = make()
+                ir, lowered, plan, inputs, params, prep, check = make()
                 ex = mlp.make_executor(ir, lowered, plan)
                 ex.build_env(inputs=inputs, params=params, reuse_static=False)
                 for vid in plan.statics:  # defined contents for never-written scratch
@@ -160,6 +180,8 @@ def test_recapture_of_a_different_plan_reinstantiates(C):
                 else:
                     ex.run(inputs={}, params={}, reuse_static=True)
                 torch.cuda.synchronize()
+                res = {"ok": True}
+                assert check(ex, res), res
                 snaps.append(_env_snapshot(ex))
             assert snaps[0].keys() == snaps[1].keys()
             for vid in snaps[0]:

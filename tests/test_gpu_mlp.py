@@ -105,8 +105,12 @@ def test_mlp_mse_benchmark_shape_runs_finite(C):
 
 def test_json_loaded_plan_runs_bit_identically(C):
     """The reference MLP written to the JSON IR document and read back
-    (interchange.ir_to_json / ir_from_json) lowers to the same op list and,
-    replayed as a graph, gives bit-identical loss, gradients and parameters."""
+    (interchange.ir_to_json / ir_from_json, the format of core_v2/
+    cuda_exec.py:306-371) lowers to the same op list; replayed as a graph,
+    every step of the JSON-loaded plan matches the oracle (loss and argmax,
+    all gradients <= 1e-4, AdamW bit-exact on the GPU's gradients) and is
+    bit-identical to the natively built plan."""
+    import mlp_checks
     import torch
 
     from aicf_hip import mlp
@@ -120,17 +124,25 @@ def test_json_loaded_plan_runs_bit_identically(C):
     assert lowered_to_text(lowered2, ir2.name) == lowered_to_text(lowered, ir.name)
     data = mlp.init_mlp_xent()
     results = []
-    for g_ir, g_low, g_plan in ((ir, lowered, plan), (ir2, lowered2, build_binding_plan(ir2))):
+    for tag, (g_ir, g_low, g_plan) in (("native", (ir, lowered, plan)),
+                                       ("json", (ir2, lowered2, build_binding_plan(ir2)))):
         params = {k: torch.from_numpy(v.copy()).cuda() for k, v in data.items() if "." in k}
         inputs = {"x": torch.from_numpy(data["x"]).cuda(), "t": torch.from_numpy(data["t"]).cuda()}
         ex = mlp.make_executor(g_ir, g_low, g_plan)
         ex.build_env(inputs=inputs, params=params, reuse_static=False)
         ex.capture(inputs=inputs, params=params, reuse_static=True)
-        ex.replay(3)
-        torch.cuda.synchronize()
-        snap = {k: ex.value(k).detach().cpu().clone() for k in ("loss", "d_0.W", "d_2.b")}
-        snap.update({k: p.detach().cpu().clone() for k, p in params.items()})
+        orc_state = mlp_checks.XentOracle(data)
+        res = {"ok": True}
+        snaps = []
+        for t in range(1, 4):
+            ex.replay(1)
+            torch.cuda.synchronize()
+            assert orc_state.check(ex, params, data["x"], data["t"], f"{tag}_replay{t}", res), res
+            snap = {k: ex.value(k).detach().cpu().clone() for k in ("loss", "pred", "d_0.W", "d_2.b")}
+            snap.update({k: p.detach().cpu().clone() for k, p in params.items()})
+            snaps.append(snap)
         ex.reset_graph()
-        results.append(snap)
-    for k in results[0]:
-        assert torch.equal(results[0][k], results[1][k]), k
+        results.append(snaps)
+    for a, b in zip(*results):
+        for k in a:
+            assert torch.equal(a[k], b[k]), k

@@ -163,6 +163,40 @@ def test_add_f16_is_correctly_rounded():
     assert np.array_equal(got, exact.astype(np.float16).view(np.uint16))
 
 
+def test_add_f32_is_numpy_float32_add():
+    """orc_add_f32 (add/launcher.cu:44-50: out = a + b in fp32) against
+    numpy's IEEE float32 addition: bit-identical on random magnitudes
+    spanning cancellation, denormals and the special values."""
+    r = rng(17)
+    a = (r.standard_normal(20000) * 10.0 ** r.integers(-40, 38, 20000)).astype(np.float32)
+    b = (r.standard_normal(20000) * 10.0 ** r.integers(-40, 38, 20000)).astype(np.float32)
+    b[:500] = -a[:500]                       # exact cancellation gives +0
+    b[500:1000] = np.nextafter(-a[500:1000], np.float32(0))  # one-ulp differences
+    sp = np.array([np.inf, -np.inf, np.nan, 0.0, -0.0, 1e-45, -1e-45, 3.4e38], np.float32)
+    a = np.concatenate([a, np.repeat(sp, sp.size)])
+    b = np.concatenate([b, np.tile(sp, sp.size)])
+    got = orc.add_f32(a, b)
+    want = (a + b).astype(np.float32)
+    assert np.array_equal(got.view(np.uint32)[~np.isnan(want)], want.view(np.uint32)[~np.isnan(want)])
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    # inf + -inf is NaN, -0 + -0 keeps its sign
+    i = a.size - sp.size * sp.size
+    assert np.isnan(got[i + 1]) and got.view(np.uint32)[i + 4 * 8 + 4] == np.float32(-0.0).view(np.uint32)
+
+
+def test_relu_bwd_f16_matches_numpy_mask():
+    """orc_relu_bwd_f16 (relu_bwd/launcher.cu:47-56: dY = Y > 0 ? dOut : +0,
+    as half bits) against a numpy float16 mask over every one of the 65536
+    half bit patterns of Y (NaN and -0 give +0, positive denormals pass dOut)."""
+    y = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    r = rng(18)
+    dout = r.standard_normal(65536).astype(np.float16).view(np.uint16)
+    got = orc.relu_bwd_f16(dout, y)
+    want = np.where(y.view(np.float16) > np.float16(0), dout, np.uint16(0)).astype(np.uint16)
+    assert np.array_equal(got, want)
+    assert got[0x0001] == dout[0x0001] and got[0x8000] == 0 and got[0x7E00] == 0
+
+
 def test_relu_special_values():
     x = np.array([1.5, -2.0, 0.0, -0.0, np.nan, np.inf, -np.inf, 1e-40], np.float32)
     y = orc.relu_f32(x)
