@@ -15,6 +15,8 @@
 // f16 arithmetic uses native v_*_f16 instructions, which round once, as the
 // reference's __hadd/__hmul2/__hsub2 do.  grad_zero writes zeros with a
 // kernel, not a memset, so it is safe inside captured graphs.
+#include <mutex>
+
 #include "../common/hip_util.hpp"
 
 namespace aicf::hip {
@@ -682,35 +684,37 @@ bool mse_loss_check(const TensorDesc* in, int ni, const TensorDesc* out, int no)
 bool mse_loss_sup(const TensorDesc* i, int ni, const TensorDesc* o, int no, const void*) {
   return mse_loss_check(i, ni, o, no);
 }
-Status mse_loss_launch(const TensorDesc* in, int ni, TensorDesc* out, int no, const void* a, void*,
-                       size_t, void* stream) {
-  if (!mse_loss_check(in, ni, out, no)) return Status::InvalidArgument;
-  const int64_t n = numel_of(in[0]);
-  const float sc = mse_scale(a, n);
-  hipStream_t s = as_stream(stream);
-  const bool bf = dt(in[0]) == DType::kBF16;
+// Both passes over n elements with `partial` (room for `cap` >= kMseBlocks
+// floats) holding the per-workgroup sums; every slot pass 2 reads is written
+// by pass 1 first, so the buffer needs no clearing.
+Status mse_loss_run(const void* pred, const float* tgt, void* dpred, float* loss, float* partial,
+                    int64_t cap, int64_t n, bool bf, float sc, hipStream_t s) {
   const int64_t oneshot_blocks = (n + kMseElemsPerBlock - 1) / kMseElemsPerBlock;
-  const bool oneshot = n % 8 == 0 && aligned(in[0].data, 16) && aligned(out[0].data, 16) &&
-                       oneshot_blocks <= numel_of(out[2]) && oneshot_blocks <= INT32_MAX;
+  const bool oneshot = n % 8 == 0 && aligned(pred, 16) && aligned(dpred, 16) && oneshot_blocks <= cap &&
+                       oneshot_blocks <= INT32_MAX;
   int nparts = kMseBlocks;
   if (oneshot) {
     nparts = (int)oneshot_blocks;
     if (bf)
-      mse_loss_grad_oneshot<true><<<(unsigned)nparts, 256, 0, s>>>(
-          in[0].data, (const float*)in[1].data, out[0].data, (float*)out[2].data, n / 8, sc);
+      mse_loss_grad_oneshot<true><<<(unsigned)nparts, 256, 0, s>>>(pred, tgt, dpred, partial, n / 8, sc);
     else
-      mse_loss_grad_oneshot<false><<<(unsigned)nparts, 256, 0, s>>>(
-          in[0].data, (const float*)in[1].data, out[0].data, (float*)out[2].data, n / 8, sc);
+      mse_loss_grad_oneshot<false><<<(unsigned)nparts, 256, 0, s>>>(pred, tgt, dpred, partial, n / 8, sc);
   } else if (bf) {
-    mse_loss_grad_pass1<true><<<kMseBlocks, 256, 0, s>>>(in[0].data, (const float*)in[1].data,
-                                                         out[0].data, (float*)out[2].data, n, sc);
+    mse_loss_grad_pass1<true><<<kMseBlocks, 256, 0, s>>>(pred, tgt, dpred, partial, n, sc);
   } else {
-    mse_loss_grad_pass1<false><<<kMseBlocks, 256, 0, s>>>(in[0].data, (const float*)in[1].data,
-                                                          out[0].data, (float*)out[2].data, n, sc);
+    mse_loss_grad_pass1<false><<<kMseBlocks, 256, 0, s>>>(pred, tgt, dpred, partial, n, sc);
   }
-  mse_loss_grad_pass2<<<1, 1024, 0, s>>>((const float*)out[2].data, nparts, (float*)out[1].data,
-                                         1.0 / (double)n);
+  mse_loss_grad_pass2<<<1, 1024, 0, s>>>(partial, nparts, loss, 1.0 / (double)n);
   return launch_status("mse_loss_grad_v0");
+}
+
+Status mse_loss_launch(const TensorDesc* in, int ni, TensorDesc* out, int no, const void* a, void*,
+                       size_t, void* stream) {
+  if (!mse_loss_check(in, ni, out, no)) return Status::InvalidArgument;
+  const int64_t n = numel_of(in[0]);
+  return mse_loss_run(in[0].data, (const float*)in[1].data, out[0].data, (float*)out[1].data,
+                      (float*)out[2].data, numel_of(out[2]), n, dt(in[0]) == DType::kBF16,
+                      mse_scale(a, n), as_stream(stream));
 }
 
 // ---------------------------------------------------------------------------
@@ -904,3 +908,83 @@ KernelVariant make_transpose_variant() {
 }
 
 }  // namespace aicf::hip
+
+// ---------------------------------------------------------------------------
+// MSE loss + gradient without allocation.  The partial sums of both passes
+// live in `scratch`, a library-owned device array of kMseScratchParts floats
+// (256 KiB, held on every GPU the library runs on until the process ends).
+// In host code `scratch` names a host-side stand-in, not device memory: its
+// device address is taken once per device with hipGetSymbolAddress, with
+// that device current, and only that address is handed to the kernels.
+// Calls on one GPU share the array: calls that overlap on one GPU (on
+// different streams, unordered) race on it.  Nothing in it needs clearing:
+// pass 1 writes every slot pass 2 reads.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) float scratch[65536];
+
+namespace {
+constexpr int64_t kMseScratchParts = sizeof(scratch) / sizeof(float);
+constexpr int64_t kMseNoallocMaxElems = kMseScratchParts * aicf::hip::kMseElemsPerBlock;  // 2^27
+constexpr int kMaxDevices = 64;
+static_assert(aicf::hip::kMseBlocks <= kMseScratchParts, "strided pass 1 needs kMseBlocks partials");
+
+std::mutex g_scratch_mu;
+float* g_scratch_dev[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device (looked up on the
+// first call per device), or nullptr with the error recorded.
+float* scratch_on_current_device() {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    aicf::hip::set_last_error("hipGetDevice", hipGetErrorString(e));
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    aicf::hip::set_last_error("aicf_mse_loss_grad_noalloc", "device ordinal out of range");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      aicf::hip::set_last_error("hipGetSymbolAddress", e != hipSuccess ? hipGetErrorString(e) : "null address");
+      return nullptr;
+    }
+    g_scratch_dev[dev] = static_cast<float*>(p);
+  }
+  return g_scratch_dev[dev];
+}
+}  // namespace
+
+extern "C" int32_t aicf_mse_loss_grad_noalloc(const void* pred, const float* target, void* dpred,
+                                              float* loss, int64_t n, int32_t dtype, float scale,
+                                              void* stream) {
+  using aicf::hip::aligned;
+  const char* what = "aicf_mse_loss_grad_noalloc";
+  if (!pred || !target || !dpred || !loss || n < 1) {
+    aicf::hip::set_last_error(what, "null pointer or n < 1");
+    return AICF_STATUS_INVALID_ARGUMENT;
+  }
+  if (dtype != AICF_DTYPE_F32 && dtype != AICF_DTYPE_BF16) {
+    aicf::hip::set_last_error(what, "pred/dpred dtype must be AICF_DTYPE_F32 or AICF_DTYPE_BF16");
+    return AICF_STATUS_INVALID_ARGUMENT;
+  }
+  if (n > kMseNoallocMaxElems) {
+    aicf::hip::set_last_error(what, "n exceeds 134217728 elements, the maximum of the no-allocation "
+                                    "entry point (its scratch holds 65536 partial sums)");
+    return AICF_STATUS_INVALID_ARGUMENT;
+  }
+  const uintptr_t psz = dtype == AICF_DTYPE_F32 ? 16 : 8;
+  if (!aligned(pred, psz) || !aligned(dpred, psz) || !aligned(target, 16) || !aligned(loss, 4)) {
+    aicf::hip::set_last_error(what, "misaligned pointer (pred/dpred 16 B for f32, 8 B for bf16; "
+                                    "target 16 B)");
+    return AICF_STATUS_INVALID_ARGUMENT;
+  }
+  float* part = scratch_on_current_device();
+  if (!part) return AICF_STATUS_INTERNAL;
+  return static_cast<int32_t>(aicf::hip::mse_loss_run(pred, target, dpred, loss, part, kMseScratchParts, n,
+                                                      dtype == AICF_DTYPE_BF16, scale,
+                                                      aicf::hip::as_stream(stream)));
+}

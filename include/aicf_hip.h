@@ -159,6 +159,27 @@ void aicf_cuda_register_all_kernels(void);
  * dB[n] = sum_m dY[m, n] over a row-major [M, N] fp32 matrix. */
 int32_t aicf_reduce_sum_lastdim_f32(const float* dY, float* dB, int32_t M, int32_t N, void* stream);
 
+/*
+ * No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under hipGraph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): the fused MSE loss + gradient of kernel
+ * mse_loss_grad_v0 (OpKind MseGrad with outputs dPred, loss, partials) with
+ * no partials argument.  Its per-workgroup partial sums live in a
+ * library-owned device array of 65536 floats (256 KiB on every GPU the
+ * library runs on, held until the process ends); nothing is allocated.
+ *   dpred[i] = (pred[i] - target[i]) * scale     (2/n is the reference's default)
+ *   loss[0]  = mean((pred - target)^2)
+ * pred and dpred are AICF_DTYPE_F32 or AICF_DTYPE_BF16 (`dtype`), target is
+ * fp32; pred/dpred 16-byte aligned for f32 (8 for bf16), target 16-byte.
+ * Limit: 1 <= n <= 134217728 (2^27); larger n, a null pointer, another dtype
+ * or a misaligned pointer return INVALID_ARGUMENT with aicf_last_error() set.
+ * Every call on one GPU shares that array: calls that overlap on one GPU
+ * (unordered streams) race.  Results are bit-identical to mse_loss_grad_v0
+ * given a partials buffer of at least ceil(n / 2048) floats.
+ */
+int32_t aicf_mse_loss_grad_noalloc(const void* pred, const float* target, void* dpred, float* loss,
+                                   int64_t n, int32_t dtype, float scale, void* stream);
+
 /* Measurement aid, no counterpart in the reference: launches `blocks`
  * workgroups of 4 waves, each running `iters` rounds of 8 independent
  * v_mfma_f32_32x32x16_bf16 on random register operands (no memory traffic),
