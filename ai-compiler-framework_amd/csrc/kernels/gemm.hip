@@ -39,6 +39,7 @@ namespace aicf::hip {
 namespace {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
@@ -231,6 +232,25 @@ __device__ __forceinline__ floatx16 mfma32<IN_F16>(const uint16_t* a, const uint
   const f16x8 av = __builtin_bit_cast(f16x8, *reinterpret_cast<const u16x8*>(a));
   const f16x8 bv = __builtin_bit_cast(f16x8, *reinterpret_cast<const u16x8*>(b));
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, acc, 0, 0, 0);
+}
+
+// 16 x 16 x 32 MFMA (16-bit operands): a lane holds 8 consecutive K of one
+// row of each operand; the 16 x 16 fp32 result has row (lane & 15) of the
+// A operand and 4 consecutive columns 4 (lane >> 4) .. +3 of the B operand.
+// Same flops per issue cycle as 32 x 32 x 16 with a quarter of the
+// accumulator registers per instruction: it moves half the accumulator bits
+// per flop, and on this power-limited part it sustains a ~10% higher clock.
+template <int IN>
+__device__ __forceinline__ floatx4 mfma16(const uint16_t* a, const uint16_t* b, floatx4 acc) {
+  if constexpr (IN == IN_BF16) {
+    const bf16x8 av = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8*>(a));
+    const bf16x8 bv = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8*>(b));
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, acc, 0, 0, 0);
+  } else {
+    const f16x8 av = __builtin_bit_cast(f16x8, *reinterpret_cast<const u16x8*>(a));
+    const f16x8 bv = __builtin_bit_cast(f16x8, *reinterpret_cast<const u16x8*>(b));
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc, 0, 0, 0);
+  }
 }
 
 // Grouped raster: workgroup w of XCD x (dispatch order w*8+x) gets
@@ -466,72 +486,118 @@ struct NTParams {
   float* colsum;   // see GemmParams::colsum
 };
 
-// Epilogue of the NT kernels.  Block (i, j) of the accumulators holds D[n][m];
-// this lane has m = .. + fr and n = .. + 8g + 4fh + {0..3} in
-// acc[i][j][4g .. 4g+3].  The fragments go through LDS (`smem`, at least
+// Epilogue of the NT kernels.  Block (i, j) of the accumulators holds D[n][m]
+// (MS x MS, see col_of below for the lane's elements).  The fragments go
+// through LDS (`smem`, at least
 // STAGE_BYTES, free when this is called) so that every global store, and the
 // load of the dGELU pre-activation, moves whole 512-1024 byte rows.  LDS rows
 // hold 16-byte chunks XOR-swizzled by row, which keeps both the fragment
 // writes (32 rows, one chunk each) and the row reads bank-balanced.  A tile
-// that does not fit (fp32 256x256) is done in passes over the wave's 32-row
+// that does not fit (fp32 256x256) is done in passes over the wave's MS-row
 // fragment groups.
-template <int OUT, int ACT, int BM, int BN, int WM, int WN, int STAGE_BYTES>
+template <int MS>
+using nt_acc_t = typename std::conditional<MS == 16, floatx4, floatx16>::type;
+
+template <int OUT, int ACT, int BM, int BN, int WM, int WN, int STAGE_BYTES, int MS>
 __device__ __forceinline__ void nt_epilogue_staged(const NTParams& p,
-                                                   floatx16 (&acc)[BN / WN / 32][BM / WM / 32],
+                                                   nt_acc_t<MS> (&acc)[BN / WN / MS][BM / WM / MS],
                                                    uint8_t* smem, int m0, int n0) {
   constexpr int NW = WM * WN;
   constexpr int WTM = BM / WM, WTN = BN / WN;
-  constexpr int TM = WTM / 32, TN = WTN / 32;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  constexpr int TM = WTM / MS, TN = WTN / MS;
+  // 32 x 32 blocks: lane (fr, fh) holds row fr, columns 8 g + 4 fh + {0..3}
+  // in acc[..][4 g .. 4 g + 3] (g = 0..3); 16 x 16 blocks: row fr, columns
+  // 4 fh + {0..3} in acc[0..3].
+  constexpr int G = MS == 32 ? 4 : 1;
+  // The lane's coordinates come from a thread index the compiler cannot see
+  // through (see opaque_tid below): the LDS slots derived from them are then
+  // computed here rather than hoisted out of the persistent tile loop and
+  // spilled across the K loop.
+  int tid_e = threadIdx.x;
+  asm volatile("" : "+v"(tid_e));
+  const int lane = tid_e & 63, wave = tid_e >> 6;
   const int wm = wave / WN, wn = wave % WN;
-  const int fr = lane & 31, fh = lane >> 5;
+  const int fr = lane % MS, fh = lane / MS;
+  auto col_of = [&](int i, int g) -> int { return wn * WTN + i * MS + (MS == 32 ? 8 * g + 4 * fh : 4 * fh); };
   constexpr int NT = 64 * NW;
   constexpr int OB = OUT == OUT_F32 ? 4 : 2;
   constexpr int ROWB = BN * OB;    // bytes per staged row
   constexpr int CPR = ROWB / 16;   // 16-byte chunks per row
-  constexpr int ROWS_PASS = STAGE_BYTES / ROWB < BM ? STAGE_BYTES / ROWB : BM;
+  // GELU stages the pre-activation z and the activation side by side (two
+  // regions of half the staging bytes, so half the rows per pass): the
+  // accumulators of a pass are dead once both are staged, and none are live
+  // beside the copies of the other outputs.
+  constexpr bool GELU_DUAL = ACT == ACT_GELU;
+  constexpr int REGION = GELU_DUAL ? STAGE_BYTES / 2 : STAGE_BYTES;
+  constexpr int ROWS_PASS = REGION / ROWB < BM ? REGION / ROWB : BM;
   constexpr int NPASS = BM / ROWS_PASS;
-  constexpr int JP = TM / NPASS;   // 32-row fragment groups per wave per pass
-  constexpr int WROWS = JP * 32;   // rows per wave per pass
+  constexpr int JP = TM / NPASS;   // MS-row fragment groups per wave per pass
+  constexpr int WROWS = JP * MS;   // rows per wave per pass
   static_assert(NPASS * ROWS_PASS == BM && JP * NPASS == TM, "pass split");
   static_assert((CPR & (CPR - 1)) == 0 && (ROWS_PASS * CPR) % NT == 0, "chunk split");
   uint8_t* const tile = smem;
 
-  if constexpr (ACT != ACT_DGELU && ACT != ACT_ADAMW) {
-    if (p.bias) {
+  // Bias of the lane's columns.  32 x 32 blocks: added to the accumulators
+  // in place (8 floats per block).  16 x 16 blocks: the lane's 4 x TN bias
+  // values are loaded once and added where each fragment is staged; an
+  // in-place pass over 32 small accumulator blocks behind the runtime bias
+  // test makes the compiler materialise all of them a second time and spill.
+  constexpr bool HAS_BIAS_ACT = ACT != ACT_DGELU && ACT != ACT_ADAMW;
+  const bool with_bias = HAS_BIAS_ACT && p.bias != nullptr;
+  auto bias4 = [&](int i, int g, float* b) {
+    const int n = n0 + col_of(i, g);
+    if (p.bias_f32) {
+      const f32x4 bv = *reinterpret_cast<const f32x4*>((const float*)p.bias + n);
 #pragma unroll
-      for (int i = 0; i < TN; ++i)
+      for (int e = 0; e < 4; ++e) b[e] = bv[e];
+    } else {
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int n = n0 + wn * WTN + i * 32 + 8 * g + 4 * fh;
-          float b[4];
-          if (p.bias_f32) {
-            const f32x4 bv = *reinterpret_cast<const f32x4*>((const float*)p.bias + n);
+      for (int e = 0; e < 4; ++e) b[e] = load_out<OUT>(p.bias, n + e);
+    }
+  };
+  constexpr int BI = MS == 16 ? TN : 1;
+  float bias_v[BI][4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) b[e] = bv[e];
-          } else {
+  for (int i = 0; i < BI; ++i)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) b[e] = load_out<OUT>(p.bias, n + e);
+    for (int e = 0; e < 4; ++e) bias_v[i][e] = 0.0f;
+  if constexpr (HAS_BIAS_ACT) {
+    if (with_bias) {
+      if constexpr (MS == 16) {
+#pragma unroll
+        for (int i = 0; i < TN; ++i) bias4(i, 0, bias_v[i]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            float b[4];
+            bias4(i, g, b);
+#pragma unroll
+            for (int j = 0; j < TM; ++j)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) acc[i][j][4 * g + e] += b[e];
           }
-#pragma unroll
-          for (int j = 0; j < TM; ++j)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) acc[i][j][4 * g + e] += b[e];
-        }
+      }
     }
   }
+  // accumulators of fragment (j, i, g), plus the bias for 16 x 16 blocks
+  auto frag4 = [&](int j, int i, int g, float* v) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * g + e];
+    if constexpr (MS == 16) {
+      if (with_bias) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] += bias_v[i][e];
+      }
+    }
+  };
 
   // byte offset of this lane's 4 outputs of fragment (jj, i, g) in the tile
   auto slot = [&](int jj, int i, int g) -> int {
-    const int pr = wm * WROWS + jj * 32 + fr;
-    int c, half;
-    if constexpr (OB == 2) {
-      c = (wn * WTN + i * 32) / 8 + g;
-      half = fh * 8;
-    } else {
-      c = (wn * WTN + i * 32) / 4 + 2 * g + fh;
-      half = 0;
-    }
+    const int pr = wm * WROWS + jj * MS + fr;
+    const int cb = col_of(i, g) * OB;  // byte of the 4 outputs in the row
+    const int c = cb / 16, half = cb % 16;
     return pr * ROWB + ((c ^ (pr & (CPR - 1))) * 16) + half;
   };
   auto put4 = [&](int off, const float* v) {
@@ -574,13 +640,16 @@ __device__ __forceinline__ void nt_epilogue_staged(const NTParams& p,
     return t;
   };
   // tile rows of this pass -> global matrix (row stride ld elements)
-  auto copy_out = [&](int pass, void* dst, int64_t ld) {
+  // (at most four 16-byte chunks in flight: the GELU epilogue calls this
+  // with all accumulators live, and more in flight spill them)
+  auto copy_out = [&](int pass, void* dst, int64_t ld, const uint8_t* src = nullptr) {
+    const uint8_t* from = src ? src : tile;
     const int tid = opaque_tid();
-#pragma unroll
+#pragma unroll 4
     for (int k = 0; k < ROWS_PASS * CPR / NT; ++k) {
       const int idx = tid + k * NT;
       const int pr = idx / CPR, c = idx % CPR;
-      const u16x8 x = *reinterpret_cast<const u16x8*>(tile + pr * ROWB + ((c ^ (pr & (CPR - 1))) * 16));
+      const u16x8 x = *reinterpret_cast<const u16x8*>(from + pr * ROWB + ((c ^ (pr & (CPR - 1))) * 16));
       *reinterpret_cast<u16x8*>((uint8_t*)dst + (grow(pass, pr) * ld + n0) * OB + c * 16) = x;
     }
   };
@@ -680,17 +749,16 @@ __device__ __forceinline__ void nt_epilogue_staged(const NTParams& p,
       copy_in(pass, p.aux, p.aux_ld);
       __syncthreads();
     }
-    if constexpr (ACT == ACT_GELU) {
+    if constexpr (ACT == ACT_GELU && !GELU_DUAL) {
       if (p.aux) {  // pre-activation z
 #pragma unroll
         for (int jj = 0; jj < JP; ++jj)
 #pragma unroll
           for (int i = 0; i < TN; ++i)
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
+            for (int g = 0; g < G; ++g) {
               float v[4];
-#pragma unroll
-              for (int e = 0; e < 4; ++e) v[e] = acc[i][pass * JP + jj][4 * g + e];
+              frag4(pass * JP + jj, i, g, v);
               put4(slot(jj, i, g), v);
             }
         __syncthreads();
@@ -703,11 +771,10 @@ __device__ __forceinline__ void nt_epilogue_staged(const NTParams& p,
 #pragma unroll
       for (int i = 0; i < TN; ++i)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
+        for (int g = 0; g < G; ++g) {
           const int off = slot(jj, i, g);
           float v[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = acc[i][pass * JP + jj][4 * g + e];
+          frag4(pass * JP + jj, i, g, v);
           if constexpr (ACT == ACT_DGELU) {
             float z[4];
             get4(off, z);  // this lane's own slot: no barrier between read and write
@@ -717,13 +784,19 @@ __device__ __forceinline__ void nt_epilogue_staged(const NTParams& p,
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[e] = v[e] > 0.0f ? v[e] : 0.0f;
           } else if constexpr (ACT == ACT_GELU) {
+            if constexpr (GELU_DUAL) {
+              if (p.aux) put4(REGION + off, v);  // pre-activation z
+            }
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[e] = gelu_tanh_f(v[e]);
           }
           put4(off, v);
         }
     __syncthreads();
-    if constexpr (ACT == ACT_ADAMW) {
+    if constexpr (GELU_DUAL) {
+      if (p.aux) copy_out(pass, p.aux, p.aux_ld, tile + REGION);
+      copy_out(pass, p.C, p.ldc);
+    } else if constexpr (ACT == ACT_ADAMW) {
       adam_out(pass);
     } else if constexpr (ACT == ACT_DGELU && OUT == OUT_BF16 && NPASS == 1 && CPR == 32 && NT == 512) {
       if (p.colsum)
@@ -746,19 +819,29 @@ using template_int_t = std::integral_constant<int, V>;
 // share of the NV loads (load u after MFMA t when t*NV/NMF <= u <
 // (t+1)*NV/NMF).  sched_group_barrier masks: 0x008 MFMA, 0x100 DS read,
 // 0x020 VMEM read.
-template <int TM, int TN, int ES, bool AKC, bool BKC>
+template <int TM, int TN, int ES, bool AKC, bool BKC, int MS>
 struct NTSched {
   static constexpr int NMF = TM * TN * (ES == 4 ? 4 : 1);  // MFMAs per sub-step
   static constexpr int NFR = TM + TN;                      // fragments per sub-step
   static constexpr int FPER = (NFR + NMF - 1) / NMF;       // fragments per MFMA
+  // 16 x 16 blocks (RECYCLE): the MFMAs run A-fragment-major (t -> block
+  // (t % TN, t / TN)) and the next sub-step's A fragment j is read into the
+  // same registers right after its last MFMA (t = j TN + TN - 1), so only
+  // the B fragments are double-buffered; the next B fragment t is read after
+  // MFMA t.  Otherwise fragment r (A for r < TM, else B) after MFMA r / FPER.
+  static constexpr bool RECYCLE = MS == 16;
   static constexpr int ds_instrs(int lo, int hi) {
     int n = 0;
     for (int r = lo; r < hi && r < NFR; ++r) n += r < TM ? (AKC ? 1 : 2) : (BKC ? 1 : 2);
     return n;
   }
+  static constexpr int ds_after(int t) {
+    if (!RECYCLE) return ds_instrs(t * FPER, (t + 1) * FPER);
+    return (t < TN ? (BKC ? 1 : 2) : 0) + (t % TN == TN - 1 ? (AKC ? 1 : 2) : 0);
+  }
   template <bool R, int NV, int T>
   static __device__ __forceinline__ void step() {
-    constexpr int nds = R ? ds_instrs(T * FPER, (T + 1) * FPER) : 0;
+    constexpr int nds = R ? ds_after(T) : 0;
     constexpr int vlo = T * NV / NMF, vhi = (T + 1) * NV / NMF;
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
     if constexpr (nds > 0) __builtin_amdgcn_sched_group_barrier(0x100, nds, 0);
@@ -783,14 +866,24 @@ struct NTSched {
 //     8j + lane/8, physical chunk lane%8.
 //   MN-contiguous (memory [K][MN] with row stride ld): 64 K-rows of BMN
 //     elements; row k keeps logical chunk c (8 MN-elements) at physical chunk
-//     c ^ (4 (k & 3)).  A fragment (32 MN x 16 K) is two ds_read_b64_tr_b16:
-//     in each 16-lane group lane j points at row k0 + j/4, elements
-//     m + 4 (j%4) .. +3, and the transposing read hands lane i the four K
-//     values of element m + i; the swizzle keeps the 4-row x 32-byte pattern
-//     of a group conflict-free.
+//     c ^ nt_mn_swizzle(k).  A fragment (MS MN x 16 or 32 K) is two
+//     ds_read_b64_tr_b16 per 16-lane group: lane j points at row k0 + j/4,
+//     elements m + 4 (j%4) .. +3, and the transposing read hands lane i the
+//     four K values of element m + i.  The 32 lanes of one LDS pass read 8
+//     K-rows: with 32 x 32 fragments (groups 0 and 1 at MN + 0 and + 16)
+//     c ^ 4 (k & 3) keeps them on distinct banks; with 16 x 16 fragments
+//     both groups read the same 16 MN elements 8 rows apart, and the extra
+//     2 ((k >> 3) & 1) term moves the second group to the other bank half.
+//   K-contiguous rows are 128 B: the chunk c ^ ((r >> 1) & 7) keeps the 32
+//     (or 16) rows of one fragment read on all 64 banks.
 // Loads are buffer loads straight into LDS with per-lane offsets fixed for
 // the whole K loop (the K advance is the scalar offset); the host checks that
 // the bytes a resource spans fit a signed 32-bit offset.
+template <int MS>
+__device__ __forceinline__ int nt_mn_swizzle(int k) {
+  return MS == 16 ? ((4 * (k & 3)) ^ (2 * ((k >> 3) & 1))) : 4 * (k & 3);
+}
+
 template <bool KC, int BMN, int NW, int ES>
 struct NTOperand {
   static constexpr int BYTES = BMN * 128;            // a stage holds 128 B of K per row
@@ -805,7 +898,7 @@ struct NTOperand {
   int soff_step;  // scalar byte offset per K-step
 };
 
-template <bool KC, int BMN, int NW, int ES>
+template <bool KC, int BMN, int NW, int ES, int MS>
 __device__ __forceinline__ void nt_operand_init(NTOperand<KC, BMN, NW, ES>& o, const void* X, int64_t ld,
                                                 int mn0, int K, int lane, int wave) {
   const uint8_t* Xb = static_cast<const uint8_t*>(X);
@@ -828,7 +921,7 @@ __device__ __forceinline__ void nt_operand_init(NTOperand<KC, BMN, NW, ES>& o, c
     for (int t = 0; t < o.BLOCKS; ++t) {
       const int q = wave + t * NW;
       const int k = q * RPB + lane / CPR;
-      const int c = (lane % CPR) ^ (4 * (k & 3));
+      const int c = (lane % CPR) ^ nt_mn_swizzle<MS>(k);
       o.voff[t] = (k * (int)ld + c * 8) * 2;
     }
     o.soff_step = 64 * (int)ld * 2;
@@ -847,10 +940,14 @@ constexpr bool nt_persistent(int BM, int BN, int WM, int WN) {
 template <int IN, int OUT, int ACT, int BM, int BN, int WM, int WN, bool AKC, bool BKC>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_nt_kernel(NTParams p) {
   constexpr int ES = IN == IN_F32 ? 4 : 2;  // element bytes
-  constexpr int KS = 4;                      // MFMA sub-steps per K-step (one 16-byte chunk pair each)
+  // MFMA block: 16 x 16 x 32 for 16-bit operands, 32 x 32 x 2 for fp32
+  constexpr int MS = ES == 2 ? 16 : 32;
+  constexpr int KS = MS == 16 ? 2 : 4;  // MFMA sub-steps per K-step
+  constexpr int CPS = 64 / MS;          // 16-byte chunks of a 128-byte K-row per sub-step
+  constexpr int KPS = 16 * CPS / 2;     // K-rows of an MN-contiguous stage per sub-step (16-bit)
   constexpr int NW = WM * WN;
   constexpr int WTM = BM / WM, WTN = BN / WN;
-  constexpr int TM = WTM / 32, TN = WTN / 32;
+  constexpr int TM = WTM / MS, TN = WTN / MS;
   constexpr int A_BYTES = BM * 128, B_BYTES = BN * 128;  // 128 B of K per row and stage
   constexpr int STAGE = A_BYTES + B_BYTES;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE];
@@ -886,27 +983,34 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt_kernel(NTParams p) {
     for (int u = 0; u < NVM; ++u) load_one(kt, stage, u);
   };
 
-  floatx16 acc[TN][TM];
+  nt_acc_t<MS> acc[TN][TM];
 
   // Fragment addresses.  K-contiguous: row offset of the lane's MN-row plus
-  // the swizzled chunk of (sub-step, half).  MN-contiguous: the lane's K-row
-  // within a sub-step and its swizzled column bytes (loop invariant).
-  const int fr = lane & 31, fh = lane >> 5;
-  const int rsw = (fr >> 1) & 7;  // fragment rows start at multiples of 32
+  // the swizzled chunk of (sub-step, lane group).  MN-contiguous: the lane's
+  // K-row within a sub-step and its swizzled column bytes (loop invariant).
+  // A lane of an MS x MS block holds MN-row fr and K chunk fh of the
+  // sub-step (8 K per 16-byte chunk).
+  const int fr = lane % MS, fh = lane / MS;
+  const int rsw = (fr >> 1) & 7;  // fragment rows start at multiples of MS
   const int g16 = (lane >> 4) & 3, i16 = lane & 15;
-  const int tr_row = (8 * (g16 >> 1) + (i16 >> 2));
+  // 32 x 32: groups 0/1 take MN + 0/16 of K-rows 0-7, groups 2/3 K-rows
+  // 8-15; 16 x 16: group g takes K-rows 8 g .. 8 g + 7 of the same 16 MN
+  const int tr_row = MS == 32 ? (8 * (g16 >> 1) + (i16 >> 2)) : (8 * g16 + (i16 >> 2));
   auto tr_col = [&](int mb) {  // byte offset of the lane's 8-byte piece in a K-row
-    return ((((mb >> 3) ^ (4 * ((i16 >> 2) & 3))) + 2 * (g16 & 1) + ((i16 >> 1) & 1)) * 16) + 8 * (i16 & 1);
+    if constexpr (MS == 32)
+      return ((((mb >> 3) ^ (4 * ((i16 >> 2) & 3))) + 2 * (g16 & 1) + ((i16 >> 1) & 1)) * 16) + 8 * (i16 & 1);
+    else
+      return ((((mb >> 3) ^ nt_mn_swizzle<MS>(tr_row)) + ((i16 >> 1) & 1)) * 16) + 8 * (i16 & 1);
   };
   int a_off[TM], b_off[TN];
 #pragma unroll
   for (int j = 0; j < TM; ++j) {
-    const int mb = wm * WTM + j * 32;
+    const int mb = wm * WTM + j * MS;
     a_off[j] = AKC ? (mb + fr) * 128 : tr_row * (BM * 2) + tr_col(mb);
   }
 #pragma unroll
   for (int i = 0; i < TN; ++i) {
-    const int nb = wn * WTN + i * 32;
+    const int nb = wn * WTN + i * MS;
     b_off[i] = A_BYTES + (BKC ? (nb + fr) * 128 : tr_row * (BN * 2) + tr_col(nb));
   }
 
@@ -925,40 +1029,49 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt_kernel(NTParams p) {
 
   u16x8 fa[2][TM], fb[2][TN];
   auto read_frags = [&](const uint8_t* st, int kk, int buf) {
-    const int chunk = ((kk * 2 + fh) ^ rsw) * 16;
+    const int chunk = ((kk * CPS + fh) ^ rsw) * 16;
 #pragma unroll
     for (int j = 0; j < TM; ++j) {
-      if constexpr (AKC) fa[buf][j] = *reinterpret_cast<const u16x8*>(st + a_off[j] + chunk);
-      else fa[buf][j] = tr_frag(st + a_off[j] + kk * 16 * (BM * ES), BM * ES);
+      const int ab = MS == 16 ? 0 : buf;
+      if constexpr (AKC) fa[ab][j] = *reinterpret_cast<const u16x8*>(st + a_off[j] + chunk);
+      else fa[ab][j] = tr_frag(st + a_off[j] + kk * KPS * (BM * ES), BM * ES);
     }
 #pragma unroll
     for (int i = 0; i < TN; ++i) {
       if constexpr (BKC) fb[buf][i] = *reinterpret_cast<const u16x8*>(st + b_off[i] + chunk);
-      else fb[buf][i] = tr_frag(st + b_off[i] + kk * 16 * (BN * ES), BN * ES);
+      else fb[buf][i] = tr_frag(st + b_off[i] + kk * KPS * (BN * ES), BN * ES);
     }
   };
   // Single operations of the pipeline, emitted one by one in the order the
   // schedule below pins (the compiler keeps LDS-writing loads and LDS reads
   // in program order, so the order has to be written out).
-  //   fragment r: r < TM is A fragment r, else B fragment r - TM (one
+  //   fragment f: f < TM is A fragment f, else B fragment f - TM (one
   //     ds_read_b128, or two ds_read_b64_tr_b16 for an M/N-contiguous tile);
-  //   MFMA t: block (i, j) = (t / TM % TN, t % TM); fp32 runs 4 MFMAs per
-  //     block and sub-step, t / (TM * TN) selecting the fragment element;
+  //     with RECYCLE (NTSched) the A fragments use register set 0 only;
+  //   MFMA t: block (i, j) = (t / TM % TN, t % TM), or (t % TN, t / TN) with
+  //     RECYCLE; fp32 runs 4 MFMAs per block and sub-step, t / (TM * TN)
+  //     selecting the fragment element;
   //   load u: 1 KB direct-to-LDS block u of the wave (A blocks first).
-  auto read_one = [&](const uint8_t* st, int kk, int buf, int r) {
-    const int chunk = ((kk * 2 + fh) ^ rsw) * 16;
-    if (r < TM) {
-      if constexpr (AKC) fa[buf][r] = *reinterpret_cast<const u16x8*>(st + a_off[r] + chunk);
-      else fa[buf][r] = tr_frag(st + a_off[r] + kk * 16 * (BM * ES), BM * ES);
+  using Sched = NTSched<TM, TN, ES, AKC, BKC, MS>;
+  constexpr bool RECYCLE = Sched::RECYCLE;
+  auto read_one = [&](const uint8_t* st, int kk, int buf, int f) {
+    const int chunk = ((kk * CPS + fh) ^ rsw) * 16;
+    if (f < TM) {
+      const int ab = RECYCLE ? 0 : buf;
+      if constexpr (AKC) fa[ab][f] = *reinterpret_cast<const u16x8*>(st + a_off[f] + chunk);
+      else fa[ab][f] = tr_frag(st + a_off[f] + kk * KPS * (BM * ES), BM * ES);
     } else {
-      const int i = r - TM;
+      const int i = f - TM;
       if constexpr (BKC) fb[buf][i] = *reinterpret_cast<const u16x8*>(st + b_off[i] + chunk);
-      else fb[buf][i] = tr_frag(st + b_off[i] + kk * 16 * (BN * ES), BN * ES);
+      else fb[buf][i] = tr_frag(st + b_off[i] + kk * KPS * (BN * ES), BN * ES);
     }
   };
   auto mfma_one = [&](int buf, int t) {
-    const int i = (t / TM) % TN, j = t % TM;
-    if constexpr (ES == 2) {
+    const int i = RECYCLE ? t % TN : (t / TM) % TN, j = RECYCLE ? t / TN : t % TM;
+    if constexpr (MS == 16) {
+      acc[i][j] = mfma16<IN>(reinterpret_cast<const uint16_t*>(&fb[buf][i]),
+                             reinterpret_cast<const uint16_t*>(&fa[0][j]), acc[i][j]);
+    } else if constexpr (ES == 2) {
       acc[i][j] = mfma32<IN>(reinterpret_cast<const uint16_t*>(&fb[buf][i]),
                              reinterpret_cast<const uint16_t*>(&fa[buf][j]), acc[i][j]);
     } else {
@@ -968,7 +1081,6 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt_kernel(NTParams p) {
       acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc[i][j], 0, 0, 0);
     }
   };
-  using Sched = NTSched<TM, TN, ES, AKC, BKC>;
   constexpr int NMF = Sched::NMF, NFR = Sched::NFR, FPER = Sched::FPER;
   // One sub-step: the MFMAs on fragment buffer `buf`; when R, the fragments
   // of sub-step rkk of stage `rst` into buffer rbuf (front-loaded, FPER per
@@ -980,9 +1092,14 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt_kernel(NTParams p) {
     for (int t = 0; t < NMF; ++t) {
       mfma_one(buf, t);
       if constexpr (decltype(R)::value) {
+        if constexpr (RECYCLE) {
+          if (t < TN) read_one(rst, rkk, rbuf, TM + t);
+          if (t % TN == TN - 1) read_one(rst, rkk, rbuf, t / TN);
+        } else {
 #pragma unroll
-        for (int q = 0; q < FPER; ++q)
-          if (t * FPER + q < NFR) read_one(rst, rkk, rbuf, t * FPER + q);
+          for (int q = 0; q < FPER; ++q)
+            if (t * FPER + q < NFR) read_one(rst, rkk, rbuf, t * FPER + q);
+        }
       }
       if constexpr (nv > 0) {
 #pragma unroll
@@ -995,16 +1112,17 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt_kernel(NTParams p) {
   using NoRd = std::false_type;
   template_int_t<0> z;
 
-  // Pipeline.  A K-step (128 bytes of K per row) has four sub-steps; the
+  // Pipeline.  A K-step (128 bytes of K per row) has KS sub-steps (four of
+  // 32 x 32 x 16 or 32 x 32 x 2 MFMAs, or two of 16 x 16 x 32); the
   // fragments of sub-step s+1 are read during the MFMAs of sub-step s, from
   // two register sets.  The body of the K loop starts with the K-step's only
   // barrier: after it the stage of K-step kt+1 is visible to every wave and
   // the stage of K-step kt is read by none, so the loads of K-step kt+2
   // refill it.  The body then runs the last sub-step of kt (its fragments are
-  // already in registers) and sub-steps 0-2 of kt+1, with the loads of kt+2
-  // spread over its first two sub-steps: issued all at once after the barrier
-  // they back up the address queue and stall the MFMA issue, and issued in
-  // the third sub-step they have too little time left before the next wait.
+  // already in registers) and the other sub-steps of kt+1, with the loads of
+  // kt+2 spread over the first half of the body: issued all at once after the
+  // barrier they back up the address queue and stall the MFMA issue, and
+  // issued later they have too little time left before the next wait.
   // Tiles: the grid covers all tiles (one per workgroup), or, persistent,
   // one workgroup per CU loops over tiles blockIdx.x + q * gridDim.x, so that
   // the global stores of a tile's epilogue drain while the next tile's loads
@@ -1019,49 +1137,64 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt_kernel(NTParams p) {
     m0 = tm_i * BM;
     n0 = tn_i * BN;
   }
-  nt_operand_init(opa, p.A, p.lda, m0, p.K, lane, wave);
-  nt_operand_init(opb, p.B, p.ldb, n0, p.K, lane, wave);
+  nt_operand_init<AKC, BM, NW, ES, MS>(opa, p.A, p.lda, m0, p.K, lane, wave);
+  nt_operand_init<BKC, BN, NW, ES, MS>(opb, p.B, p.ldb, n0, p.K, lane, wave);
 #pragma unroll
   for (int i = 0; i < TN; ++i)
 #pragma unroll
     for (int j = 0; j < TM; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+      for (int r = 0; r < (MS == 16 ? 4 : 16); ++r) acc[i][j][r] = 0.0f;
 
   const int nk = p.K / (128 / ES);
-  constexpr int L1 = NVM / 2;  // loads in the first of the two sub-steps
+  constexpr int L1 = NVM / 2;  // with four sub-steps: loads in the first of the two
   issue_loads(0, 0);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (nk > 1) issue_loads(1, 1);
   read_frags(smem, 0, 0);
-  substep(Rd{}, z, z, 0, smem, 1, 1, 0, 0);
-  substep(Rd{}, z, z, 1, smem, 2, 0, 0, 0);
-  substep(Rd{}, z, z, 0, smem, 3, 1, 0, 0);
+  if constexpr (KS == 4) {
+    substep(Rd{}, z, z, 0, smem, 1, 1, 0, 0);
+    substep(Rd{}, z, z, 1, smem, 2, 0, 0, 0);
+    substep(Rd{}, z, z, 0, smem, 3, 1, 0, 0);
+  } else {
+    substep(Rd{}, z, z, 0, smem, 1, 1, 0, 0);
+  }
   int kt = 0;
   for (; kt + 2 < nk; ++kt) {
     __builtin_amdgcn_s_waitcnt(0);  // own loads of K-step kt+1 and fragment reads done
     __syncthreads();
     const uint8_t* nx = smem + ((kt + 1) & 1) * STAGE;
     const int ls = kt & 1;
-    substep(Rd{}, z, template_int_t<L1>{}, 1, nx, 0, 0, kt + 2, ls);
-    substep(Rd{}, template_int_t<L1>{}, template_int_t<NVM>{}, 0, nx, 1, 1, kt + 2, ls);
-    substep(Rd{}, z, z, 1, nx, 2, 0, 0, 0);
-    substep(Rd{}, z, z, 0, nx, 3, 1, 0, 0);
+    if constexpr (KS == 4) {
+      substep(Rd{}, z, template_int_t<L1>{}, 1, nx, 0, 0, kt + 2, ls);
+      substep(Rd{}, template_int_t<L1>{}, template_int_t<NVM>{}, 0, nx, 1, 1, kt + 2, ls);
+      substep(Rd{}, z, z, 1, nx, 2, 0, 0, 0);
+      substep(Rd{}, z, z, 0, nx, 3, 1, 0, 0);
+    } else {
+      // two sub-steps of twice the MFMAs: the loads of K-step kt+2 over the first
+      substep(Rd{}, z, template_int_t<NVM>{}, 1, nx, 0, 0, kt + 2, ls);
+      substep(Rd{}, z, z, 0, nx, 1, 1, 0, 0);
+    }
   }
   if (kt + 1 < nk) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     const uint8_t* nx = smem + ((kt + 1) & 1) * STAGE;
-    substep(Rd{}, z, z, 1, nx, 0, 0, 0, 0);
-    substep(Rd{}, z, z, 0, nx, 1, 1, 0, 0);
-    substep(Rd{}, z, z, 1, nx, 2, 0, 0, 0);
-    substep(Rd{}, z, z, 0, nx, 3, 1, 0, 0);
+    if constexpr (KS == 4) {
+      substep(Rd{}, z, z, 1, nx, 0, 0, 0, 0);
+      substep(Rd{}, z, z, 0, nx, 1, 1, 0, 0);
+      substep(Rd{}, z, z, 1, nx, 2, 0, 0, 0);
+      substep(Rd{}, z, z, 0, nx, 3, 1, 0, 0);
+    } else {
+      substep(Rd{}, z, z, 1, nx, 0, 0, 0, 0);
+      substep(Rd{}, z, z, 0, nx, 1, 1, 0, 0);
+    }
   }
   substep(NoRd{}, z, z, 1, nullptr, 0, 0, 0, 0);
 
   __syncthreads();  // every wave is done reading the last stage
-  nt_epilogue_staged<OUT, ACT, BM, BN, WM, WN, 2 * STAGE>(p, acc, smem, m0, n0);
+  nt_epilogue_staged<OUT, ACT, BM, BN, WM, WN, 2 * STAGE, MS>(p, acc, smem, m0, n0);
   if constexpr (!PERSIST) break;  // one tile per workgroup: no loop-carried registers
   __syncthreads();  // the staged tile is read out before the next tile's loads refill the stages
   }

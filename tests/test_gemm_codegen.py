@@ -210,3 +210,17 @@ def test_asm_offset_guard_flags_a_planted_write(asm):
     assert _written_vgprs("\tds_read_b128 v[4:7], v1 offset:16") == {4, 5, 6, 7}
     assert _written_vgprs("\tds_write_b128 v1, v[4:7]") == set()
     assert _is_vm_drain("\ts_waitcnt vmcnt(0) lgkmcnt(0)") and not _is_vm_drain("\ts_waitcnt vmcnt(3)")
+
+
+def test_no_nt_kernel_uses_scratch(asm):
+    """Every gemm_nt_kernel instantiation (4- and 8-wave, every epilogue and
+    operand layout) keeps its registers within the file: no private segment
+    (spill) bytes in its kernel descriptor."""
+    found = 0
+    for m in re.finditer(r"\.amdhsa_kernel (\S+)\n(.*?)\.end_amdhsa_kernel", asm, re.S):
+        if "gemm_nt_kernel" not in m.group(1):
+            continue
+        found += 1
+        seg = re.search(r"\.amdhsa_private_segment_fixed_size\s+(\d+)", m.group(2))
+        assert seg and int(seg.group(1)) == 0, (m.group(1), seg.group(1) if seg else None)
+    assert found > 100, found
