@@ -7,9 +7,9 @@
 //   graph_launch / graph_reset / graph_stream.
 // Every call goes through the C-ABI of libaicf_hip (include/aicf_hip.h); this
 // file holds no HIP code.  Differences: bf16 tensors are accepted
-// (DType::kBF16 = 3), HIP errors read "[HIP] ...", and graph_launch orders
-// the replay after the work already queued on torch's current stream and
-// before the work queued there afterwards (also on the default stream).
+// (DType::kBF16 = 3), HIP errors read "[HIP] ...", and graph_launch replays
+// on torch's current stream (ordered after the work already queued there and
+// before the work queued there afterwards).
 #include <c10/hip/HIPStream.h>
 #include <pybind11/pybind11.h>
 #include <pybind11/stl.h>

@@ -803,7 +803,7 @@ __device__ __forceinline__ void nt_epilogue_staged(const NTParams& p,
         copy_out_colsum();
       else
         copy_out(pass, p.C, p.ldc);
-    } else {
+    } else {  // (run_gemm sends column-sum launches to the branch above only)
       copy_out(pass, p.C, p.ldc);
     }
     if (pass + 1 < NPASS) __syncthreads();
@@ -1405,7 +1405,10 @@ template <int IN, int OUT>
 Status run_gemm(GemmParams& p, hipStream_t s) {
   if (p.colsum) {  // dGELU with column sums: the 8-wave 256 x 256 bf16-output path only
     if constexpr (OUT == OUT_BF16 && IN != IN_F32) {
-      if (p.act == ACT_DGELU && nt_eligible<IN, OUT>(p, 256, 256, true)) return run_nt256<IN, OUT>(p, s);
+      // the column sums live in that configuration's epilogue (8 waves,
+      // whole tile in one pass): dispatch to it directly
+      if (p.act == ACT_DGELU && nt_eligible<IN, OUT>(p, 256, 256, true))
+        return run_nt<IN, OUT, 256, 256, 2, 4, true>(p, s);
     }
     return Status::NotImplemented;
   }

@@ -13,14 +13,13 @@
 // same topology - the usual case when a plan is captured again with other
 // buffers bound - and instantiates afresh only when the update is refused.
 //
-// Launch orders the replay between the caller's work on both sides: the
-// graph stream first waits on an event recorded on the caller's stream (so
-// input copies and device-scalar updates queued there run before the
-// replay), and the caller's stream then waits on an event recorded after the
-// replay (so what it queues next reads the replay's results).  A NULL caller
-// stream is the null stream, torch's default; the graph stream is created
-// non-blocking and would not otherwise synchronise with it.  The reference
-// replays with no such edges.
+// Launch replays the executable on the caller's stream (NULL: the null
+// stream, torch's default), so the replay runs after the work already queued
+// there (input copies, host-side updates of device scalars) and before the
+// work queued there afterwards (reads of its results), in stream order and
+// with no cross-stream events.  The dedicated stream is the capture stream.
+// The reference replays on its dedicated stream with no ordering against
+// the caller's work.
 #include <hip/hip_runtime_api.h>
 
 #include <map>
@@ -38,15 +37,11 @@ struct GraphState {
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
   hipStream_t stream = nullptr;
-  hipEvent_t edge = nullptr;  // caller's queued work -> replay
-  hipEvent_t done = nullptr;  // replay -> caller's later work
   uint64_t updates = 0;  // re-captures applied through hipGraphExecUpdate
 
   hipError_t ensure_stream() {
     hipError_t e = hipSuccess;
     if (!stream) e = hipStreamCreateWithFlags(&stream, hipStreamNonBlocking);
-    if (e == hipSuccess && !edge) e = hipEventCreateWithFlags(&edge, hipEventDisableTiming);
-    if (e == hipSuccess && !done) e = hipEventCreateWithFlags(&done, hipEventDisableTiming);
     return e;
   }
 
@@ -76,11 +71,7 @@ struct GraphState {
 
   void release() {
     reset_full();
-    if (edge) (void)hipEventDestroy(edge);
-    if (done) (void)hipEventDestroy(done);
     if (stream) (void)hipStreamDestroy(stream);
-    edge = nullptr;
-    done = nullptr;
     stream = nullptr;
   }
 };
@@ -165,25 +156,9 @@ int32_t launch_on(GraphState& g, void* caller_stream) {
     aicf::hip::set_last_error("graph_launch", "graph_launch called but no captured graph exists");
     return AICF_STATUS_INVALID_ARGUMENT;
   }
-  hipError_t e = g.ensure_stream();
-  if (e != hipSuccess) return fail(e, "hipStreamCreateWithFlags");
-  // NULL is the null stream (torch's default stream), not "no caller"
-  hipStream_t caller = reinterpret_cast<hipStream_t>(caller_stream);
-  const bool edges = caller != g.stream;
-  if (edges) {
-    e = hipEventRecord(g.edge, caller);
-    if (e != hipSuccess) return fail(e, "hipEventRecord");
-    e = hipStreamWaitEvent(g.stream, g.edge, 0);
-    if (e != hipSuccess) return fail(e, "hipStreamWaitEvent");
-  }
-  e = hipGraphLaunch(g.exec, g.stream);
+  // NULL is the null stream (torch's default stream)
+  const hipError_t e = hipGraphLaunch(g.exec, reinterpret_cast<hipStream_t>(caller_stream));
   if (e != hipSuccess) return fail(e, "hipGraphLaunch");
-  if (edges) {
-    e = hipEventRecord(g.done, g.stream);
-    if (e != hipSuccess) return fail(e, "hipEventRecord");
-    e = hipStreamWaitEvent(caller, g.done, 0);
-    if (e != hipSuccess) return fail(e, "hipStreamWaitEvent");
-  }
   return AICF_STATUS_OK;
 }
 

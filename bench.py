@@ -124,7 +124,6 @@ def bench_c1(steps=200, warmup=5):
     """Replayed-graph time of one C1 train step."""
     import torch
 
-    from aicf_cuda import _C
     from aicf_hip import mlp
 
     ir, lowered, plan = mlp.build_mlp_xent()
@@ -134,7 +133,7 @@ def bench_c1(steps=200, warmup=5):
     ex = mlp.make_executor(ir, lowered, plan)
     ex.build_env(inputs=inputs, params=params, reuse_static=False)
     ex.capture(inputs=inputs, params=params, reuse_static=True)
-    gs = torch.cuda.ExternalStream(int(_C.graph_stream()))
+    gs = torch.cuda.current_stream()  # graph_launch replays on the caller's stream
     ex.replay(warmup)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -336,7 +335,7 @@ def bench_mlp(B, D, L, steps, warmup, dead_dx=True, fuse_optimizer=False, fuse_c
     ex.build_env(inputs=inputs, params=params, reuse_static=False)
     mlp.refresh_shadow(ex)
     ex.capture(inputs=inputs, params=params, reuse_static=True)
-    gs = torch.cuda.ExternalStream(int(ex_stream()))
+    gs = torch.cuda.current_stream()  # graph_launch replays on the caller's stream
     losses = []
     for _ in range(warmup):
         ex.replay(1)
@@ -461,12 +460,6 @@ def bench_mfma_ceiling(waves_per_simd=4, iters=20000, launches=8, warm=4):
             times.append(e0.elapsed_time(e1))
     ms = sum(times) / len(times)
     return {"tflops": flops / (ms * 1e-3) / 1e12, "ms": ms}
-
-
-def ex_stream():
-    from aicf_cuda import _C
-
-    return _C.graph_stream()
 
 
 # ------------------------------------------------------------------ CPU baseline

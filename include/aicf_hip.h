@@ -219,18 +219,16 @@ int32_t aicf_graph_begin(uint64_t* out_stream);
 /* Ends the capture and instantiates the executable graph.  INVALID_ARGUMENT
  * when no capture is in progress. */
 int32_t aicf_graph_end(void);
-/* Launches the instantiated graph on the dedicated stream, ordered after the
- * work already queued on `caller_stream` (input copies, host-side updates of
- * device scalars) and before the work queued there afterwards (reads of the
- * replay's results): an event recorded on the caller's stream is waited on
- * by the graph stream, and one recorded after the replay by the caller's
- * stream.  NULL is the null stream (torch's default stream), which the
- * non-blocking graph stream does not otherwise synchronise with.
- * INVALID_ARGUMENT when no graph was captured. */
+/* Launches the instantiated graph on `caller_stream` (NULL: the null stream,
+ * torch's default), so the replay is ordered after the work already queued
+ * there (input copies, host-side updates of device scalars) and before the
+ * work queued there afterwards (reads of its results).  The reference
+ * replays on its dedicated stream instead, unordered against the caller's
+ * work.  INVALID_ARGUMENT when no graph was captured. */
 int32_t aicf_graph_launch(void* caller_stream);
 /* Ends a dangling capture and destroys the graph objects. */
 int32_t aicf_graph_reset(void);
-/* The dedicated stream (0 before the first aicf_graph_begin). */
+/* The dedicated capture stream (0 before the first aicf_graph_begin). */
 uint64_t aicf_graph_stream(void);
 /* 1 while capturing, 2 when a graph is instantiated, 0 otherwise. */
 int32_t aicf_graph_state(void);
@@ -258,7 +256,7 @@ int32_t aicf_graph_begin_h(uint64_t handle, uint64_t* out_stream);
  * updated in place (hipGraphExecUpdate) if the new capture has the same
  * topology; otherwise a new executable is instantiated. */
 int32_t aicf_graph_end_h(uint64_t handle);
-/* As aicf_graph_launch, on the handle's graph and stream. */
+/* As aicf_graph_launch, for the handle's graph. */
 int32_t aicf_graph_launch_h(uint64_t handle, void* caller_stream);
 /* As aicf_graph_reset, for one handle (the handle stays valid). */
 int32_t aicf_graph_reset_h(uint64_t handle);
