@@ -28,7 +28,7 @@ ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 HIPCC = str(ROCM / "bin" / "hipcc")
 
 HIP_SOURCES = ["kernels/optim.hip", "kernels/eltwise.hip", "kernels/reduce.hip", "kernels/gemm.hip",
-               "kernels/norm.hip", "kernels/diag.hip"]
+               "kernels/norm.hip", "kernels/diag.hip", "kernels/smallstep.hip"]
 CXX_SOURCES = ["registry/registry.cpp", "registry/register_all.cpp", "runtime/graph.cpp"]
 
 HIP_FLAGS = [

@@ -56,6 +56,9 @@ enum class OpKind : int {
   EltwiseGelu = AICF_OP_ELTWISE_GELU,
   Transpose = AICF_OP_TRANSPOSE,
   GemmAdamW = AICF_OP_GEMM_ADAMW,
+  XentHead = AICF_OP_XENT_HEAD,
+  GradGroup = AICF_OP_GRAD_GROUP,
+  AdamWMulti = AICF_OP_ADAMW_MULTI,
 };
 
 std::string tensor_brief(const torch::Tensor& t) {
@@ -229,6 +232,9 @@ PYBIND11_MODULE(_C, m) {
       .value("EltwiseGelu", OpKind::EltwiseGelu)
       .value("Transpose", OpKind::Transpose)
       .value("GemmAdamW", OpKind::GemmAdamW)
+      .value("XentHead", OpKind::XentHead)
+      .value("GradGroup", OpKind::GradGroup)
+      .value("AdamWMulti", OpKind::AdamWMulti)
       .export_values();
 
   m.def(

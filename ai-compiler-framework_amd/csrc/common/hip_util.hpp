@@ -128,4 +128,21 @@ __device__ __forceinline__ float gelu_tanh_grad_f(float x) {
   return fmaf(s * (1.0f - s), x * fmaf(c3, x * x, c2), s);
 }
 
+// ---- mean of a vector in a fixed order (one 256-lane workgroup) -----------
+// Lane t accumulates v[t], v[t + 256], ... in fp64; the lanes of each wave
+// combine by butterfly, the four waves as ((w0 + w1) + (w2 + w3)); the
+// result is rounded to fp32 once.  `red` is 4 doubles of LDS.  The loss
+// means of softmax cross-entropy use it wherever they are taken, so a fused
+// and an unfused step produce the same bits.
+__device__ __forceinline__ void block_mean_f64(const float* __restrict__ v, int64_t n,
+                                               float* __restrict__ out, double* red) {
+  double acc = 0.0;
+  for (int64_t i = threadIdx.x; i < n; i += 256) acc += (double)v[i];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) out[0] = (float)(((red[0] + red[1]) + (red[2] + red[3])) / (double)n);
+}
+
 }  // namespace aicf::hip

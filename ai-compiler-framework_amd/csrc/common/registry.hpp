@@ -64,6 +64,9 @@ enum class OpKind : int {
   EltwiseGelu = AICF_OP_ELTWISE_GELU,
   Transpose = AICF_OP_TRANSPOSE,
   GemmAdamW = AICF_OP_GEMM_ADAMW,
+  XentHead = AICF_OP_XENT_HEAD,
+  GradGroup = AICF_OP_GRAD_GROUP,
+  AdamWMulti = AICF_OP_ADAMW_MULTI,
   _Count = AICF_OP_COUNT,
 };
 

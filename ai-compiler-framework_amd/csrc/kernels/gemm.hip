@@ -33,6 +33,7 @@
 
 #include "../common/adamw.hpp"
 #include "../common/hip_util.hpp"
+#include "../common/smallstep.hpp"
 
 namespace aicf::hip {
 
@@ -1417,6 +1418,30 @@ Status run_gemm(GemmParams& p, hipStream_t s) {
       if (nt_eligible<IN, OUT>(p, 256, 256, true)) return run_nt256<IN, OUT>(p, s);
     }
     return Status::NotImplemented;
+  }
+  if constexpr (IN == IN_F32 && OUT == OUT_F32) {
+    // fewer than 128 tiles of 64 x 64: one 16 x 16 tile per wave with K split
+    // over the waves of a workgroup reaches more CUs than any tiled
+    // configuration, and reads every operand layout in place
+    const int64_t tiles64 = ((p.M + 63) / 64) * ((p.N + 63) / 64);
+    if (tiles64 < 128 && (p.act == ACT_NONE || p.act == ACT_RELU) && p.c_cs == 1 && !p.aux) {
+      SmallGemm g{};
+      g.A = (const float*)p.A;
+      g.B = (const float*)p.B;
+      g.C = (float*)p.C;
+      g.bias = (const float*)p.bias;
+      g.a_m = p.a_rs;
+      g.a_k = p.a_cs;
+      g.b_k = p.b_rs;
+      g.b_n = p.b_cs;
+      g.c_m = p.c_rs;
+      g.bias_s = p.bias_s;
+      g.M = p.M;
+      g.N = p.N;
+      g.K = p.K;
+      g.relu = p.act == ACT_RELU;
+      if (small_gemm_ok(g)) return small_gemm_f32(g, s);
+    }
   }
   {
     constexpr bool MN = IN != IN_F32;

@@ -577,13 +577,7 @@ __global__ __launch_bounds__(256) void row_loop_kernel(RowArgs a) {
 __global__ __launch_bounds__(256) void mean_kernel(const float* __restrict__ v, int64_t n,
                                                    float* __restrict__ out) {
   __shared__ double red[4];
-  double acc = 0.0;
-  for (int64_t i = threadIdx.x; i < n; i += 256) acc += (double)v[i];
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
-  __syncthreads();
-  if (threadIdx.x == 0) out[0] = (float)(((red[0] + red[1]) + (red[2] + red[3])) / (double)n);
+  block_mean_f64(v, n, out, red);
 }
 
 // Picks a register-resident configuration when C is one of the row widths

@@ -1,0 +1,739 @@
+// Kernels for train steps whose tensors are too small for one launch per op
+// to fill the GPU (the reference's own MLP: batch 64, 784 -> 256 -> 10).
+// There every launch is a few microseconds of dispatch around well under a
+// microsecond of work, so the step is built from few launches that each do
+// several ops' work:
+//
+//  * small fp32 GEMM (also taken by the GEMM dispatcher for problems with
+//    few tiles): one 16 x 16 output tile per wave, read straight from global
+//    memory in whatever layout the operands have, v_mfma_f32_16x16x4f32, the
+//    waves of a workgroup splitting K and summing through LDS in a fixed
+//    order;
+//  * xent_head: the classifier head of a ReLU MLP, forward and backward, one
+//    wave per row: logits = H W^T + b, softmax cross-entropy (dlogits,
+//    argmax, row loss), dH = dlogits W, dX = dH where the saved ReLU output
+//    is positive;
+//  * grad_group: independent small jobs in one launch: gradient GEMMs,
+//    column sums (bias gradients), the fixed-order loss mean, the step
+//    counter;
+//  * adamw_multi: AdamW over several parameter tensors in one launch, with
+//    the element update and bias corrections of adamw_step (same bits).
+//
+// Reference contracts restated: the gradient GEMMs and column sums of
+// LinearBwd (python/aicf_fw/core_v2/lower.py:94-110), relu_bwd
+// (src/backends/cuda/ops/relu_bwd/launcher.cu:37-77), reduce_sum over axis 0
+// (reduce_sum/launcher.cu:140-155), step_inc (step_inc/launcher.cu:34-38).
+// The fused ops themselves have no reference counterpart; they play the
+// role of the reference's epilogue fusion (rewrites/stageC_fuse_epilogue.py)
+// for a step whose cost is launches rather than bytes or flops.
+#include "../common/adamw.hpp"
+#include "../common/hip_util.hpp"
+#include "../common/host_util.hpp"
+#include "../common/smallstep.hpp"
+
+namespace aicf::hip {
+
+namespace {
+
+size_t no_workspace(const TensorDesc*, int, const void*) { return 0; }
+
+KernelVariant make(const char* name, LaunchFn l, SupportedFn s, uint32_t schema = 0) {
+  KernelVariant v;
+  v.name = name;
+  v.launch = l;
+  v.supported = s;
+  v.query_workspace = no_workspace;
+  v.expected_attr_schema_id = schema;
+  return v;
+}
+
+// ===========================================================================
+// Small GEMM
+// ===========================================================================
+constexpr int kNB = 8;  // K blocks (16 K each) whose loads a wave issues before its MFMAs
+
+struct SgJob {
+  SmallGemm g;
+  int tn;          // tiles along N
+  int tiles;       // tiles along M times tn
+  int kb;          // 16-K blocks
+  int splits;      // waves per tile (K split): 1, 2 or 4
+  int tpb;         // tiles per workgroup: 4 / splits
+  int avec, bvec;  // 16-byte loads along K (K-contiguous, aligned operand)
+};
+
+__device__ __forceinline__ f32x4 sg_load(const float* row, int64_t sk, int64_t k, int64_t K, bool ok,
+                                         bool vec) {
+  f32x4 v = {0.f, 0.f, 0.f, 0.f};
+  if (!ok || k >= K) return v;
+  if (vec) return *reinterpret_cast<const f32x4*>(row + k);  // K % 4 == 0: all four in range
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+    if (k + c < K) v[c] = row[(k + c) * sk];
+  return v;
+}
+
+// One 16 x 16 tile over the K blocks split, split + splits, ...  Lane
+// l = 16 q + r reads row m0 + r of A and column n0 + r of B; for K block kb
+// it holds k = 16 kb + 4 q + c (c = 0..3) and feeds component c to the c-th
+// MFMA of the block, so k slot q of that MFMA carries the same k for A and
+// B.  Accumulator element i is C[m0 + 4 q + i][n0 + r].
+__device__ __forceinline__ f32x4 sg_tile(const SgJob& j, int64_t m0, int64_t n0, int split, int lane) {
+  const int r = lane & 15, q = lane >> 4;
+  const int64_t m = m0 + r, n = n0 + r;
+  const bool mok = m < j.g.M, nok = n < j.g.N;
+  const float* ar = j.g.A + (mok ? m : 0) * j.g.a_m;
+  const float* br = j.g.B + (nok ? n : 0) * j.g.b_n;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int kb0 = split; kb0 < j.kb; kb0 += j.splits * kNB) {
+    f32x4 a[kNB], b[kNB];
+#pragma unroll
+    for (int u = 0; u < kNB; ++u) {
+      const int kb = kb0 + u * j.splits;
+      const int64_t k = (int64_t)kb * 16 + 4 * q;
+      a[u] = sg_load(ar, j.g.a_k, k, j.g.K, mok && kb < j.kb, j.avec);
+      b[u] = sg_load(br, j.g.b_k, k, j.g.K, nok && kb < j.kb, j.bvec);
+    }
+#pragma unroll
+    for (int u = 0; u < kNB; ++u) {
+      if (kb0 + u * j.splits >= j.kb) break;  // uniform across the wave
+#pragma unroll
+      for (int c = 0; c < 4; ++c) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u][c], b[u][c], acc, 0, 0, 0);
+    }
+  }
+  return acc;
+}
+
+__device__ __forceinline__ void sg_store(const SmallGemm& g, int64_t m0, int64_t n0, int lane, f32x4 acc) {
+  const int r = lane & 15, q = lane >> 4;
+  const int64_t n = n0 + r;
+  if (n >= g.N) return;
+  const float bv = g.bias ? g.bias[n * g.bias_s] : 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t m = m0 + 4 * q + i;
+    if (m >= g.M) break;
+    float v = g.bias ? acc[i] + bv : acc[i];
+    if (g.relu) v = v > 0.0f ? v : 0.0f;
+    g.C[m * g.c_m + n] = v;
+  }
+}
+
+// Workgroup `blk` of a small GEMM: 4 waves = tpb tiles x splits K parts.
+// The parts of a tile are summed in split order (part 0 + 1 + 2 + 3).
+// `red` is 256 f32x4 of LDS.  Every thread reaches the barrier.
+__device__ __forceinline__ void sg_block(const SgJob& j, int blk, f32x4* red) {
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int tile = blk * j.tpb + w / j.splits;
+  const int split = w % j.splits;
+  const bool live = tile < j.tiles;
+  const int64_t m0 = live ? (int64_t)(tile / j.tn) * 16 : 0;
+  const int64_t n0 = live ? (int64_t)(tile % j.tn) * 16 : 0;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  if (live) acc = sg_tile(j, m0, n0, split, lane);
+  if (j.splits > 1) {
+    red[w * 64 + lane] = acc;
+    __syncthreads();
+    if (!live || split != 0) return;
+    for (int s = 1; s < j.splits; ++s) acc += red[(w + s) * 64 + lane];
+  } else if (!live) {
+    return;
+  }
+  sg_store(j.g, m0, n0, lane, acc);
+}
+
+__global__ __launch_bounds__(256) void gemm_small_kernel(SgJob j) {
+  __shared__ f32x4 red[256];
+  sg_block(j, blockIdx.x, red);
+}
+
+SgJob sg_plan(const SmallGemm& g) {
+  SgJob j{};
+  j.g = g;
+  j.tn = (int)((g.N + 15) / 16);
+  j.tiles = (int)((g.M + 15) / 16) * j.tn;
+  j.kb = (int)((g.K + 15) / 16);
+  j.splits = j.kb >= 16 ? 4 : j.kb >= 8 ? 2 : 1;
+  j.tpb = 4 / j.splits;
+  j.avec = g.a_k == 1 && g.K % 4 == 0 && (g.M == 1 || g.a_m % 4 == 0) && aligned(g.A, 16);
+  j.bvec = g.b_k == 1 && g.K % 4 == 0 && (g.N == 1 || g.b_n % 4 == 0) && aligned(g.B, 16);
+  return j;
+}
+int sg_blocks(const SgJob& j) { return (j.tiles + j.tpb - 1) / j.tpb; }
+
+// ===========================================================================
+// xent_head: classifier head forward + backward, one wave per row
+// ===========================================================================
+struct XentHeadArgs {
+  const float* H;          // [B, K] head input (the ReLU output)
+  const float* W;          // [C, K]
+  const float* bias;       // [C]
+  const int32_t* labels;   // [B]
+  const float* S;          // [B, K] saved ReLU output (mask of the ReLU backward)
+  float* logits;           // [B, C]
+  float* dlogits;          // [B, C] (softmax - onehot) / B
+  int32_t* argmax;         // [B]
+  float* row_loss;         // [B]
+  float* dH;               // [B, K] dlogits . W
+  float* dX;               // [B, K] dH where S > 0, else 0
+  int64_t B;
+  int K, C;
+  float inv_batch;
+};
+
+// Q: 16-byte vectors per lane along K (K <= 256 Q); CM: classes (C <= CM).
+template <int Q, int CM>
+__global__ __launch_bounds__(256) void xent_head_kernel(XentHeadArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= a.B) return;  // a whole wave; the kernel has no barrier
+  const int K4 = a.K >> 2;
+  const f32x4* hr = reinterpret_cast<const f32x4*>(a.H + row * a.K);
+  f32x4 h[Q];
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+    const int idx = q * 64 + lane;
+    h[q] = idx < K4 ? hr[idx] : f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  const int lab = a.labels[row];
+
+  // logits: each lane's partial dot products, then a butterfly (every lane
+  // ends with the same bits)
+  float z[CM];
+#pragma unroll
+  for (int c = 0; c < CM; ++c) {
+    z[c] = 0.0f;
+    if (c < a.C) {
+      const f32x4* wr = reinterpret_cast<const f32x4*>(a.W + (int64_t)c * a.K);
+      float p = 0.0f;
+#pragma unroll
+      for (int q = 0; q < Q; ++q) {
+        const int idx = q * 64 + lane;
+        if (idx < K4) {
+          const f32x4 w = wr[idx];
+          p = fmaf(h[q][0], w[0], p);
+          p = fmaf(h[q][1], w[1], p);
+          p = fmaf(h[q][2], w[2], p);
+          p = fmaf(h[q][3], w[3], p);
+        }
+      }
+      z[c] = wave_sum(p) + a.bias[c];
+    }
+  }
+
+  // softmax cross-entropy of the row (first index of the maximum)
+  float M = z[0];
+  int am = 0;
+#pragma unroll
+  for (int c = 1; c < CM; ++c)
+    if (c < a.C && z[c] > M) {
+      M = z[c];
+      am = c;
+    }
+  float e[CM];
+  float S = 0.0f;
+#pragma unroll
+  for (int c = 0; c < CM; ++c) {
+    e[c] = c < a.C ? __expf(z[c] - M) : 0.0f;
+    S += e[c];
+  }
+  const float invS = 1.0f / S;
+  float zl = 0.0f, zv = 0.0f, dv = 0.0f;
+  float d[CM];
+#pragma unroll
+  for (int c = 0; c < CM; ++c) {
+    d[c] = (e[c] * invS - (c == lab ? 1.0f : 0.0f)) * a.inv_batch;
+    if (c == lab) zl = z[c];
+    if (c == lane) {
+      zv = z[c];
+      dv = d[c];
+    }
+  }
+  if (lane < a.C) {
+    a.logits[row * a.C + lane] = zv;
+    a.dlogits[row * a.C + lane] = dv;
+  }
+  if (lane == 0) {
+    a.argmax[row] = am;
+    const bool valid = lab >= 0 && lab < a.C;
+    a.row_loss[row] = valid ? (logf(S) + M - zl) : __builtin_nanf("");
+  }
+
+  // dH = dlogits . W and the ReLU backward against the saved output
+  const f32x4* sr = reinterpret_cast<const f32x4*>(a.S + row * a.K);
+  f32x4* dhr = reinterpret_cast<f32x4*>(a.dH + row * a.K);
+  f32x4* dxr = reinterpret_cast<f32x4*>(a.dX + row * a.K);
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+    const int idx = q * 64 + lane;
+    if (idx >= K4) break;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < CM; ++c) {
+      if (c < a.C) {
+        const f32x4 w = reinterpret_cast<const f32x4*>(a.W + (int64_t)c * a.K)[idx];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = fmaf(d[c], w[i], acc[i]);
+      }
+    }
+    const f32x4 s = sr[idx];
+    f32x4 dx;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dx[i] = s[i] > 0.0f ? acc[i] : 0.0f;
+    dhr[idx] = acc;
+    dxr[idx] = dx;
+  }
+}
+
+bool f32_rows(const TensorDesc& t, int64_t R, int64_t C) {
+  return dt(t) == DType::kF32 && t.rank == 2 && t.shape[0] == R && t.shape[1] == C &&
+         is_contig_2d_rowmajor(t) && aligned(t.data, 16);
+}
+bool f32_vec(const TensorDesc& t, int64_t n) {
+  return dt(t) == DType::kF32 && t.contiguous && t.rank >= 1 && numel_of(t) == n;
+}
+bool i32_vec(const TensorDesc& t, int64_t n) {
+  return dt(t) == DType::kI32 && t.contiguous && t.rank >= 1 && numel_of(t) == n;
+}
+
+// inputs (H [B,K], W [C,K], bias [C], labels [B] i32, S [B,K]);
+// outputs (logits [B,C], dlogits [B,C], argmax [B] i32, row_loss [B], dH [B,K], dX [B,K]).
+bool xent_head_sup(const TensorDesc* in, int ni, const TensorDesc* out, int no, const void*) {
+  if (!in || !out || ni != 5 || no != 6) return false;
+  if (in[0].rank != 2 || in[1].rank != 2) return false;
+  const int64_t B = in[0].shape[0], K = in[0].shape[1], C = in[1].shape[0];
+  if (B < 1 || K < 4 || K % 4 || K > 2048 || C < 1 || C > 32) return false;
+  if (!f32_rows(in[0], B, K) || !f32_rows(in[1], C, K) || !f32_vec(in[2], C) || !i32_vec(in[3], B) ||
+      !f32_rows(in[4], B, K))
+    return false;
+  for (int o = 0; o < 2; ++o)  // logits, dlogits: scalar stores, any alignment
+    if (dt(out[o]) != DType::kF32 || out[o].rank != 2 || out[o].shape[0] != B || out[o].shape[1] != C ||
+        !is_contig_2d_rowmajor(out[o]))
+      return false;
+  if (!i32_vec(out[2], B) || !f32_vec(out[3], B) || !f32_rows(out[4], B, K) || !f32_rows(out[5], B, K))
+    return false;
+  // the written tensors may not alias what the kernel still reads
+  for (int o = 0; o < 6; ++o)
+    for (int i = 0; i < 5; ++i)
+      if (out[o].data == in[i].data) return false;
+  return B <= INT32_MAX;
+}
+
+template <int Q>
+void xent_head_go(const XentHeadArgs& a, unsigned grid, hipStream_t s) {
+  if (a.C <= 16)
+    xent_head_kernel<Q, 16><<<grid, 256, 0, s>>>(a);
+  else
+    xent_head_kernel<Q, 32><<<grid, 256, 0, s>>>(a);
+}
+
+Status xent_head_launch(const TensorDesc* in, int ni, TensorDesc* out, int no, const void* at, void*,
+                        size_t, void* stream) {
+  if (!xent_head_sup(in, ni, out, no, at)) return Status::InvalidArgument;
+  XentHeadArgs a{};
+  a.H = (const float*)in[0].data;
+  a.W = (const float*)in[1].data;
+  a.bias = (const float*)in[2].data;
+  a.labels = (const int32_t*)in[3].data;
+  a.S = (const float*)in[4].data;
+  a.logits = (float*)out[0].data;
+  a.dlogits = (float*)out[1].data;
+  a.argmax = (int32_t*)out[2].data;
+  a.row_loss = (float*)out[3].data;
+  a.dH = (float*)out[4].data;
+  a.dX = (float*)out[5].data;
+  a.B = in[0].shape[0];
+  a.K = (int)in[0].shape[1];
+  a.C = (int)in[1].shape[0];
+  a.inv_batch = 1.0f / (float)a.B;
+  const unsigned grid = (unsigned)((a.B + 3) / 4);
+  const int q = (a.K / 4 + 63) / 64;
+  hipStream_t s = as_stream(stream);
+  if (q <= 1)
+    xent_head_go<1>(a, grid, s);
+  else if (q <= 2)
+    xent_head_go<2>(a, grid, s);
+  else if (q <= 4)
+    xent_head_go<4>(a, grid, s);
+  else
+    xent_head_go<8>(a, grid, s);
+  return launch_status("xent_head");
+}
+
+// ===========================================================================
+// grad_group: independent small jobs in one launch
+// ===========================================================================
+enum GroupJobType { GJ_GEMM = 0, GJ_COLSUM = 1, GJ_MEAN = 2, GJ_STEP = 3 };
+constexpr int kMaxJobs = 8;
+
+struct GroupJob {
+  int type;
+  SgJob gemm;
+  const float* x;  // colsum: out[n] = sum_r x[r * ld + n]; mean: mean of x[0 .. rows)
+  float* out;
+  int64_t rows, cols, ld;
+  const int32_t* step_in;
+  int32_t* step_out;
+  int inc;  // step: out = in + inc (0 for the warmup copy)
+};
+struct GroupArgs {
+  int n;
+  int start[kMaxJobs + 1];  // first workgroup of each job
+  GroupJob job[kMaxJobs];
+};
+
+// Column sum over 64 columns: wave w adds rows w, w + 4, ... in order, the
+// four waves combine as (w0 + w1) + (w2 + w3).
+__device__ __forceinline__ void colsum_block(const GroupJob& j, int b, float* red) {
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t n = (int64_t)b * 64 + lane;
+  float s = 0.0f;
+  if (n < j.cols) {
+    const float* p = j.x + n;
+#pragma unroll 8
+    for (int64_t r = w; r < j.rows; r += 4) s += p[r * j.ld];
+  }
+  red[w * 64 + lane] = s;
+  __syncthreads();
+  if (w == 0 && n < j.cols) j.out[n] = (red[lane] + red[64 + lane]) + (red[128 + lane] + red[192 + lane]);
+}
+
+__global__ __launch_bounds__(256) void grad_group_kernel(GroupArgs a) {
+  __shared__ f32x4 red[256];
+  const int blk = blockIdx.x;
+  int j = 0;
+  while (j + 1 < a.n && blk >= a.start[j + 1]) ++j;
+  const GroupJob& job = a.job[j];
+  const int b = blk - a.start[j];
+  switch (job.type) {
+    case GJ_GEMM:
+      sg_block(job.gemm, b, red);
+      break;
+    case GJ_COLSUM:
+      colsum_block(job, b, reinterpret_cast<float*>(red));
+      break;
+    case GJ_MEAN:
+      block_mean_f64(job.x, job.rows, job.out, reinterpret_cast<double*>(red));
+      break;
+    default:  // GJ_STEP
+      if (threadIdx.x == 0) job.step_out[0] = job.step_in[0] + job.inc;
+      break;
+  }
+}
+
+// Schema GGRP: <i n> then n records <iiiiii> (type, in0, in1, out0, f0, f1):
+//   GEMM    C[out0] = op(in0) . op(in1), f0 = transA, f1 = transB
+//   COLSUM  out0[n] = sum over rows of in0 (2-D, unit column stride)
+//   MEAN    out0 (1 element) = mean of in0, fp64 accumulation, fixed order
+//   STEP    out0 = in0 + f0 (int32 scalars; f0 is 1, or 0 for the warmup copy)
+struct GroupRec {
+  int type, in0, in1, out0, f0, f1;
+};
+
+bool read_group(const void* attr, int ni, int no, GroupRec* recs, int* n) {
+  const AttrBlob& a = blob(attr);
+  if (a.schema_id != AICF_SCHEMA_GGRP || !payload_ok(a, 4)) return false;
+  const int cnt = field<int32_t>(a, 0);
+  if (cnt < 1 || cnt > kMaxJobs || !payload_ok(a, 4 + 24 * (uint32_t)cnt)) return false;
+  for (int k = 0; k < cnt; ++k) {
+    GroupRec r;
+    r.type = field<int32_t>(a, 4 + 24 * k);
+    r.in0 = field<int32_t>(a, 8 + 24 * k);
+    r.in1 = field<int32_t>(a, 12 + 24 * k);
+    r.out0 = field<int32_t>(a, 16 + 24 * k);
+    r.f0 = field<int32_t>(a, 20 + 24 * k);
+    r.f1 = field<int32_t>(a, 24 + 24 * k);
+    if (r.type < GJ_GEMM || r.type > GJ_STEP) return false;
+    if (r.in0 < 0 || r.in0 >= ni || r.out0 < 0 || r.out0 >= no) return false;
+    if (r.type == GJ_GEMM && (r.in1 < 0 || r.in1 >= ni)) return false;
+    recs[k] = r;
+  }
+  *n = cnt;
+  return true;
+}
+
+// Byte range a view can touch (positive strides).
+struct Span {
+  uintptr_t lo, hi;
+};
+Span span_of(const TensorDesc& t) {
+  const int es = dt(t) == DType::kF32 || dt(t) == DType::kI32 ? 4 : 2;
+  int64_t last = 0;
+  for (int i = 0; i < t.rank; ++i) last += (t.shape[i] - 1) * t.stride[i];
+  const uintptr_t lo = reinterpret_cast<uintptr_t>(t.data);
+  return {lo, lo + (uintptr_t)((last + 1) * es)};
+}
+bool overlap(const Span& a, const Span& b) { return a.lo < b.hi && b.lo < a.hi; }
+
+bool group_fill(const TensorDesc* in, int ni, const TensorDesc* out, int no, const void* attr,
+                GroupArgs* ga) {
+  if (!in || !out || ni < 1 || no < 1) return false;
+  GroupRec recs[kMaxJobs];
+  int n = 0;
+  if (!read_group(attr, ni, no, recs, &n)) return false;
+  GroupArgs a{};
+  a.n = n;
+  int blocks = 0;
+  for (int k = 0; k < n; ++k) {
+    const GroupRec& r = recs[k];
+    GroupJob& j = a.job[k];
+    j.type = r.type;
+    const TensorDesc &X = in[r.in0], &O = out[r.out0];
+    int nb = 1;
+    if (r.type == GJ_GEMM) {
+      const TensorDesc& Y = in[r.in1];
+      if (dt(X) != DType::kF32 || dt(Y) != DType::kF32 || dt(O) != DType::kF32) return false;
+      if (X.rank != 2 || Y.rank != 2 || O.rank != 2 || O.stride[1] != 1 || O.stride[0] < O.shape[1])
+        return false;
+      for (const TensorDesc* t : {&X, &Y})
+        if (t->stride[0] < 0 || t->stride[1] < 0) return false;
+      const bool ta = r.f0 != 0, tb = r.f1 != 0;
+      SmallGemm g{};
+      g.A = (const float*)X.data;
+      g.B = (const float*)Y.data;
+      g.C = (float*)O.data;
+      g.M = ta ? X.shape[1] : X.shape[0];
+      g.K = ta ? X.shape[0] : X.shape[1];
+      g.a_m = ta ? X.stride[1] : X.stride[0];
+      g.a_k = ta ? X.stride[0] : X.stride[1];
+      const int64_t KB = tb ? Y.shape[1] : Y.shape[0];
+      g.N = tb ? Y.shape[0] : Y.shape[1];
+      g.b_k = tb ? Y.stride[1] : Y.stride[0];
+      g.b_n = tb ? Y.stride[0] : Y.stride[1];
+      g.c_m = O.stride[0];
+      if (KB != g.K || O.shape[0] != g.M || O.shape[1] != g.N) return false;
+      if (!small_gemm_ok(g)) return false;
+      j.gemm = sg_plan(g);
+      nb = sg_blocks(j.gemm);
+    } else if (r.type == GJ_COLSUM) {
+      if (dt(X) != DType::kF32 || X.rank != 2 || X.stride[1] != 1 || X.stride[0] < X.shape[1]) return false;
+      if (X.shape[0] < 1 || X.shape[1] < 1 || !f32_vec(O, X.shape[1])) return false;
+      j.x = (const float*)X.data;
+      j.out = (float*)O.data;
+      j.rows = X.shape[0];
+      j.cols = X.shape[1];
+      j.ld = X.stride[0];
+      nb = (int)((j.cols + 63) / 64);
+    } else if (r.type == GJ_MEAN) {
+      int64_t cnt = 0;
+      if (dt(X) != DType::kF32 || !X.contiguous || !numel_pos(X, &cnt)) return false;
+      if (dt(O) != DType::kF32 || numel_of(O) != 1) return false;
+      j.x = (const float*)X.data;
+      j.out = (float*)O.data;
+      j.rows = numel_of(X);
+    } else {  // GJ_STEP
+      if (dt(X) != DType::kI32 || numel_of(X) != 1 || dt(O) != DType::kI32 || numel_of(O) != 1) return false;
+      if (r.f0 != 0 && r.f0 != 1) return false;
+      j.step_in = (const int32_t*)X.data;
+      j.step_out = (int32_t*)O.data;
+      j.inc = r.f0;
+    }
+    a.start[k] = blocks;
+    if ((int64_t)blocks + nb > INT32_MAX) return false;
+    blocks += nb;
+  }
+  a.start[n] = blocks;
+  // the jobs run concurrently: what a job writes may not be read or written
+  // by another job
+  for (int k = 0; k < n; ++k) {
+    const Span w = span_of(out[recs[k].out0]);
+    for (int l = 0; l < n; ++l) {
+      if (l == k) continue;
+      if (overlap(w, span_of(out[recs[l].out0])) || overlap(w, span_of(in[recs[l].in0])))
+        return false;
+      if (recs[l].type == GJ_GEMM && overlap(w, span_of(in[recs[l].in1]))) return false;
+    }
+    // and a job does not read its own output (the step counter is the exception:
+    // one lane reads it, then writes it)
+    if (recs[k].type != GJ_STEP) {
+      if (overlap(w, span_of(in[recs[k].in0]))) return false;
+      if (recs[k].type == GJ_GEMM && overlap(w, span_of(in[recs[k].in1]))) return false;
+    }
+  }
+  if (ga) *ga = a;
+  return true;
+}
+
+bool grad_group_sup(const TensorDesc* in, int ni, const TensorDesc* out, int no, const void* attr) {
+  return group_fill(in, ni, out, no, attr, nullptr);
+}
+
+Status grad_group_launch(const TensorDesc* in, int ni, TensorDesc* out, int no, const void* attr, void*,
+                         size_t, void* stream) {
+  GroupArgs a;
+  if (!group_fill(in, ni, out, no, attr, &a)) return Status::InvalidArgument;
+  grad_group_kernel<<<(unsigned)a.start[a.n], 256, 0, as_stream(stream)>>>(a);
+  return launch_status("grad_group");
+}
+
+// ===========================================================================
+// adamw_multi: AdamW over several tensors in one launch
+// ===========================================================================
+constexpr int kMaxTensors = 8;
+
+struct AdamWTensor {
+  const float* P;
+  const float* G;
+  const float* M;
+  const float* V;
+  float* Po;
+  float* Mo;
+  float* Vo;
+  int64_t n;
+};
+struct AdamWMultiArgs {
+  int nt;
+  int start[kMaxTensors + 1];
+  AdamWTensor t[kMaxTensors];
+  AdamWArgs a;
+  const int32_t* step;
+};
+
+// Per tensor, the element mapping of adamw_step (one 16-byte vector per
+// lane, 1024 elements per workgroup, the n % 4 tail by the lane of vector
+// n / 4) and its element update: the same bits.
+__global__ __launch_bounds__(256) void adamw_multi_kernel(AdamWMultiArgs args) {
+  __shared__ float sh[2];
+  if (threadIdx.x < 64) {
+    const AdamWScalars t = adamw_scalars(args.step, args.a);
+    if (threadIdx.x == 0) {
+      sh[0] = t.step;
+      sh[1] = t.ibc2;
+    }
+  }
+  __syncthreads();
+  const AdamWScalars s{sh[0], sh[1]};
+  const int blk = blockIdx.x;
+  int j = 0;
+  while (j + 1 < args.nt && blk >= args.start[j + 1]) ++j;
+  const AdamWTensor& T = args.t[j];
+  const int64_t n = T.n, n4 = n / 4;
+  const int64_t i = (int64_t)(blk - args.start[j]) * 256 + threadIdx.x;
+  if (i < n4) {
+    f32x4 p = reinterpret_cast<const f32x4*>(T.P)[i];
+    const f32x4 g = reinterpret_cast<const f32x4*>(T.G)[i];
+    f32x4 m = reinterpret_cast<const f32x4*>(T.M)[i];
+    f32x4 v = reinterpret_cast<const f32x4*>(T.V)[i];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      float pp = p[c], mm = m[c], vv = v[c];
+      adamw_elem(pp, g[c], mm, vv, s, args.a);
+      p[c] = pp;
+      m[c] = mm;
+      v[c] = vv;
+    }
+    reinterpret_cast<f32x4*>(T.Po)[i] = p;
+    reinterpret_cast<f32x4*>(T.Mo)[i] = m;
+    reinterpret_cast<f32x4*>(T.Vo)[i] = v;
+  } else if (i == n4) {
+    for (int64_t e = 4 * n4; e < n; ++e) {
+      float pp = T.P[e], mm = T.M[e], vv = T.V[e];
+      adamw_elem(pp, T.G[e], mm, vv, s, args.a);
+      T.Po[e] = pp;
+      T.Mo[e] = mm;
+      T.Vo[e] = vv;
+    }
+  }
+}
+
+// Schema ADAM <fffff>: lr, beta1, beta2, eps, weight_decay (adamw_step's).
+bool read_adamw(const void* attr, AdamWArgs* out) {
+  float lr = 1e-3f, b1 = 0.9f, b2 = 0.999f, eps = 1e-8f, wd = 0.0f;
+  const AttrBlob& a = blob(attr);
+  if (attr && a.schema_id != 0) {
+    if (a.schema_id != AICF_SCHEMA_ADAM || !payload_ok(a, 16)) return false;
+    lr = field<float>(a, 0);
+    b1 = field<float>(a, 4);
+    b2 = field<float>(a, 8);
+    eps = field<float>(a, 12);
+    if (payload_ok(a, 20)) wd = field<float>(a, 16);
+  }
+  *out = AdamWArgs{lr, b1, b2, eps, wd, 1.0f - b1, 1.0f - b2, 1.0f - lr * wd};
+  return true;
+}
+
+// inputs (P0, G0, M0, V0, ..., P_{T-1}, G, M, V, step i32); outputs (P0, M0, V0, ...).
+bool adamw_multi_fill(const TensorDesc* in, int ni, const TensorDesc* out, int no, const void* attr,
+                      AdamWMultiArgs* pa) {
+  if (!in || !out || ni < 5 || (ni - 1) % 4 || no != 3 * ((ni - 1) / 4)) return false;
+  const int T = (ni - 1) / 4;
+  if (T > kMaxTensors) return false;
+  AdamWMultiArgs a{};
+  if (!read_adamw(attr, &a.a)) return false;
+  const TensorDesc& st = in[ni - 1];
+  if (dt(st) != DType::kI32 || !st.contiguous || numel_of(st) != 1) return false;
+  a.step = (const int32_t*)st.data;
+  a.nt = T;
+  int blocks = 0;
+  for (int k = 0; k < T; ++k) {
+    const TensorDesc *P = &in[4 * k], *G = &in[4 * k + 1], *M = &in[4 * k + 2], *V = &in[4 * k + 3];
+    const TensorDesc *Po = &out[3 * k], *Mo = &out[3 * k + 1], *Vo = &out[3 * k + 2];
+    int64_t n = 0;
+    if (!numel_pos(*P, &n)) return false;
+    for (const TensorDesc* t : {P, G, M, V, Po, Mo, Vo})
+      if (dt(*t) != DType::kF32 || !t->contiguous || numel_of(*t) != n || !aligned(t->data, 16))
+        return false;
+    // in place per buffer, nothing else shared (adam_step/launcher.cu:98-128)
+    if (Po->data != P->data || Mo->data != M->data || Vo->data != V->data) return false;
+    if (G->data == P->data || G->data == M->data || G->data == V->data || P->data == M->data ||
+        P->data == V->data || M->data == V->data)
+      return false;
+    a.t[k] = AdamWTensor{(const float*)P->data, (const float*)G->data, (const float*)M->data,
+                         (const float*)V->data, (float*)Po->data, (float*)Mo->data, (float*)Vo->data, n};
+    a.start[k] = blocks;
+    const int64_t nb = (n / 4 + 1 + 255) / 256;  // vectors plus the tail lane
+    if ((int64_t)blocks + nb > INT32_MAX) return false;
+    blocks += (int)nb;
+  }
+  a.start[T] = blocks;
+  // distinct tensors do not overlap
+  for (int k = 0; k < T; ++k)
+    for (int l = k + 1; l < T; ++l)
+      for (int x = 0; x < 4; ++x)
+        for (int y = 0; y < 4; ++y)
+          if (overlap(span_of(in[4 * k + x]), span_of(in[4 * l + y]))) return false;
+  if (pa) *pa = a;
+  return true;
+}
+
+bool adamw_multi_sup(const TensorDesc* in, int ni, const TensorDesc* out, int no, const void* attr) {
+  return adamw_multi_fill(in, ni, out, no, attr, nullptr);
+}
+
+Status adamw_multi_launch(const TensorDesc* in, int ni, TensorDesc* out, int no, const void* attr, void*,
+                          size_t, void* stream) {
+  AdamWMultiArgs a;
+  if (!adamw_multi_fill(in, ni, out, no, attr, &a)) return Status::InvalidArgument;
+  adamw_multi_kernel<<<(unsigned)a.start[a.nt], 256, 0, as_stream(stream)>>>(a);
+  return launch_status("adamw_multi");
+}
+
+}  // namespace
+
+// ===========================================================================
+// Small GEMM entry for the GEMM dispatcher
+// ===========================================================================
+bool small_gemm_ok(const SmallGemm& g) {
+  if (!g.A || !g.B || !g.C || g.M < 1 || g.N < 1 || g.K < 1) return false;
+  if (g.M > INT32_MAX / 2 || g.N > INT32_MAX / 2 || g.K > INT32_MAX / 2) return false;
+  if (g.a_m < 0 || g.a_k < 0 || g.b_k < 0 || g.b_n < 0 || g.c_m < g.N) return false;
+  const int64_t tiles = ((g.M + 15) / 16) * ((g.N + 15) / 16);
+  return tiles <= INT32_MAX / 4;
+}
+
+Status small_gemm_f32(const SmallGemm& g, hipStream_t s) {
+  if (!small_gemm_ok(g)) return Status::InvalidArgument;
+  const SgJob j = sg_plan(g);
+  gemm_small_kernel<<<(unsigned)sg_blocks(j), 256, 0, s>>>(j);
+  return launch_status("gemm_small");
+}
+
+KernelVariant make_xent_head_f32_variant() { return make("xent_head_f32", xent_head_launch, xent_head_sup); }
+KernelVariant make_grad_group_f32_variant() {
+  return make("grad_group_f32", grad_group_launch, grad_group_sup, AICF_SCHEMA_GGRP);
+}
+KernelVariant make_adamw_multi_f32_variant() {
+  return make("adamw_multi_f32", adamw_multi_launch, adamw_multi_sup, AICF_SCHEMA_ADAM);
+}
+
+}  // namespace aicf::hip

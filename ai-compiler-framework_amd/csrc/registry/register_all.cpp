@@ -67,6 +67,10 @@ KernelVariant make_gemm_bias_relu_f16_tc_wmma_out_f16_variant();
 KernelVariant make_gemm_epilogue_bf16_variant();
 KernelVariant make_gemm_epilogue_bf16_f32out_variant();
 KernelVariant make_gemm_adamw_bf16_variant();
+// smallstep.hip
+KernelVariant make_xent_head_f32_variant();
+KernelVariant make_grad_group_f32_variant();
+KernelVariant make_adamw_multi_f32_variant();
 
 void register_all_kernels_into(KernelRegistry& R) {
   if (std::getenv("AICF_VERBOSE")) std::fprintf(stderr, "[aicf] register_all: gfx950 backend\n");
@@ -164,6 +168,9 @@ void register_all_kernels_into(KernelRegistry& R) {
   reg(OpKind::EltwiseGelu, make_gelu_f32_variant(), 0, "gelu_f32_v0");
   reg(OpKind::Transpose, make_transpose_variant(), 0, "transpose2d_v0");
   reg(OpKind::GemmAdamW, make_gemm_adamw_bf16_variant(), 0, "gemm_adamw_bf16_v0");
+  reg(OpKind::XentHead, make_xent_head_f32_variant(), 0, "xent_head_f32_v0");
+  reg(OpKind::GradGroup, make_grad_group_f32_variant(), 0, "grad_group_f32_v0");
+  reg(OpKind::AdamWMulti, make_adamw_multi_f32_variant(), 0, "adamw_multi_f32_v0");
 }
 
 }  // namespace aicf::hip

@@ -158,6 +158,9 @@ const char* opkind_name(OpKind k) {
     case OpKind::EltwiseGelu: return "gelu";
     case OpKind::Transpose: return "transpose";
     case OpKind::GemmAdamW: return "gemm_adamw";
+    case OpKind::XentHead: return "xent_head";
+    case OpKind::GradGroup: return "grad_group";
+    case OpKind::AdamWMulti: return "adamw_multi";
     case OpKind::_Count: break;
   }
   return "unknown";

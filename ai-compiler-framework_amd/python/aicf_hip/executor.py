@@ -60,7 +60,8 @@ OPNAME_TO_KIND: Dict[str, int] = {
     "row_softmax": int(_C.OpKind.RowSoftmax), "row_reduce": int(_C.OpKind.RowReduce),
     "softmax_xent": int(_C.OpKind.SoftmaxXent), "gelu_bwd": int(_C.OpKind.GeluBwd),
     "gelu": int(_C.OpKind.EltwiseGelu), "transpose": int(_C.OpKind.Transpose),
-    "gemm_adamw": int(_C.OpKind.GemmAdamW),
+    "gemm_adamw": int(_C.OpKind.GemmAdamW), "xent_head": int(_C.OpKind.XentHead),
+    "grad_group": int(_C.OpKind.GradGroup), "adamw_multi": int(_C.OpKind.AdamWMulti),
 }
 
 
@@ -75,6 +76,7 @@ SCHEMA_SGDS = _fourcc_le(b"SGDS")
 SCHEMA_MSEG = _fourcc_le(b"MSEG")
 SCHEMA_RRED = _fourcc_le(b"RRED")
 SCHEMA_GADW = _fourcc_le(b"GADW")
+SCHEMA_GGRP = _fourcc_le(b"GGRP")
 SCHEMA_GEMM = int.from_bytes(b"GEMM", "big")
 SCHEMA_RSUM = int.from_bytes(b"RSUM", "big")
 
@@ -100,6 +102,18 @@ def epilogue_kind(attrs: Dict[str, Any]) -> int:
     return 0 if bias else 2
 
 
+def warmup_attrs(op: str, attrs: Dict[str, Any]) -> Dict[str, Any]:
+    """Attributes of an op under AICF_WARMUP=1 (exec.py:423-431): every Adam
+    update runs with lr 0, and a grad_group's step_inc job adds 0 (the copy
+    the warmup makes of step_inc)."""
+    if op in ("adam_step", "adamw_step", "gemm_adamw", "adamw_multi"):
+        return dict(attrs, lr=0.0)
+    if op == "grad_group":
+        return dict(attrs, jobs=[[j[0], j[1], j[2], j[3], 0 if j[0] == 3 else j[4], j[5]]
+                                 for j in attrs.get("jobs", [])])
+    return attrs
+
+
 def pack_attrs(op: str, attrs: Dict[str, Any]) -> Tuple[int, bytes]:
     op = str(op).strip().lower()
     a = dict(attrs or {})
@@ -113,10 +127,13 @@ def pack_attrs(op: str, attrs: Dict[str, Any]) -> Tuple[int, bytes]:
                                         int(bool(a.get("transB", False))), float(a.get("lr", 1e-3)),
                                         float(a.get("beta1", 0.9)), float(a.get("beta2", 0.999)),
                                         float(a.get("eps", 1e-8)), float(a.get("weight_decay", 0.0)))
-    if op in ("adam_step", "adamw_step"):
+    if op == "grad_group":
+        jobs = [tuple(int(x) for x in j) for j in a.get("jobs", [])]
+        return SCHEMA_GGRP, struct.pack("<i", len(jobs)) + b"".join(struct.pack("<iiiiii", *j) for j in jobs)
+    if op in ("adam_step", "adamw_step", "adamw_multi"):
         vals = [float(a.get("lr", 1e-3)), float(a.get("beta1", 0.9)), float(a.get("beta2", 0.999)),
                 float(a.get("eps", 1e-8))]
-        if op == "adamw_step":
+        if op in ("adamw_step", "adamw_multi"):
             vals.append(float(a.get("weight_decay", 0.0)))
         return SCHEMA_ADAM, struct.pack("<" + "f" * len(vals), *vals)
     if op == "bias_corr":
@@ -253,8 +270,8 @@ class PlannedExecutor:
         if warmup and op == "step_inc":
             outs_t[0].copy_(ins_t[0])
             return
-        if warmup and op in ("adam_step", "adamw_step", "gemm_adamw"):
-            attrs = dict(attrs, lr=0.0)
+        if warmup:
+            attrs = warmup_attrs(op, attrs)
         schema, payload = pack_attrs(op, attrs)
         if kid is not None:
             _C.launch_by_id(str(kid), _C.OpKind(kind), ins_t, outs_t, schema, payload, int(stream))

@@ -86,12 +86,31 @@ _LINE = re.compile(r"^\s*#(\d+)\s+(\S+)\s+\(([^)]*)\)\s+->\s+\(([^)]*)\)(?:\s+\{
 def _attr_value(s: str) -> Any:
     if s in ("True", "False"):
         return s == "True"
+    if s.startswith("["):  # a list attribute (grad_group jobs): Python literal of ints
+        return json.loads(s)
     for cast in (int, float):
         try:
             return cast(s)
         except ValueError:
             pass
     return s
+
+
+def _split_top(s: str) -> List[str]:
+    """Splits `k=v, k=v` at the commas outside brackets."""
+    parts, depth, cur = [], 0, ""
+    for i, ch in enumerate(s):
+        depth += ch == "["
+        depth -= ch == "]"
+        if depth == 0 and s.startswith(", ", i):
+            parts.append(cur)
+            cur = ""
+            continue
+        if depth == 0 and ch == " " and cur == "":
+            continue
+        cur += ch
+    parts.append(cur)
+    return parts
 
 
 def lowered_from_text(text: str) -> Lowered:
@@ -111,7 +130,7 @@ def lowered_from_text(text: str) -> Lowered:
             "attrs": {},
         }
         if attrs:
-            for kv in attrs.split(", "):
+            for kv in _split_top(attrs):
                 k, v = kv.split("=", 1)
                 item["attrs"][k.strip()] = _attr_value(v.strip())
         if kid:

@@ -19,6 +19,15 @@ compile-time rewrites of the reference pipeline:
   weight-gradient GEMM whose output only feeds the flat AdamW step becomes
   gemm_adamw (AdamW applied in the GEMM's epilogue, no fp32 gradient in
   memory); the flat step keeps the remaining ranges.
+* StageF  fuse_small_step (not in the reference; opt-in): for steps whose
+  tensors are too small to fill the GPU, so that every launch costs its
+  dispatch time rather than its work: copy_saved of a value nothing writes
+  again is dropped (readers take the source); the classifier head
+  gemm -> bias_add -> softmax_xent with its backward gemm (dY.W) and the
+  relu_bwd behind it becomes one xent_head op (one wave per row); runs of
+  independent small jobs (fp32 GEMMs with few tiles, column sums, the loss
+  mean, step_inc) become one grad_group launch; consecutive adamw_step ops
+  sharing step and hyperparameters become one adamw_multi launch.
 * StageB  apply_kernel_selection (reference kernel_select.py:22-142 and the
   vec2/half2 upgrades of plan.py:371-444): pins a kernel_id on every op.
 
@@ -38,7 +47,7 @@ _PRIMITIVES = {
     "copy", "copy_saved", "copy_aux", "grad_zero", "adam_step", "step_inc", "bias_corr",
     "sgd_step", "gelu", "gelu_bwd", "softmax_xent", "row_softmax", "row_reduce", "mse_loss",
     "adamw_step", "layernorm_fwd", "layernorm_bwd", "batchnorm_fwd", "batchnorm_bwd",
-    "transpose", "gemm_adamw",
+    "transpose", "gemm_adamw", "xent_head", "grad_group", "adamw_multi",
 }
 
 _ALIASES = {"adamstep": "adam_step", "stepinc": "step_inc", "biascorr": "bias_corr",
@@ -342,6 +351,12 @@ def pick_kernel_id(ir: IRGraph, it: Dict[str, Any]) -> Optional[str]:
         return "row_reduce_f32_v0"
     if op == "transpose":
         return "transpose2d_v0"
+    if op == "xent_head":
+        return "xent_head_f32_v0"
+    if op == "grad_group":
+        return "grad_group_f32_v0"
+    if op == "adamw_multi":
+        return "adamw_multi_f32_v0"
     if op in ("layernorm_fwd", "layernorm_bwd"):
         return f"{op}_{'f16' if f16 else 'f32'}_v0"
     if op in ("batchnorm_fwd", "batchnorm_bwd"):
@@ -529,13 +544,258 @@ def fuse_colsum_into_dgelu(ir: IRGraph, lowered: Lowered) -> Lowered:
     return [it for j, it in enumerate(out) if j not in drop]
 
 
+# ---------------------------------------------------------------- StageF
+GJ_GEMM, GJ_COLSUM, GJ_MEAN, GJ_STEP = 0, 1, 2, 3
+MAX_GROUP_JOBS = 8
+MAX_ADAMW_TENSORS = 8
+
+
+def _kind(it: Dict[str, Any]) -> str:
+    return str(it.get("op", "")).strip().lower()
+
+
+def _f32(ir: IRGraph, vid: int) -> bool:
+    return "float32" in _dt(ir, vid)
+
+
+def _base(ir: IRGraph, vid: int) -> int:
+    return _base_and_offset(ir, int(vid))[0]
+
+
+def drop_dead_saves(ir: IRGraph, lowered: Lowered) -> Lowered:
+    """copy_saved(src) -> dst where nothing after the copy writes src (or its
+    base buffer): the readers of dst read src instead and the copy goes."""
+    out = [dict(it, inputs=list(it["inputs"]), outputs=list(it["outputs"])) for it in lowered]
+    drop = set()
+    for i, it in enumerate(out):
+        if _kind(it) != "copy_saved" or len(it["inputs"]) != 1 or len(it["outputs"]) != 1:
+            continue
+        src, dst = int(it["inputs"][0]), int(it["outputs"][0])
+        if ir.values[src].view_of or ir.values[dst].view_of:
+            continue
+        later = out[i + 1:]
+        if any(_base(ir, o) == src for x in later for o in x["outputs"]):
+            continue
+        if any(int(o) == dst for x in later for o in x["outputs"]):
+            continue
+        for x in later:
+            x["inputs"] = [src if int(v) == dst else int(v) for v in x["inputs"]]
+        drop.add(i)
+    return [it for i, it in enumerate(out) if i not in drop]
+
+
+def _head_shapes_ok(ir: IRGraph, H: int, W: int, b: int, t: int, L: int, S: int) -> bool:
+    sh = lambda v: tuple(int(d) for d in ir.values[int(v)].shape)  # noqa: E731
+    if len(sh(H)) != 2 or len(sh(W)) != 2:
+        return False
+    B, K = sh(H)
+    C = sh(W)[0]
+    return (sh(W) == (C, K) and sh(b) == (C,) and sh(t) == (B,) and sh(L) == (B, C) and sh(S) == (B, K)
+            and K % 4 == 0 and 4 <= K <= 2048 and 1 <= C <= 32 and "int32" in _dt(ir, t)
+            and all(_f32(ir, v) for v in (H, W, b, L, S)))
+
+
+def fuse_xent_head(ir: IRGraph, lowered: Lowered) -> Lowered:
+    """gemm(H, W^T) -> L; bias_add(L, b) in place; softmax_xent(L, t) ->
+    (loss, dY, pred, row_loss); later gemm(dY, W) -> dH and relu_bwd(dH, S)
+    -> dX  ==>  xent_head(H, W, b, t, S) -> (L, dY, pred, row_loss, dH, dX)
+    followed by loss_mean(row_loss) -> loss (a grad_group job).  The
+    backward gemm and relu_bwd move up to the head: allowed when nothing in
+    between writes W, S, H or dY or reads dH or dX."""
+    out = list(lowered)
+    i = 0
+    while i + 2 < len(out):
+        g, ba, sx = out[i], out[i + 1], out[i + 2]
+        if not (_kind(g) == "gemm" and _kind(ba) == "bias_add" and _kind(sx) == "softmax_xent"):
+            i += 1
+            continue
+        ga = g.get("attrs", {}) or {}
+        if bool(ga.get("transA", False)) or not bool(ga.get("transB", False)) or len(g["inputs"]) != 2:
+            i += 1
+            continue
+        H, W = (int(x) for x in g["inputs"])
+        L = int(g["outputs"][0])
+        if [int(x) for x in ba["inputs"]][:1] != [L] or [int(x) for x in ba["outputs"]] != [L] \
+                or [int(x) for x in sx["inputs"]][:1] != [L] or len(sx["outputs"]) != 4:
+            i += 1
+            continue
+        b, t = int(ba["inputs"][1]), int(sx["inputs"][1])
+        loss, dY, pred, rl = (int(x) for x in sx["outputs"])
+        d = r = None
+        for j in range(i + 3, len(out)):
+            it = out[j]
+            if d is None and _kind(it) == "gemm" and [int(x) for x in it["inputs"]] == [dY, W] and \
+                    not bool((it.get("attrs") or {}).get("transA", False)) and \
+                    not bool((it.get("attrs") or {}).get("transB", False)):
+                d = j
+            elif d is not None and _kind(it) == "relu_bwd" and \
+                    int(it["inputs"][0]) == int(out[d]["outputs"][0]):
+                r = j
+                break
+        if d is None or r is None:
+            i += 1
+            continue
+        dH, S, dX = int(out[d]["outputs"][0]), int(out[r]["inputs"][1]), int(out[r]["outputs"][0])
+        if not _head_shapes_ok(ir, H, W, b, t, L, S):
+            i += 1
+            continue
+        bases_fixed = {_base(ir, v) for v in (W, S, H, dY, b, t)}
+        moved_reads = {_base(ir, v) for v in (dH, dX)}
+        ok = True
+        for j in range(i + 3, r):
+            if j == d:
+                continue
+            it = out[j]
+            if any(_base(ir, o) in (bases_fixed | moved_reads) for o in it["outputs"]) or \
+                    any(_base(ir, v) in moved_reads for v in it["inputs"]):
+                ok = False
+                break
+        if not ok or any(int(v) == dH for k, it in enumerate(out) if k not in (d, r) for v in it["inputs"]):
+            i += 1
+            continue
+        head = _item("xent_head", [H, W, b, t, S], [L, dY, pred, rl, dH, dX])
+        mean = _item("loss_mean", [rl], [loss])
+        out = out[:i] + [head, mean] + [it for k, it in enumerate(out[i + 3:], start=i + 3) if k not in (d, r)]
+        i += 2
+    return out
+
+
+def _job_of(ir: IRGraph, it: Dict[str, Any]) -> Optional[tuple]:
+    """(type, inputs, outputs, f0, f1) when the op can run as a grad_group job."""
+    k = _kind(it)
+    ins, outs = [int(x) for x in it["inputs"]], [int(x) for x in it["outputs"]]
+    attrs = it.get("attrs", {}) or {}
+    if k == "gemm" and len(ins) == 2 and len(outs) == 1 and all(_f32(ir, v) for v in ins + outs):
+        sa, sb = ir.values[ins[0]].shape, ir.values[ins[1]].shape
+        if len(sa) != 2 or len(sb) != 2:
+            return None
+        ta, tb = bool(attrs.get("transA", False)), bool(attrs.get("transB", False))
+        M = sa[1] if ta else sa[0]
+        N = sb[0] if tb else sb[1]
+        if ((M + 63) // 64) * ((N + 63) // 64) >= 128:  # the GEMM dispatcher's small-problem bound
+            return None
+        return (GJ_GEMM, ins, outs, int(ta), int(tb))
+    if k == "reduce_sum" and len(ins) == 1 and len(outs) == 1 and int(attrs.get("axis", 0)) == 0 \
+            and len(ir.values[ins[0]].shape) == 2 and _f32(ir, ins[0]) and _f32(ir, outs[0]):
+        return (GJ_COLSUM, ins, outs, 0, 0)
+    if k == "loss_mean":
+        return (GJ_MEAN, ins, outs, 0, 0)
+    if k == "step_inc" and len(ins) == 1 and len(outs) == 1 and ins == outs:
+        return (GJ_STEP, ins, outs, 1, 0)
+    return None
+
+
+def _group_item(jobs: List[tuple]) -> Dict[str, Any]:
+    ins: List[int] = []
+    outs: List[int] = []
+    recs = []
+    for typ, ji, jo, f0, f1 in jobs:
+        for v in ji:
+            if v not in ins:
+                ins.append(v)
+        for v in jo:
+            if v not in outs:
+                outs.append(v)
+        recs.append([typ, ins.index(ji[0]), ins.index(ji[1]) if len(ji) > 1 else 0, outs.index(jo[0]), f0, f1])
+    return _item("grad_group", ins, outs, {"jobs": recs})
+
+
+def group_small_jobs(ir: IRGraph, lowered: Lowered) -> Lowered:
+    """Runs of consecutive ops that can run as grad_group jobs and are
+    independent (no job reads or writes a buffer another job of the run
+    writes) become one grad_group; a run of one op stays as it is, except
+    loss_mean, which has no kernel of its own."""
+    out: Lowered = []
+    run: List[tuple] = []
+    run_items: Lowered = []
+
+    def flush():
+        if len(run) >= 2 or any(j[0] == GJ_MEAN for j in run):
+            out.append(_group_item(run))
+        else:
+            out.extend(run_items)
+        run.clear()
+        run_items.clear()
+
+    for it in lowered:
+        job = _job_of(ir, it)
+        if job is None:
+            flush()
+            out.append(it)
+            continue
+        _, ji, jo, _, _ = job
+        rb = {_base(ir, v) for j in run for v in j[1]}
+        wb = {_base(ir, v) for j in run for v in j[2]}
+        jr, jw = {_base(ir, v) for v in ji}, {_base(ir, v) for v in jo}
+        if len(run) >= MAX_GROUP_JOBS or (jr & wb) or (jw & (rb | wb)):
+            flush()
+        run.append(job)
+        run_items.append(it)
+    flush()
+    return out
+
+
+def fuse_adamw_multi(ir: IRGraph, lowered: Lowered) -> Lowered:
+    """Consecutive adamw_step(P, G, M, V, step) -> (P, M, V) ops (fp32, in
+    place, same step and hyperparameters, distinct buffers) become
+    adamw_multi((P, G, M, V) x T, step) -> (P, M, V) x T."""
+    out: Lowered = []
+    run: Lowered = []
+
+    def key(it):
+        return (int(it["inputs"][4]), tuple(sorted((it.get("attrs") or {}).items())))
+
+    def flush():
+        if len(run) >= 2:
+            ins: List[int] = []
+            outs: List[int] = []
+            for it in run:
+                ins += [int(x) for x in it["inputs"][:4]]
+                outs += [int(x) for x in it["outputs"]]
+            ins.append(int(run[0]["inputs"][4]))
+            out.append(_item("adamw_multi", ins, outs, dict(run[0].get("attrs") or {})))
+        else:
+            out.extend(run)
+        run.clear()
+
+    for it in lowered:
+        ok = (_kind(it) == "adamw_step" and len(it["inputs"]) == 5 and len(it["outputs"]) == 3
+              and [int(x) for x in it["outputs"]] == [int(it["inputs"][k]) for k in (0, 2, 3)]
+              and all(_f32(ir, int(v)) for v in it["inputs"][:4]))
+        if ok and run:
+            used = {_base(ir, int(v)) for r in run for v in r["inputs"][:4]}
+            if key(it) != key(run[0]) or len(run) >= MAX_ADAMW_TENSORS or \
+                    any(_base(ir, int(v)) in used for v in it["inputs"][:4]):
+                flush()
+        if ok:
+            run.append(it)
+        else:
+            flush()
+            out.append(it)
+    flush()
+    return out
+
+
+def fuse_small_step(ir: IRGraph, lowered: Lowered) -> Lowered:
+    """StageF: drop_dead_saves -> fuse_xent_head -> group_small_jobs ->
+    fuse_adamw_multi."""
+    low = drop_dead_saves(ir, lowered)
+    low = fuse_xent_head(ir, low)
+    low = group_small_jobs(ir, low)
+    low = fuse_adamw_multi(ir, low)
+    assert not any(_kind(it) == "loss_mean" for it in low)
+    return low
+
+
 def compile_lowered(ir: IRGraph, *, fuse: bool = True, fuse_bias: bool = False,
                     nt_layout: Any = False, nt_min_flops: float = 2.0 ** 30,
-                    fuse_optimizer: bool = False, fuse_colsum: bool = False) -> Lowered:
-    """StageA -> StageC -> (StageC') -> (StageD) -> (StageE) -> StageB.
+                    fuse_optimizer: bool = False, fuse_colsum: bool = False,
+                    fuse_small: bool = False) -> Lowered:
+    """StageA -> StageC -> (StageC') -> (StageD) -> (StageE) -> (StageF) -> StageB.
     nt_layout: False (no StageD), True / "all" (transpose every M/N-contiguous
     16-bit operand) or "cost" (transpose only where that is cheaper than
-    reading it in place); fuse_colsum: StageC'; fuse_optimizer: StageE."""
+    reading it in place); fuse_colsum: StageC'; fuse_optimizer: StageE;
+    fuse_small: StageF."""
     low = lower_to_backend_ops(ir)
     if fuse:
         low = fuse_gemm_epilogue(ir, low, fuse_bias=fuse_bias)
@@ -546,6 +806,8 @@ def compile_lowered(ir: IRGraph, *, fuse: bool = True, fuse_bias: bool = False,
         low = normalize_gemm_layout(ir, low, min_flops=nt_min_flops, policy=policy)
     if fuse_optimizer:
         low = fuse_optimizer_into_gemms(ir, low)
+    if fuse_small:
+        low = fuse_small_step(ir, low)
     return apply_kernel_selection(ir, low)
 
 

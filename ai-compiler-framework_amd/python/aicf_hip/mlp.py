@@ -32,7 +32,10 @@ F32, BF16, I32 = "torch.float32", "torch.bfloat16", "torch.int32"
 # ============================================================ xent MLP (fp32)
 def build_mlp_xent(B: int = 64, din: int = 784, dh: int = 256, dout: int = 10, *,
                    lr: float = 1e-3, beta1: float = 0.9, beta2: float = 0.999,
-                   eps: float = 1e-8, device: str = "cuda:0"):
+                   eps: float = 1e-8, device: str = "cuda:0", fuse_small: bool = False):
+    """fuse_small: StageF (the step in four launches: forward GEMM, xent
+    head, gradient group, multi-tensor AdamW); off, the lowering is the
+    reference pipeline's (17 ops)."""
     ir = IRGraph(name=f"mlp_xent_{B}x{din}x{dh}x{dout}")
     nv = lambda n, s, dt=F32: ir.new_value(name=n, shape=s, dtype=dt, device=device)  # noqa: E731
     x = nv("x", (B, din))
@@ -68,7 +71,7 @@ def build_mlp_xent(B: int = 64, din: int = 784, dh: int = 256, dout: int = 10, *
         m = nv(f"opt.m.{p.name}", p.shape)
         v = nv(f"opt.v.{p.name}", p.shape)
         ir.emit(op="AdamWStep", inputs=[p, g, m, v, step], outputs=[p, m, v], attrs=hp)
-    lowered = compile_lowered(ir)
+    lowered = compile_lowered(ir, fuse_small=fuse_small)
     plan = build_binding_plan(ir)
     return ir, lowered, plan
 

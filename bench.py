@@ -120,13 +120,14 @@ def bench_c4(C, dtype="bf16", shapes=C4_SHAPES, acts=("none", "relu", "gelu"), i
 
 
 # C1: the reference MLP (fp32, B=64, 784->256(ReLU)->10, softmax-xent, Adam)
-def bench_c1(steps=200, warmup=5):
-    """Replayed-graph time of one C1 train step."""
+def bench_c1(steps=200, warmup=5, fuse_small=True):
+    """Replayed-graph time of one C1 train step; fuse_small: the four-launch
+    lowering (StageF), else the reference pipeline's 17 ops."""
     import torch
 
     from aicf_hip import mlp
 
-    ir, lowered, plan = mlp.build_mlp_xent()
+    ir, lowered, plan = mlp.build_mlp_xent(fuse_small=fuse_small)
     data = mlp.init_mlp_xent()
     params = {k: torch.from_numpy(v.copy()).cuda() for k, v in data.items() if "." in k}
     inputs = {"x": torch.from_numpy(data["x"]).cuda(), "t": torch.from_numpy(data["t"]).cuda()}
@@ -1233,6 +1234,7 @@ def main():
                     "the headline keeps it, as the reference's lowering emits it"}
         log(f"[bench] mlp without dead dX {nd}")
         c1 = bench_c1()
+        c1["reference_lowering"] = bench_c1(fuse_small=False)
         comps["c1_mlp_fp32_64x784x256x10_step"] = c1
         log(f"[bench] c1 {c1}")
         for dt, shapes in (("bf16", C4_SHAPES), ("fp32", C4_SHAPES)):

@@ -71,7 +71,13 @@ extern "C" {
 #define AICF_OP_ELTWISE_GELU 22 /* X -> gelu_tanh(X) */
 #define AICF_OP_TRANSPOSE 23    /* X[R,C] -> X^T[C,R] (2-D, row-major) */
 #define AICF_OP_GEMM_ADAMW 24   /* A, B, P, M, V, step -> P, M, V, Wb: AdamW on P with grad op(A).op(B) (schema GADW) */
-#define AICF_OP_COUNT 25
+#define AICF_OP_XENT_HEAD 25     /* H, W, b, labels, S -> logits, dlogits, argmax, row loss, dH, dX: the
+                                    classifier head of a ReLU MLP forward and backward (softmax xent,
+                                    dH = dlogits.W, dX = dH where S > 0) */
+#define AICF_OP_GRAD_GROUP 26    /* independent small jobs in one launch: GEMMs, column sums, a loss
+                                    mean, the step counter (schema GGRP) */
+#define AICF_OP_ADAMW_MULTI 27   /* (P, G, M, V) x T, step -> (P, M, V) x T: AdamW over T tensors (schema ADAM) */
+#define AICF_OP_COUNT 28
 
 /*
  * Attribute schema ids (numeric ABI).  The reference mixes big-endian fourccs
@@ -89,6 +95,9 @@ extern "C" {
 #define AICF_SCHEMA_LNEP 0x50454E4Cu /* layernorm/launcher.cu:41      <f>   eps (default 1e-5) */
 #define AICF_SCHEMA_BNEP 0x50454E42u /* batchnorm/launcher.cu:51      <fI>  eps, flags (bit0 use_running_stats) */
 #define AICF_SCHEMA_RRED 0x44455252u /* appended: b"RRED" little-endian, <i> 0=sum 1=max */
+#define AICF_SCHEMA_GGRP 0x50524747u /* appended: b"GGRP" little-endian, <i n> + n x <iiiiii> type, in0, in1,
+                                       out0, f0, f1 (type 0 GEMM f0,f1 = transA,transB; 1 column sum;
+                                       2 mean; 3 step counter += f0) */
 #define AICF_SCHEMA_GADW 0x57444147u /* appended: b"GADW" little-endian, <ii fffff> transA, transB, lr, b1, b2, eps, wd */
 
 /* GEPI epilogue kinds.  0..2 are the values core_v2/exec.py:223-252 packs;
