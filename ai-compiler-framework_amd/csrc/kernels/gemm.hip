@@ -938,8 +938,28 @@ constexpr bool nt_persistent(int BM, int BN, int WM, int WN) {
   return BM == 256 && BN == 256 && WM * WN == 8;
 }
 
-template <int IN, int OUT, int ACT, int BM, int BN, int WM, int WN, bool AKC, bool BKC>
+// s_waitcnt immediate for vmcnt(n), lgkmcnt(0), expcnt left alone (gfx9
+// layout: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (((N >> 4) & 0x3) << 14));
+}
+
+// Workgroup barrier without the vmcnt(0) the compiler puts in front of
+// __syncthreads (its release fence waits for every load in flight, which
+// would drain a pipeline of more than two stages); the "memory" clobber
+// keeps the compiler from moving memory accesses across it.  The caller
+// waits right before for what the barrier publishes (its own loads of the
+// next stage, its LDS reads of the stage about to be refilled).
+__device__ __forceinline__ void barrier_keep_loads() { asm volatile("s_barrier" ::: "memory"); }
+
+// S: LDS stages.  Two for the large tiles (their K-step's MFMA work covers a
+// load's latency); small tiles, whose K-step is a few hundred cycles of MFMA
+// work, keep S - 1 K-steps of loads in flight.
+template <int IN, int OUT, int ACT, int BM, int BN, int WM, int WN, bool AKC, bool BKC, int S = 2>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_nt_kernel(NTParams p) {
+  static_assert(S == 2 || S == 4 || S == 8, "stages: 2, 4 or 8");
   constexpr int ES = IN == IN_F32 ? 4 : 2;  // element bytes
   // MFMA block: 16 x 16 x 32 for 16-bit operands, 32 x 32 x 2 for fp32
   constexpr int MS = ES == 2 ? 16 : 32;
@@ -951,7 +971,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt_kernel(NTParams p) {
   constexpr int TM = WTM / MS, TN = WTN / MS;
   constexpr int A_BYTES = BM * 128, B_BYTES = BN * 128;  // 128 B of K per row and stage
   constexpr int STAGE = A_BYTES + B_BYTES;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[S * STAGE];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / WN, wn = wave % WN;
@@ -1149,10 +1169,30 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt_kernel(NTParams p) {
 
   const int nk = p.K / (128 / ES);
   constexpr int L1 = NVM / 2;  // with four sub-steps: loads in the first of the two
+  // Wait until at most n K-steps of this wave's loads are in flight (and its
+  // fragment reads are done); n < S - 1.
+  auto wait_steps = [&](int n) {
+    if constexpr (S > 2) {
+      if (n >= 6) { wait_vm_lgkm0<6 * NVM>(); return; }
+      if (n == 5) { wait_vm_lgkm0<5 * NVM>(); return; }
+      if (n == 4) { wait_vm_lgkm0<4 * NVM>(); return; }
+      if (n == 3) { wait_vm_lgkm0<3 * NVM>(); return; }
+      if (n == 2) { wait_vm_lgkm0<2 * NVM>(); return; }
+      if (n == 1) { wait_vm_lgkm0<NVM>(); return; }
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+  };
   issue_loads(0, 0);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (nk > 1) issue_loads(1, 1);
+  if constexpr (S > 2) {
+    // K-steps 1 .. S - 2 go out before the first wait
+    for (int q = 1; q < S - 1 && q < nk; ++q) issue_loads(q, q);
+    wait_steps((nk - 1 < S - 2 ? nk - 1 : S - 2));
+    barrier_keep_loads();
+  } else {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+  if (S - 1 < nk) issue_loads(S - 1, S - 1);
   read_frags(smem, 0, 0);
   if constexpr (KS == 4) {
     substep(Rd{}, z, z, 0, smem, 1, 1, 0, 0);
@@ -1162,26 +1202,49 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt_kernel(NTParams p) {
     substep(Rd{}, z, z, 0, smem, 1, 1, 0, 0);
   }
   int kt = 0;
-  for (; kt + 2 < nk; ++kt) {
-    __builtin_amdgcn_s_waitcnt(0);  // own loads of K-step kt+1 and fragment reads done
-    __syncthreads();
-    const uint8_t* nx = smem + ((kt + 1) & 1) * STAGE;
-    const int ls = kt & 1;
+  for (; kt + S < nk; ++kt) {
+    // own loads of K-step kt+1 and fragment reads done; K-steps kt+2 ..
+    // kt+S-1 may still be in flight
+    if constexpr (S > 2) {
+      wait_vm_lgkm0<(S - 2) * NVM>();
+      barrier_keep_loads();
+    } else {
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    }
+    const uint8_t* nx = smem + ((kt + 1) % S) * STAGE;
+    const int ls = kt % S;  // the stage of K-step kt, free after the barrier, takes K-step kt+S
     if constexpr (KS == 4) {
-      substep(Rd{}, z, template_int_t<L1>{}, 1, nx, 0, 0, kt + 2, ls);
-      substep(Rd{}, template_int_t<L1>{}, template_int_t<NVM>{}, 0, nx, 1, 1, kt + 2, ls);
+      substep(Rd{}, z, template_int_t<L1>{}, 1, nx, 0, 0, kt + S, ls);
+      substep(Rd{}, template_int_t<L1>{}, template_int_t<NVM>{}, 0, nx, 1, 1, kt + S, ls);
       substep(Rd{}, z, z, 1, nx, 2, 0, 0, 0);
       substep(Rd{}, z, z, 0, nx, 3, 1, 0, 0);
     } else {
-      // two sub-steps of twice the MFMAs: the loads of K-step kt+2 over the first
-      substep(Rd{}, z, template_int_t<NVM>{}, 1, nx, 0, 0, kt + 2, ls);
+      // two sub-steps of twice the MFMAs: the loads of K-step kt+S over the first
+      substep(Rd{}, z, template_int_t<NVM>{}, 1, nx, 0, 0, kt + S, ls);
       substep(Rd{}, z, z, 0, nx, 1, 1, 0, 0);
+    }
+  }
+  if constexpr (S > 2) {
+    for (; kt + 2 < nk; ++kt) {  // nothing left to load: K-steps kt+2 .. nk-1 in flight
+      wait_steps(nk - 2 - kt);
+      barrier_keep_loads();
+      const uint8_t* nx = smem + ((kt + 1) % S) * STAGE;
+      if constexpr (KS == 4) {
+        substep(Rd{}, z, z, 1, nx, 0, 0, 0, 0);
+        substep(Rd{}, z, z, 0, nx, 1, 1, 0, 0);
+        substep(Rd{}, z, z, 1, nx, 2, 0, 0, 0);
+        substep(Rd{}, z, z, 0, nx, 3, 1, 0, 0);
+      } else {
+        substep(Rd{}, z, z, 1, nx, 0, 0, 0, 0);
+        substep(Rd{}, z, z, 0, nx, 1, 1, 0, 0);
+      }
     }
   }
   if (kt + 1 < nk) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    const uint8_t* nx = smem + ((kt + 1) & 1) * STAGE;
+    const uint8_t* nx = smem + ((kt + 1) % S) * STAGE;
     if constexpr (KS == 4) {
       substep(Rd{}, z, z, 1, nx, 0, 0, 0, 0);
       substep(Rd{}, z, z, 0, nx, 1, 1, 0, 0);
@@ -1298,7 +1361,7 @@ int device_cu_count() {
   return cached[dev];
 }
 
-template <int IN, int OUT, int ACT, int BM, int BN, int WM, int WN, bool AKC, bool BKC>
+template <int IN, int OUT, int ACT, int BM, int BN, int WM, int WN, bool AKC, bool BKC, int S = 2>
 Status run_nt_act(const GemmParams& g, hipStream_t s) {
   NTParams p{};
   p.A = g.A;
@@ -1326,31 +1389,31 @@ Status run_nt_act(const GemmParams& g, hipStream_t s) {
     const int ncu = device_cu_count();
     if (ncu > 0 && ncu % 8 == 0 && grid > (unsigned)ncu) grid = (unsigned)ncu;
   }
-  gemm_nt_kernel<IN, OUT, ACT, BM, BN, WM, WN, AKC, BKC><<<grid, 64 * WM * WN, 0, s>>>(p);
+  gemm_nt_kernel<IN, OUT, ACT, BM, BN, WM, WN, AKC, BKC, S><<<grid, 64 * WM * WN, 0, s>>>(p);
   return launch_status("gemm_nt");
 }
 
-template <int IN, int OUT, int BM, int BN, int WM, int WN, bool AKC, bool BKC>
+template <int IN, int OUT, int BM, int BN, int WM, int WN, bool AKC, bool BKC, int S = 2>
 Status run_nt_layout(const GemmParams& g, hipStream_t s) {
   switch (g.act) {
-    case ACT_RELU: return run_nt_act<IN, OUT, ACT_RELU, BM, BN, WM, WN, AKC, BKC>(g, s);
-    case ACT_GELU: return run_nt_act<IN, OUT, ACT_GELU, BM, BN, WM, WN, AKC, BKC>(g, s);
-    case ACT_DGELU: return run_nt_act<IN, OUT, ACT_DGELU, BM, BN, WM, WN, AKC, BKC>(g, s);
+    case ACT_RELU: return run_nt_act<IN, OUT, ACT_RELU, BM, BN, WM, WN, AKC, BKC, S>(g, s);
+    case ACT_GELU: return run_nt_act<IN, OUT, ACT_GELU, BM, BN, WM, WN, AKC, BKC, S>(g, s);
+    case ACT_DGELU: return run_nt_act<IN, OUT, ACT_DGELU, BM, BN, WM, WN, AKC, BKC, S>(g, s);
     case ACT_ADAMW:
       if constexpr (OUT == OUT_F32 && BM == 256 && BN == 256)
         return run_nt_act<IN, OUT, ACT_ADAMW, BM, BN, WM, WN, AKC, BKC>(g, s);
       return Status::Internal;  // fused AdamW runs on the 256 x 256 fp32-output tiles only
-    default: return run_nt_act<IN, OUT, ACT_NONE, BM, BN, WM, WN, AKC, BKC>(g, s);
+    default: return run_nt_act<IN, OUT, ACT_NONE, BM, BN, WM, WN, AKC, BKC, S>(g, s);
   }
 }
 
 // Operand layouts: K-contiguous ([MN][K]) on every tile configuration;
 // MN-contiguous ([K][MN], read through the transposing LDS loads) on the
 // 256 x 256 configuration (MN_OK).
-template <int IN, int OUT, int BM, int BN, int WM, int WN, bool MN_OK>
+template <int IN, int OUT, int BM, int BN, int WM, int WN, bool MN_OK, int S = 2>
 Status run_nt(const GemmParams& g, hipStream_t s) {
   const bool akc = g.a_mode == LD_KCONTIG, bkc = g.b_mode == LD_KCONTIG;
-  if (akc && bkc) return run_nt_layout<IN, OUT, BM, BN, WM, WN, true, true>(g, s);
+  if (akc && bkc) return run_nt_layout<IN, OUT, BM, BN, WM, WN, true, true, S>(g, s);
   if constexpr (MN_OK) {
     if (akc) return run_nt_layout<IN, OUT, BM, BN, WM, WN, true, false>(g, s);
     if (bkc) return run_nt_layout<IN, OUT, BM, BN, WM, WN, false, true>(g, s);
@@ -1457,10 +1520,24 @@ Status run_gemm(GemmParams& p, hipStream_t s) {
         nt_eligible<IN, OUT>(p, 128, 128, false))
       return run_nt<IN, OUT, 128, 128, 2, 2, false>(p, s);
     if (tiles256 >= 128 && nt_eligible<IN, OUT>(p, 256, 256, MN)) return run_nt256<IN, OUT>(p, s);
-    if (tiles128 >= 128 && nt_eligible<IN, OUT>(p, 128, 128, false))
+    // 16-bit operands with at least 16 K-steps: small tiles take deeper
+    // pipelines (a K-step is a few hundred cycles of MFMA work per wave, less
+    // than a load's latency).  128 x 128 with 4 stages needs all of LDS, so
+    // only where one workgroup per CU is all the grid gives anyway.
+    const bool deep = IN != IN_F32 && p.K >= 16 * (128 / (IN == IN_F32 ? 4 : 2));
+    if (tiles128 >= 128 && nt_eligible<IN, OUT>(p, 128, 128, false)) {
+      if constexpr (IN != IN_F32) {
+        if (deep && tiles128 <= 256) return run_nt<IN, OUT, 128, 128, 2, 2, false, 4>(p, s);
+      }
       return run_nt<IN, OUT, 128, 128, 2, 2, false>(p, s);
+    }
     // fewer tiles than CUs at 128x128: 64x64 tiles (4 waves of 32x32)
-    if (nt_eligible<IN, OUT>(p, 64, 64, false)) return run_nt<IN, OUT, 64, 64, 2, 2, false>(p, s);
+    if (nt_eligible<IN, OUT>(p, 64, 64, false)) {
+      if constexpr (IN != IN_F32) {
+        if (deep) return run_nt<IN, OUT, 64, 64, 2, 2, false, 8>(p, s);
+      }
+      return run_nt<IN, OUT, 64, 64, 2, 2, false>(p, s);
+    }
     if (nt_eligible<IN, OUT>(p, 128, 128, false)) return run_nt<IN, OUT, 128, 128, 2, 2, false>(p, s);
   }
   // Large problems: 128x128 workgroup tiles (4 waves, 64x64 per wave).

@@ -224,3 +224,39 @@ def test_no_nt_kernel_uses_scratch(asm):
         seg = re.search(r"\.amdhsa_private_segment_fixed_size\s+(\d+)", m.group(2))
         assert seg and int(seg.group(1)) == 0, (m.group(1), seg.group(1) if seg else None)
     assert found > 100, found
+
+
+# Small-tile kernels with deeper pipelines (S LDS stages): the loop that
+# issues loads waits once per K-step with vmcnt((S - 2) x loads per K-step),
+# so S - 2 K-steps of loads stay in flight across the barrier, and no
+# vmcnt(0) (from __syncthreads' fence or a compiler-inserted wait) drains them.
+DEEP = [("gemm_nt_kernelILi2ELi2ELi0ELi64ELi64ELi2ELi2ELb1ELb1ELi8E", 24),   # 64x64, 8 stages, 4 loads
+        ("gemm_nt_kernelILi2ELi2ELi3ELi64ELi64ELi2ELi2ELb1ELb1ELi8E", 24),   # with the GELU epilogue
+        ("gemm_nt_kernelILi2ELi2ELi0ELi128ELi128ELi2ELi2ELb1ELb1ELi4E", 16)]  # 128x128, 4 stages, 8 loads
+
+
+def loops(lines: list[str]) -> list[list[str]]:
+    out = []
+    for i, ln in enumerate(lines):
+        if "Loop Header" not in ln:
+            continue
+        j = i
+        while j >= 0 and not lines[j].startswith(".LBB"):
+            j -= 1
+        label = lines[j].split(":")[0]
+        for k in range(j + 1, len(lines)):
+            if re.search(r"s_cbranch_\w+\s+" + re.escape(label) + r"\b", lines[k]):
+                out.append(lines[j:k + 1])
+                break
+    return out
+
+
+@pytest.mark.parametrize("kernel,vm", DEEP)
+def test_deep_pipeline_keeps_loads_in_flight(asm, kernel, vm):
+    body = kernel_body(asm, kernel)
+    main = [lp for lp in loops(body) if any("v_mfma" in l for l in lp)
+            and any(re.search(r"(buffer|global)_load\w*.*\blds\b", l) for l in lp)]
+    assert len(main) == 1, len(main)
+    waits = [l.strip() for l in main[0] if "s_waitcnt" in l and "vmcnt" in l]
+    assert waits == [f"s_waitcnt vmcnt({vm}) lgkmcnt(0)"], waits
+    assert sum("s_barrier" in l for l in main[0]) == 1

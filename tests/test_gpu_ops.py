@@ -422,7 +422,11 @@ def test_gemm_f16_probe_shapes(C, ta, tb):
 @pytest.mark.parametrize("M,N,K,ta,tb", [
     (4096, 4096, 128, False, True),   # 256x256 tiles
     (2048, 1024, 128, False, True),   # 128x128 tiles
-    (1024, 1024, 1024, False, True),  # 64x64 tiles
+    (1024, 1024, 1024, False, True),  # 64x64 tiles, 8 LDS stages (16 K-steps: no tail loop)
+    (1024, 512, 1088, False, True),   # 64x64, 8 stages, 17 K-steps: the tail loop's waits
+    (1024, 1024, 4096, False, True),  # 64x64, 8 stages, 64 K-steps
+    (2048, 2048, 2048, False, True),  # 128x128 tiles, 4 stages
+    (2048, 2048, 1088, False, True),  # 128x128, 4 stages, 17 K-steps
     (100, 72, 784, False, True),
     (64, 256, 784, False, True),
     (256, 4096, 256, False, True),
@@ -588,8 +592,10 @@ def test_gemm_epilogue_default_is_bias_relu_and_gepi_kinds(C):
 
 
 @pytest.mark.parametrize("M,N,K", [(256, 512, 384), (1024, 1024, 1024), (100, 200, 64),
-                                   (4096, 4096, 64)])
+                                   (4096, 4096, 64), (2048, 2048, 1024)])
 def test_gemm_epilogue_bf16_gelu_aux_and_dgelu(C, M, N, K):
+    """bias+GELU with the pre-activation (1024^3: 64x64 tiles, 8 LDS stages;
+    2048 x 2048 x 1024: 128x128 tiles, 4 stages) and the dGELU epilogue."""
     r = rng(15)
     s = 1.0 / np.sqrt(K)
     X = orc.bf16_bits_from_f32(r.uniform(-1, 1, (M, K)).astype(np.float32))
