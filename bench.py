@@ -40,11 +40,41 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def time_launches(fn, iters: int, warmup: int, stream=None) -> float:
-    """Average milliseconds per call of fn(), HIP events on `stream`
-    (torch's current stream by default)."""
+def _cs() -> int:
+    """torch's current stream as the launch stream argument."""
     import torch
 
+    return torch.cuda.current_stream().cuda_stream
+
+
+def time_launches(fn, iters: int, warmup: int, stream=None, graph: bool = False) -> float:
+    """Average milliseconds per call of fn(), HIP events on `stream`
+    (torch's current stream by default).  graph: the `iters` calls are
+    captured into one graph (fn launches on torch's current stream) and the
+    graph is timed, so that kernels of a few microseconds are timed back to
+    back on the device rather than at the rate the host issues them."""
+    import torch
+
+    if graph:
+        gs = torch.cuda.Stream()
+        with torch.cuda.stream(gs):
+            for _ in range(warmup):
+                fn()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=gs):
+            for _ in range(iters):
+                fn()
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        rs = torch.cuda.current_stream()  # replay() launches on torch's current stream
+        e0.record(rs)
+        g.replay()
+        e1.record(rs)
+        torch.cuda.synchronize()
+        del g
+        return e0.elapsed_time(e1) / iters
     s = stream or torch.cuda.current_stream()
     for _ in range(warmup):
         fn()
@@ -170,9 +200,9 @@ def bench_softmax(C, rows, cols, iters=20, warmup=3):
     def fn():
         x, y, mx, sm = sets[k[0] % nsets]
         k[0] += 1
-        C.op_call(int(C.OpKind.RowSoftmax), [x, ], [y, mx, sm], 0, b"", 0)
+        C.op_call(int(C.OpKind.RowSoftmax), [x, ], [y, mx, sm], 0, b"", _cs())
 
-    ms = time_launches(fn, iters, warmup)
+    ms = time_launches(fn, iters, warmup, graph=True)
     nbytes = 8 * rows * cols + 8 * rows
     return {"ms": ms, "gbs": nbytes / (ms * 1e-3) / 1e9, "bytes": nbytes, "buffer_sets": nsets}
 
@@ -201,9 +231,9 @@ def bench_rowreduce(C, rows, cols, op, iters=20, warmup=3):
     def fn():
         x, o = sets[k[0] % len(sets)]
         k[0] += 1
-        C.op_call(int(C.OpKind.RowReduce), [x], [o], RRED, pay, 0)
+        C.op_call(int(C.OpKind.RowReduce), [x], [o], RRED, pay, _cs())
 
-    ms = time_launches(fn, iters, warmup)
+    ms = time_launches(fn, iters, warmup, graph=True)
     nbytes = 4 * rows * cols + 4 * rows
     return {"ms": ms, "gbs": nbytes / (ms * 1e-3) / 1e9, "buffer_sets": len(sets)}
 
@@ -228,9 +258,9 @@ def bench_xent(C, rows, cols, iters=20, warmup=3):
     def fn():
         z, lab, loss, dz, am, rl = sets[k[0] % len(sets)]
         k[0] += 1
-        C.op_call(int(C.OpKind.SoftmaxXent), [z, lab], [loss, dz, am, rl], 0, b"", 0)
+        C.op_call(int(C.OpKind.SoftmaxXent), [z, lab], [loss, dz, am, rl], 0, b"", _cs())
 
-    ms = time_launches(fn, iters, warmup)
+    ms = time_launches(fn, iters, warmup, graph=True)
     nbytes = 8 * rows * cols + 16 * rows  # logits in, dlogits out, labels, argmax, row loss (r+w)
     return {"ms": ms, "gbs": nbytes / (ms * 1e-3) / 1e9, "buffer_sets": len(sets)}
 
@@ -255,9 +285,9 @@ def bench_mse(C, rows, cols, iters=20, warmup=3):
     def fn():
         p, t, d, loss, part = sets[k[0] % len(sets)]
         k[0] += 1
-        C.launch_by_id("mse_loss_grad_v0", C.OpKind.MseGrad, [p, t], [d, loss, part])
+        C.launch_by_id("mse_loss_grad_v0", C.OpKind.MseGrad, [p, t], [d, loss, part], 0, b"", _cs())
 
-    ms = time_launches(fn, iters, warmup)
+    ms = time_launches(fn, iters, warmup, graph=True)
     nbytes = 8 * rows * cols
     return {"ms": ms, "gbs": nbytes / (ms * 1e-3) / 1e9, "buffer_sets": len(sets)}
 
@@ -279,9 +309,10 @@ def bench_colsum(C, rows, cols, iters=20, warmup=3):
     def fn():
         x, o, part = sets[k[0] % len(sets)]
         k[0] += 1
-        C.launch_by_id("reduce_sum_keep_lastdim_bf16_to_f32_v0", C.OpKind.ReduceSum, [x], [o, part])
+        C.launch_by_id("reduce_sum_keep_lastdim_bf16_to_f32_v0", C.OpKind.ReduceSum, [x], [o, part], 0, b"",
+                       _cs())
 
-    ms = time_launches(fn, iters, warmup)
+    ms = time_launches(fn, iters, warmup, graph=True)
     nbytes = 2 * rows * cols + 4 * cols
     return {"ms": ms, "gbs": nbytes / (ms * 1e-3) / 1e9, "buffer_sets": len(sets)}
 
