@@ -182,12 +182,32 @@ struct XentHeadArgs {
 };
 
 // Q: 16-byte vectors per lane along K (K <= 256 Q); CM: classes (C <= CM).
+// One wave (one row) per workgroup, so that the rows spread over as many CUs
+// as there are rows.  With Q x CM <= 16 the lane's slice of W is loaded once,
+// together with the row, and serves both the logits and dH.
 template <int Q, int CM>
-__global__ __launch_bounds__(256) void xent_head_kernel(XentHeadArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= a.B) return;  // a whole wave; the kernel has no barrier
+__global__ __launch_bounds__(64) void xent_head_kernel(XentHeadArgs a) {
+  const int lane = threadIdx.x;
+  const int64_t row = blockIdx.x;
   const int K4 = a.K >> 2;
+  constexpr bool PRE = Q * CM <= 16;
+  f32x4 wreg[PRE ? Q * CM : 1];
+  if constexpr (PRE) {
+#pragma unroll
+    for (int c = 0; c < CM; ++c)
+#pragma unroll
+      for (int q = 0; q < Q; ++q) {
+        const int idx = q * 64 + lane;
+        wreg[c * Q + q] = (c < a.C && idx < K4) ? reinterpret_cast<const f32x4*>(a.W + (int64_t)c * a.K)[idx]
+                                                : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+  }
+  auto wload = [&](int c, int q, int idx) -> f32x4 {
+    if constexpr (PRE)
+      return wreg[c * Q + q];
+    else
+      return reinterpret_cast<const f32x4*>(a.W + (int64_t)c * a.K)[idx];
+  };
   const f32x4* hr = reinterpret_cast<const f32x4*>(a.H + row * a.K);
   f32x4 h[Q];
 #pragma unroll
@@ -204,13 +224,12 @@ __global__ __launch_bounds__(256) void xent_head_kernel(XentHeadArgs a) {
   for (int c = 0; c < CM; ++c) {
     z[c] = 0.0f;
     if (c < a.C) {
-      const f32x4* wr = reinterpret_cast<const f32x4*>(a.W + (int64_t)c * a.K);
       float p = 0.0f;
 #pragma unroll
       for (int q = 0; q < Q; ++q) {
         const int idx = q * 64 + lane;
         if (idx < K4) {
-          const f32x4 w = wr[idx];
+          const f32x4 w = wload(c, q, idx);
           p = fmaf(h[q][0], w[0], p);
           p = fmaf(h[q][1], w[1], p);
           p = fmaf(h[q][2], w[2], p);
@@ -271,7 +290,7 @@ __global__ __launch_bounds__(256) void xent_head_kernel(XentHeadArgs a) {
 #pragma unroll
     for (int c = 0; c < CM; ++c) {
       if (c < a.C) {
-        const f32x4 w = reinterpret_cast<const f32x4*>(a.W + (int64_t)c * a.K)[idx];
+        const f32x4 w = wload(c, q, idx);
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[i] = fmaf(d[c], w[i], acc[i]);
       }
@@ -322,9 +341,9 @@ bool xent_head_sup(const TensorDesc* in, int ni, const TensorDesc* out, int no, 
 template <int Q>
 void xent_head_go(const XentHeadArgs& a, unsigned grid, hipStream_t s) {
   if (a.C <= 16)
-    xent_head_kernel<Q, 16><<<grid, 256, 0, s>>>(a);
+    xent_head_kernel<Q, 16><<<grid, 64, 0, s>>>(a);
   else
-    xent_head_kernel<Q, 32><<<grid, 256, 0, s>>>(a);
+    xent_head_kernel<Q, 32><<<grid, 64, 0, s>>>(a);
 }
 
 Status xent_head_launch(const TensorDesc* in, int ni, TensorDesc* out, int no, const void* at, void*,
@@ -346,7 +365,7 @@ Status xent_head_launch(const TensorDesc* in, int ni, TensorDesc* out, int no, c
   a.K = (int)in[0].shape[1];
   a.C = (int)in[1].shape[0];
   a.inv_batch = 1.0f / (float)a.B;
-  const unsigned grid = (unsigned)((a.B + 3) / 4);
+  const unsigned grid = (unsigned)a.B;  // one row per workgroup
   const int q = (a.K / 4 + 63) / 64;
   hipStream_t s = as_stream(stream);
   if (q <= 1)

@@ -395,11 +395,11 @@ STEP_GEMM_OPS = ("gemm", "gemm_epilogue", "gemm_adamw")
 # the kernel name): role, launches per step (B=8192, D=4096, L=4) and
 # algorithmic MiB moved per launch.
 STEP_GEMM_ROLES = [
-    ("<2, 2, 2, 256, 256, 2, 4, true, true>", "fwd bias+GELU (+Z)", 3, 64 + 32 + 64 + 64),
-    ("<2, 2, 0, 256, 256, 2, 2, true, true>", "fwd bias (last layer)", 1, 64 + 32 + 64),
-    ("<2, 2, 3, 256, 256, 2, 4, true, false>", "dX with dGELU", 3, 64 + 32 + 64 + 64),
-    ("<2, 2, 0, 256, 256, 2, 4, true, false>", "dX (first layer)", 1, 64 + 32 + 64),
-    ("<2, 0, 4, 256, 256, 2, 4, false, false>", "dW + AdamW", 4, 64 + 64 + 3 * 64 * 2 + 32),
+    ("<2, 2, 2, 256, 256, 2, 4, true, true, 2>", "fwd bias+GELU (+Z)", 3, 64 + 32 + 64 + 64),
+    ("<2, 2, 0, 256, 256, 2, 2, true, true, 2>", "fwd bias (last layer)", 1, 64 + 32 + 64),
+    ("<2, 2, 3, 256, 256, 2, 4, true, false, 2>", "dX with dGELU", 3, 64 + 32 + 64 + 64),
+    ("<2, 2, 0, 256, 256, 2, 4, true, false, 2>", "dX (first layer)", 1, 64 + 32 + 64),
+    ("<2, 0, 4, 256, 256, 2, 4, false, false, 2>", "dW + AdamW", 4, 64 + 64 + 3 * 64 * 2 + 32),
 ]
 
 
@@ -809,6 +809,112 @@ def pmc_mfma_compare_report(counter_csv, trace_csv):
     print("\n".join(lines))
 
 
+VENDOR_PASSES = [
+    "SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE SQ_INSTS_VALU_MFMA_MOPS_BF16 SQ_INSTS_LDS SQ_LDS_BANK_CONFLICT "
+    "SQ_LDS_IDX_ACTIVE SQ_INSTS_VMEM_RD SQ_INSTS_VMEM_WR SQ_INSTS_SALU",
+    "TA_TA_BUSY_sum TD_TD_BUSY_sum TCP_TOTAL_CACHE_ACCESSES_sum TCP_TCC_READ_REQ_sum SQ_WAIT_INST_LDS "
+    "SQ_WAIT_ANY SQ_WAVE_CYCLES SQ_INSTS_VALU GRBM_GUI_ACTIVE",
+]
+
+
+def pmc_compare_report(*paths):
+    """Per-flop counter comparison of our bf16 GEMM and hipBLASLt on the same
+    operands, from the two rocprofv3 --pmc passes of --vendor-compare
+    (VENDOR_PASSES, each with --kernel-trace): arguments are counter_csv,
+    trace_csv of pass 1, then of pass 2.  Launches are grouped by library,
+    kernel and grid (the shape); the first launch of a group is dropped."""
+    import csv
+    from collections import OrderedDict, defaultdict
+
+    def load(counter_csv, trace_csv):
+        cnt = defaultdict(lambda: defaultdict(float))
+        meta = {}
+        with open(counter_csv, newline="") as f:
+            for row in csv.DictReader(f):
+                d = int(row["Dispatch_Id"])
+                cnt[d][row["Counter_Name"]] += float(row["Counter_Value"])
+                meta[d] = (row.get("Kernel_Name", ""), row.get("Grid_Size", ""))
+        dur = {}
+        with open(trace_csv, newline="") as f:
+            for row in csv.DictReader(f):
+                dur[int(row["Dispatch_Id"])] = (int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) * 1e-9
+        groups = OrderedDict()
+        for d in sorted(cnt):
+            n, grid = meta[d]
+            if not ("gemm_nt" in n or "Cijk" in n) or d not in dur:
+                continue
+            short = n.replace("void aicf::hip::(anonymous namespace)::", "").split("(")[0][:64]
+            groups.setdefault((("ours " if "gemm_nt" in n else "hipBLASLt ") + short, grid), []).append(d)
+        out = OrderedDict()
+        for key, ds in groups.items():
+            ds = ds[1:] if len(ds) > 4 else ds
+            m = defaultdict(float)
+            for d in ds:
+                for k, v in cnt[d].items():
+                    m[k] += v / len(ds)
+            m["_us"] = sum(dur[d] for d in ds) / len(ds) * 1e6
+            m["_n"] = len(ds)
+            out[key] = m
+        return out
+
+    p1 = load(paths[0], paths[1])
+    p2 = load(paths[2], paths[3]) if len(paths) >= 4 else {}
+    lines = [
+        "# bf16 GEMM on MI355X: our kernel vs hipBLASLt, per-flop counters",
+        "",
+        "Commands (GPU box, repo root; one rocprofv3 run per counter pass):",
+        "```",
+    ]
+    for i, pas in enumerate(VENDOR_PASSES):
+        lines.append(f"rocprofv3 --pmc {pas} --kernel-trace --output-format csv -d gpurun_out/pmc_v{i + 1} -o run "
+                     "-- python3 bench.py --vendor-compare")
+    lines += [
+        "python3 bench.py --pmc-compare-report gpurun_out/pmc_v1/run_counter_collection.csv "
+        "gpurun_out/pmc_v1/run_kernel_trace.csv gpurun_out/pmc_v2/run_counter_collection.csv "
+        "gpurun_out/pmc_v2/run_kernel_trace.csv",
+        "```",
+        "",
+        "Shapes: 8192^3 NT, 8192x4096x4096 NT (the step's forward layout), dW = dZ^T.H with K = 8192 "
+        "(fp32 out for ours, bf16 for hipBLASLt).  clock = GRBM_GUI_ACTIVE per XCD / duration; MFMA busy = "
+        "SQ_VALU_MFMA_BUSY_CYCLES / (GUI cycles per XCD x 1024 SIMDs); per-GFLOP columns divide by the "
+        "flops the MFMA counter saw (SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512).  LDS conflict = "
+        "SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE; TA / TD busy = busy cycles summed over the 256 CUs' units "
+        "/ (GUI cycles per XCD x 256); waits = SQ_WAIT_* / SQ_WAVE_CYCLES.",
+        "",
+        "| kernel | grid | n | us | GHz | MFMA busy | TF/s | LDS instr /GF | LDS conflict | VMEM rd /GF | "
+        "VMEM wr /GF | SALU /GF | VALU /GF | TA busy | TD busy | TCP acc /GF | TCC rd req /GF | wait LDS | "
+        "wait any |",
+        "|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|",
+    ]
+    for key, m in p1.items():
+        name, grid = key
+        gui = m["GRBM_GUI_ACTIVE"] / 8.0
+        us = m["_us"]
+        gf = m["SQ_INSTS_VALU_MFMA_MOPS_BF16"] * 512.0 / 1e9
+        q = p2.get(key, {})
+        gui2 = q.get("GRBM_GUI_ACTIVE", 0.0) / 8.0
+        wave = q.get("SQ_WAVE_CYCLES", 0.0)
+
+        def per(v):
+            return f"{v / gf:.0f}" if gf else "-"
+
+        def frac(v, den):
+            return f"{v / den * 100:.1f}%" if den else "-"
+
+        lines.append(
+            f"| `{name}` | {grid} | {m['_n']} | {us:.1f} | {gui / (us * 1e-6) / 1e9:.2f} | "
+            f"{frac(m['SQ_VALU_MFMA_BUSY_CYCLES'], gui * 1024.0)} | {gf * 1e9 / (us * 1e-6) / 1e12:.0f} | "
+            f"{per(m['SQ_INSTS_LDS'])} | {frac(m['SQ_LDS_BANK_CONFLICT'], m['SQ_LDS_IDX_ACTIVE'])} | "
+            f"{per(m['SQ_INSTS_VMEM_RD'])} | {per(m['SQ_INSTS_VMEM_WR'])} | {per(m['SQ_INSTS_SALU'])} | "
+            f"{per(q.get('SQ_INSTS_VALU', 0.0)) if q else '-'} | "
+            f"{frac(q.get('TA_TA_BUSY_sum', 0.0), gui2 * 256.0)} | {frac(q.get('TD_TD_BUSY_sum', 0.0), gui2 * 256.0)} | "
+            f"{per(q.get('TCP_TOTAL_CACHE_ACCESSES_sum', 0.0)) if q else '-'} | "
+            f"{per(q.get('TCP_TCC_READ_REQ_sum', 0.0)) if q else '-'} | "
+            f"{frac(q.get('SQ_WAIT_INST_LDS', 0.0), wave)} | {frac(q.get('SQ_WAIT_ANY', 0.0), wave)} |")
+    lines.append("")
+    print("\n".join(lines))
+
+
 def pmc_report(fetch_csv, write_csv, mfma_csv=None, trace_csv=None):
     """Markdown summary of two rocprofv3 --pmc runs of --roofline-only
     (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch), per GEMM role of the step
@@ -908,6 +1014,8 @@ def pmc_report(fetch_csv, write_csv, mfma_csv=None, trace_csv=None):
 # algorithmic bytes per dispatch).  Shapes follow the benchmark configs.
 SR, SC = 16384, 32768
 STREAMING = [
+    ("row softmax (+max, +sum) 16384x1024 f32", "row_reg_kernel<128, 2, 0>", 8 * SR * 1024 + 8 * SR),
+    ("row softmax (+max, +sum) 16384x8192 f32", "row_reg_kernel<512, 4, 0>", 8 * SR * 8192 + 8 * SR),
     ("row softmax (+max, +sum) 16384x32768 f32", "row_reg_kernel<512, 16, 0>", 8 * SR * SC + 8 * SR),
     ("row sum 16384x32768 f32", "row_reg_kernel<512, 16, 1>", 4 * SR * SC + 4 * SR),
     ("row max 16384x32768 f32", "row_reg_kernel<512, 16, 2>", 4 * SR * SC + 4 * SR),
@@ -926,6 +1034,13 @@ def streaming_only(C):
 
     g = torch.Generator(device="cuda")
     g.manual_seed(8)
+    for cols in (1024, 8192):
+        xs = torch.randn((SR, cols), device="cuda", generator=g) * 2.0
+        ys = torch.empty_like(xs)
+        mxs, sms = torch.empty(SR, device="cuda"), torch.empty(SR, device="cuda")
+        for _ in range(3):
+            C.op_call(int(C.OpKind.RowSoftmax), [xs], [ys, mxs, sms], 0, b"", 0)
+        del xs, ys
     x = torch.randn((SR, SC), device="cuda", generator=g) * 2.0
     y = torch.empty_like(x)
     mx, sm = torch.empty(SR, device="cuda"), torch.empty(SR, device="cuda")
@@ -966,7 +1081,7 @@ def streaming_only(C):
     for _ in range(3):
         C.launch_by_id("copy_bf16_v0", C.OpKind.Copy, [xc], [yc], 0, b"")
     torch.cuda.synchronize()
-    log("[bench] streaming-only: 7 kernels x 3 dispatches, 3 calibration copies")
+    log("[bench] streaming-only: 9 kernels x 3 dispatches, 3 calibration copies")
 
 
 def pmc_streaming_report(fetch_csv, write_csv):
@@ -1053,9 +1168,9 @@ def stats_report(stats_csv, trace_csv, steps):
         f"Process contents: warmup + {steps} timed replays of the captured step (batch 8192, 4 x 4096^2, "
         "GELU, MSE, AdamW in the dW GEMMs' epilogue), then the roofline measurement: one eager pass "
         "over the step and 12 launches of each of its 12 GEMM ops.",
-        "`gemm_nt_kernel<IN, OUT, ACT, BM, BN, WM, WN, AKC, BKC>`: IN 2 = bf16; OUT 2 = bf16, 0 = fp32; "
+        "`gemm_nt_kernel<IN, OUT, ACT, BM, BN, WM, WN, AKC, BKC, S>`: IN 2 = bf16; OUT 2 = bf16, 0 = fp32; "
         "ACT 0 none, 2 GELU (+ pre-activation store), 3 dGELU, 4 AdamW; WM x WN waves; AKC/BKC operand "
-        "K-contiguous (false: M/N-contiguous, read in place through transposing LDS reads).",
+        "K-contiguous (false: M/N-contiguous, read in place through transposing LDS reads); S LDS stages.",
         "",
         "| kernel | calls | avg us | % time |",
         "|---|---:|---:|---:|",
@@ -1087,6 +1202,61 @@ def stats_report(stats_csv, trace_csv, steps):
         if g_roof:
             lines.append(f"GEMM launches after the replays (roofline measurement): {len(g_roof)}, mean "
                          f"{sum(g_roof) / len(g_roof):.1f} us.")
+    lines.append("")
+    print("\n".join(lines))
+
+
+def c1_trace_report(stats_csv, trace_csv):
+    """Markdown summary of `rocprofv3 --kernel-trace --stats` over
+    `bench.py --c1-only`: per-kernel totals, then the last replayed step of
+    the four-launch lowering and of the reference's 17-op lowering, launch by
+    launch."""
+    import csv
+
+    with open(stats_csv, newline="") as f:
+        stats = list(csv.DictReader(f))
+    with open(trace_csv, newline="") as f:
+        trace = sorted(csv.DictReader(f), key=lambda r: int(r["Start_Timestamp"]))
+    short = lambda n: n.replace("aicf::hip::(anonymous namespace)::", "").split("(")[0][:80]  # noqa: E731
+    us = lambda r: (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3  # noqa: E731
+    lines = [
+        "# Kernel time summary: C1, the reference MLP step (batch 64, 784 -> 256 ReLU -> 10, softmax "
+        "cross-entropy, Adam), hipGraph replay",
+        "",
+        "Command (repo root, one MI355X):",
+        "",
+        "```",
+        "rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/c1prof -o c1 -- python3 -u bench.py "
+        "--c1-only",
+        "python3 bench.py --c1-trace-report gpurun_out/c1prof/c1_kernel_stats.csv "
+        "gpurun_out/c1prof/c1_kernel_trace.csv",
+        "```",
+        "",
+        "Process contents: 5 warmup + 50 timed replays of the four-launch step (StageF), then the same for "
+        "the reference pipeline's 17-op lowering.",
+        "",
+        "| kernel | calls | avg us | % time |",
+        "|---|---:|---:|---:|",
+    ]
+    for r in stats[:20]:
+        lines.append(f"| `{short(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
+                     f"{float(r['Percentage']):.2f} |")
+    fused_end = [i for i, r in enumerate(trace) if "adamw_multi" in r["Kernel_Name"]]
+    # the reference lowering's step ends with its four adamw_step launches
+    ktr = [r for r in trace if "copyBuffer" not in r["Kernel_Name"]]
+    ad = [i for i, r in enumerate(ktr) if "adamw_vec4" in r["Kernel_Name"]
+          and (i + 1 == len(ktr) or "adamw_vec4" not in ktr[i + 1]["Kernel_Name"])]
+    ref_step = ktr[ad[-2] + 1:ad[-1] + 1] if len(ad) >= 2 else []
+    for title, step in (("four-launch lowering", trace[fused_end[-1] - 3:fused_end[-1] + 1] if fused_end else []),
+                        ("reference 17-op lowering", ref_step)):
+        if not step:
+            continue
+        t0, t1 = int(step[0]["Start_Timestamp"]), int(step[-1]["End_Timestamp"])
+        lines += ["", f"Last replayed step of the {title} ({len(step)} kernels, first start to last end "
+                  f"{(t1 - t0) / 1e3:.1f} us, kernels busy {sum(us(r) for r in step):.1f} us):", "",
+                  "| # | kernel | us |", "|---:|---|---:|"]
+        for i, r in enumerate(step):
+            lines.append(f"| {i} | `{short(r['Kernel_Name'])}` | {us(r):.2f} |")
     lines.append("")
     print("\n".join(lines))
 
@@ -1124,8 +1294,13 @@ def main():
                     help="summarise a rocprofv3 --kernel-trace --stats run of the step and exit")
     ap.add_argument("--vendor-compare", action="store_true",
                     help="our GEMM and torch.matmul on the same shapes (for rocprofv3 --pmc)")
+    ap.add_argument("--pmc-compare-report", nargs=4, metavar="CSV",
+                    help="per-flop counter comparison of --vendor-compare (two passes: counter, trace each)")
     ap.add_argument("--pmc-mfma-compare-report", nargs=2, metavar=("COUNTER_CSV", "TRACE_CSV"),
                     help="summarise a rocprofv3 MFMA-counter run of --vendor-compare and exit")
+    ap.add_argument("--c1-trace-report", nargs=2, metavar=("STATS_CSV", "TRACE_CSV"))
+    ap.add_argument("--c1-only", action="store_true",
+                    help="the C1 step (reference MLP) replayed, both lowerings; the program of the C1 trace")
     ap.add_argument("--streaming-only", action="store_true",
                     help="run each streaming kernel at its benchmark shape (for rocprofv3 --pmc)")
     ap.add_argument("--pmc-streaming-report", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -1136,6 +1311,12 @@ def main():
         return
     if args.pmc_mfma_compare_report:
         pmc_mfma_compare_report(*args.pmc_mfma_compare_report)
+        return
+    if args.pmc_compare_report:
+        pmc_compare_report(*args.pmc_compare_report)
+        return
+    if args.c1_trace_report:
+        c1_trace_report(*args.c1_trace_report)
         return
     if args.stats_report:
         stats_report(args.stats_report[0], args.stats_report[1], int(args.stats_report[2]))
@@ -1160,6 +1341,9 @@ def main():
         return
     if args.streaming_only:
         streaming_only(C)
+        return
+    if args.c1_only:
+        print(json.dumps({"four_launch": bench_c1(steps=50), "reference_lowering": bench_c1(steps=50, fuse_small=False)}))
         return
     if args.vendor_compare:
         vendor_compare(C)
