@@ -139,9 +139,11 @@ def bench_c4(C, dtype="bf16", shapes=C4_SHAPES, acts=("none", "relu", "gelu"), i
         flops = 2.0 * M * N * K
         for act in acts:
             pay = struct.pack("<iii", 0, 1, C4_ACTS[act])
-            fn = lambda: C.launch_by_id(kid, C.OpKind.GemmEpilogue, [X, W, b], [Y], GEPI, pay)  # noqa: E731
+            fn = lambda: C.launch_by_id(kid, C.OpKind.GemmEpilogue, [X, W, b], [Y], GEPI, pay,  # noqa: E731
+                                        _cs())
             n = iters if flops < 1e12 else max(3, iters // 2)
-            ms = time_launches(fn, n, 2)
+            # small shapes run for a few microseconds: time them from a captured graph
+            ms = time_launches(fn, n, 2, graph=flops < 1e11)
             tf = flops / (ms * 1e-3) / 1e12
             peak = PEAK_BF16_TFLOPS if dtype == "bf16" else PEAK_FP32_TFLOPS
             out[f"c4_{dtype}_{M}x{N}x{K}_{act}"] = {"value": round(tf, 2), "unit": "TFLOP/s",
