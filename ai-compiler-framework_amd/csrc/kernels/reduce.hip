@@ -396,14 +396,11 @@ __global__ __launch_bounds__(LPR >= 256 ? LPR : 256) void row_reg_kernel(RowArgs
   // cross-entropy: the label is read first, so its latency hides behind the row loads
   const int lab = (MODE == MODE_XENT && active) ? a.labels[row] : -1;
 
+  // an inactive row (past R, uniform across its lanes) reads row 0 and
+  // stores nothing: the loads need no predicate
   f32x4 v[VPT];
 #pragma unroll
-  for (int k = 0; k < VPT; ++k) {
-    if (active)
-      v[k] = __builtin_nontemporal_load(xr + k * LPR + l);
-    else
-      v[k] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
+  for (int k = 0; k < VPT; ++k) v[k] = __builtin_nontemporal_load(xr + k * LPR + l);
 
   // this lane's statistics
   RowStat st{v[0][0], 0.0f, 0.0f, l * 4};
