@@ -408,18 +408,31 @@ __global__ __launch_bounds__(LPR >= 256 ? LPR : 256) void row_reg_kernel(RowArgs
 #pragma unroll
     for (int k = 0; k < VPT; ++k) st.sx += (v[k][0] + v[k][1]) + (v[k][2] + v[k][3]);
   }
+  // cross-entropy: the label's logit sits in lane lab_l, vector lab_k,
+  // element lab & 3 (no lane for a label outside [0, C))
+  const int lab_q = lab >> 2;
+  const bool lab_here = MODE == MODE_XENT && lab >= 0 && lab_q % LPR == l;
+  const int lab_k = lab_q / LPR, lab_j = lab & 3;
   if constexpr (MODE == MODE_XENT) {
+    // the lane's maximum, then the first column holding it (for finite
+    // values the result of a running strict-greater scan), then the
+    // label's logit by a uniform pick instead of a compare per element
+    float m = v[0][0];
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) m = fmaxf(m, fmaxf(fmaxf(v[k][0], v[k][1]), fmaxf(v[k][2], v[k][3])));
+    int idx = l * 4;
+#pragma unroll
+    for (int k = VPT - 1; k >= 0; --k)
+#pragma unroll
+      for (int j = 3; j >= 0; --j) idx = v[k][j] == m ? (k * LPR + l) * 4 + j : idx;
+    float zl = 0.0f;
 #pragma unroll
     for (int k = 0; k < VPT; ++k)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int col = (k * LPR + l) * 4 + j;
-        if (v[k][j] > st.m) {
-          st.m = v[k][j];
-          st.i = col;
-        }
-        if (col == lab) st.sx = v[k][j];
-      }
+      for (int j = 0; j < 4; ++j) zl = (lab_here && k == lab_k && j == lab_j) ? v[k][j] : zl;
+    st.m = m;
+    st.i = idx;
+    st.sx = zl;
   } else if constexpr (MODE != MODE_SUM) {
 #pragma unroll
     for (int k = 0; k < VPT; ++k) st.m = fmaxf(st.m, fmaxf(fmaxf(v[k][0], v[k][1]), fmaxf(v[k][2], v[k][3])));
@@ -486,10 +499,8 @@ __global__ __launch_bounds__(LPR >= 256 ? LPR : 256) void row_reg_kernel(RowArgs
     for (int k = 0; k < VPT; ++k) {
       f32x4 o;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int col = (k * LPR + l) * 4 + j;
-        o[j] = (v[k][j] * c - (col == lab ? 1.0f : 0.0f)) * sc;
-      }
+      for (int j = 0; j < 4; ++j)  // (p - onehot) / B
+        o[j] = (v[k][j] * c - ((lab_here && k == lab_k && j == lab_j) ? 1.0f : 0.0f)) * sc;
       __builtin_nontemporal_store(o, yr + k * LPR + l);
     }
     if (l == 0) {

@@ -57,8 +57,8 @@ struct SgJob {
   int tn;          // tiles along N
   int tiles;       // tiles along M times tn
   int kb;          // 16-K blocks
-  int splits;      // waves per tile (K split): 1, 2 or 4
-  int tpb;         // tiles per workgroup: 4 / splits
+  int splits;      // waves per tile (K split): 1, 2, 4 or 8
+  int tpb;         // tiles per workgroup: waves / splits
   int avec, bvec;  // 16-byte loads along K (K-contiguous, aligned operand)
 };
 
@@ -119,9 +119,9 @@ __device__ __forceinline__ void sg_store(const SmallGemm& g, int64_t m0, int64_t
   }
 }
 
-// Workgroup `blk` of a small GEMM: 4 waves = tpb tiles x splits K parts.
-// The parts of a tile are summed in split order (part 0 + 1 + 2 + 3).
-// `red` is 256 f32x4 of LDS.  Every thread reaches the barrier.
+// Workgroup `blk` of a small GEMM: its waves = tpb tiles x splits K parts.
+// The parts of a tile are summed in split order (part 0 + 1 + 2 + ...).
+// `red` is 64 f32x4 of LDS per wave.  Every thread reaches the barrier.
 __device__ __forceinline__ void sg_block(const SgJob& j, int blk, f32x4* red) {
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int tile = blk * j.tpb + w / j.splits;
@@ -142,19 +142,23 @@ __device__ __forceinline__ void sg_block(const SgJob& j, int blk, f32x4* red) {
   sg_store(j.g, m0, n0, lane, acc);
 }
 
-__global__ __launch_bounds__(256) void gemm_small_kernel(SgJob j) {
-  __shared__ f32x4 red[256];
+template <int NWAVE>
+__global__ __launch_bounds__(64 * NWAVE) void gemm_small_kernel(SgJob j) {
+  __shared__ f32x4 red[64 * NWAVE];
   sg_block(j, blockIdx.x, red);
 }
 
-SgJob sg_plan(const SmallGemm& g) {
+// nwave 4, or 8 for the standalone kernel when K is long enough for 8 splits
+// (32 or more K blocks): each wave then has at most 8 blocks, one batch of
+// loads in flight.
+SgJob sg_plan(const SmallGemm& g, int nwave = 4) {
   SgJob j{};
   j.g = g;
   j.tn = (int)((g.N + 15) / 16);
   j.tiles = (int)((g.M + 15) / 16) * j.tn;
   j.kb = (int)((g.K + 15) / 16);
-  j.splits = j.kb >= 16 ? 4 : j.kb >= 8 ? 2 : 1;
-  j.tpb = 4 / j.splits;
+  j.splits = (nwave == 8 && j.kb >= 32) ? 8 : j.kb >= 16 ? 4 : j.kb >= 8 ? 2 : 1;
+  j.tpb = nwave / j.splits;
   j.avec = g.a_k == 1 && g.K % 4 == 0 && (g.M == 1 || g.a_m % 4 == 0) && aligned(g.A, 16);
   j.bvec = g.b_k == 1 && g.K % 4 == 0 && (g.N == 1 || g.b_n % 4 == 0) && aligned(g.B, 16);
   return j;
@@ -742,8 +746,14 @@ bool small_gemm_ok(const SmallGemm& g) {
 
 Status small_gemm_f32(const SmallGemm& g, hipStream_t s) {
   if (!small_gemm_ok(g)) return Status::InvalidArgument;
-  const SgJob j = sg_plan(g);
-  gemm_small_kernel<<<(unsigned)sg_blocks(j), 256, 0, s>>>(j);
+  const int kb = (int)((g.K + 15) / 16);
+  if (kb >= 32) {  // long K: eight waves split it
+    const SgJob j = sg_plan(g, 8);
+    gemm_small_kernel<8><<<(unsigned)sg_blocks(j), 512, 0, s>>>(j);
+  } else {
+    const SgJob j = sg_plan(g);
+    gemm_small_kernel<4><<<(unsigned)sg_blocks(j), 256, 0, s>>>(j);
+  }
   return launch_status("gemm_small");
 }
 
