@@ -59,6 +59,8 @@ enum class OpKind : int {
   XentHead = AICF_OP_XENT_HEAD,
   GradGroup = AICF_OP_GRAD_GROUP,
   AdamWMulti = AICF_OP_ADAMW_MULTI,
+  MseColsum = AICF_OP_MSE_COLSUM,
+  ColsumAdamW = AICF_OP_COLSUM_ADAMW,
 };
 
 std::string tensor_brief(const torch::Tensor& t) {
@@ -235,6 +237,8 @@ PYBIND11_MODULE(_C, m) {
       .value("XentHead", OpKind::XentHead)
       .value("GradGroup", OpKind::GradGroup)
       .value("AdamWMulti", OpKind::AdamWMulti)
+      .value("MseColsum", OpKind::MseColsum)
+      .value("ColsumAdamW", OpKind::ColsumAdamW)
       .export_values();
 
   m.def(

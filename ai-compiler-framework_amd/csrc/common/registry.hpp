@@ -67,6 +67,8 @@ enum class OpKind : int {
   XentHead = AICF_OP_XENT_HEAD,
   GradGroup = AICF_OP_GRAD_GROUP,
   AdamWMulti = AICF_OP_ADAMW_MULTI,
+  MseColsum = AICF_OP_MSE_COLSUM,
+  ColsumAdamW = AICF_OP_COLSUM_ADAMW,
   _Count = AICF_OP_COUNT,
 };
 

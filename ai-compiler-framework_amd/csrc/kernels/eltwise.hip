@@ -720,6 +720,194 @@ Status mse_loss_launch(const TensorDesc* in, int ni, TensorDesc* out, int no, co
 }
 
 // ---------------------------------------------------------------------------
+// MSE loss + gradient + the gradient's column partial sums + the step
+// counter in one pass (no reference counterpart: the loss tail of the MLP
+// step, where the reference runs mse_grad, reduce_sum(axis 0) over the
+// gradient for the last bias and step_inc).  inputs (pred [M, N] f32|bf16,
+// target f32, step i32), outputs (dPred, loss f32, loss partials f32
+// [>= blocks], column partials f32 [P, N], step (in place)).  Attr MSCS
+// <f scale, i inc>: dPred = (pred - target) * scale (scale <= 0 or no attr:
+// 2/n), step += inc (0 or 1; default 1).
+// Rows go in P blocks of M / P; within a block the four waves stride the
+// rows, each lane holds 16 bytes of pred columns, and the waves are combined
+// (w0 + w1) + (w2 + w3): the column sums the two-pass column-sum kernel
+// takes of the stored gradient with the same [P, N] workspace, bit for bit.
+// The loss partials (one per workgroup) are summed by the second pass of
+// the MSE loss.
+// ---------------------------------------------------------------------------
+constexpr int kMseColsumVecBf16 = 8;
+constexpr int kMseColsumUnroll = 2;
+
+template <bool BF16, int VEC, int UNROLL>
+__global__ __launch_bounds__(256) void mse_colsum_kernel(const void* __restrict__ pred,
+                                                         const float* __restrict__ tgt,
+                                                         void* __restrict__ dpred, float* __restrict__ lpart,
+                                                         float* __restrict__ cpart, int32_t* __restrict__ step,
+                                                         int inc, int64_t M, int64_t N, int64_t rpp,
+                                                         float scale) {
+  // VEC columns per lane, CB per workgroup, UNROLL rows in flight per lane
+  static_assert(VEC == 4 || (BF16 && VEC == 8), "4 or 8 columns per lane");
+  constexpr int CB = 64 * VEC;
+  __shared__ float red[4][CB];
+  __shared__ float lred[4];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t c0 = (int64_t)blockIdx.x * CB + lane * VEC;
+  const int64_t r0 = (int64_t)blockIdx.y * rpp;
+  const int64_t r1 = r0 + rpp < M ? r0 + rpp : M;
+  if (inc && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) step[0] += 1;
+  float acc[VEC], sq = 0.0f;
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) acc[e] = 0.0f;
+  // one row: gradient stored, its stored value added to the column sums
+  auto row = [&](int64_t r, const float (&pv)[VEC], const float (&tv)[VEC]) {
+    float d[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float x = pv[e] - tv[e];
+      sq = fmaf(x, x, sq);
+      d[e] = x * scale;
+    }
+    if constexpr (BF16) {
+      using V = std::conditional_t<VEC == 8, u16x8, u16x4>;
+      V o;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        o[e] = f32_to_bf16(d[e]);
+        acc[e] += bf16_to_f32(o[e]);
+      }
+      __builtin_nontemporal_store(o, reinterpret_cast<V*>((uint16_t*)dpred + r * N + c0));
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[e] += d[e];
+      __builtin_nontemporal_store(f32x4{d[0], d[1], d[2], d[3]},
+                                  reinterpret_cast<f32x4*>((float*)dpred + r * N + c0));
+    }
+  };
+  auto load = [&](int64_t r, float (&pv)[VEC], float (&tv)[VEC]) {
+    const float* t = tgt + r * N + c0;
+    if constexpr (BF16) {
+      using V = std::conditional_t<VEC == 8, u16x8, u16x4>;
+      const V pb = __builtin_nontemporal_load(reinterpret_cast<const V*>((const uint16_t*)pred + r * N + c0));
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) pv[e] = bf16_to_f32(pb[e]);
+#pragma unroll
+      for (int h = 0; h < VEC / 4; ++h) {
+        const f32x4 tt = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(t) + h);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) tv[4 * h + e] = tt[e];
+      }
+    } else {
+      const f32x4 p0 = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>((const float*)pred + r * N + c0));
+      const f32x4 t0 = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(t));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        pv[e] = p0[e];
+        tv[e] = t0[e];
+      }
+    }
+  };
+  if (c0 < N) {  // N % VEC == 0: the lane's columns are all in range
+    int64_t r = r0 + w;
+    for (; r + (UNROLL - 1) * 4 < r1; r += UNROLL * 4) {
+      float pv[UNROLL][VEC], tv[UNROLL][VEC];
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) load(r + u * 4, pv[u], tv[u]);
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) row(r + u * 4, pv[u], tv[u]);
+    }
+    for (; r < r1; r += 4) {
+      float pv[VEC], tv[VEC];
+      load(r, pv, tv);
+      row(r, pv, tv);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) red[w][lane * VEC + e] = acc[e];
+  sq = wave_sum(sq);
+  if (lane == 0) lred[w] = sq;
+  __syncthreads();
+  for (int cc = threadIdx.x; cc < CB; cc += 256) {
+    const int64_t col = (int64_t)blockIdx.x * CB + cc;
+    if (col < N) cpart[(int64_t)blockIdx.y * N + col] = (red[0][cc] + red[1][cc]) + (red[2][cc] + red[3][cc]);
+  }
+  if (threadIdx.x == 0)
+    lpart[(int64_t)blockIdx.y * gridDim.x + blockIdx.x] = (lred[0] + lred[1]) + (lred[2] + lred[3]);
+}
+
+struct MscsAttr {
+  float scale = 0.0f;  // <= 0: 2/n
+  int inc = 1;
+  bool ok = true;
+};
+MscsAttr read_mscs(const void* attr) {
+  MscsAttr m;
+  if (!attr) return m;
+  const AttrBlob& a = blob(attr);
+  if (a.schema_id == 0 && a.bytes == 0) return m;
+  if (a.schema_id != AICF_SCHEMA_MSCS || !payload_ok(a, 8)) {
+    m.ok = false;
+    return m;
+  }
+  m.scale = field<float>(a, 0);
+  m.inc = field<int32_t>(a, 4);
+  if (m.scale != m.scale || (m.inc != 0 && m.inc != 1)) m.ok = false;
+  return m;
+}
+
+bool mse_colsum_check(const TensorDesc* in, int ni, const TensorDesc* out, int no, const void* attr) {
+  if (!in || !out || ni != 3 || no != 5) return false;
+  if (!read_mscs(attr).ok) return false;
+  const TensorDesc &P = in[0], &T = in[1], &S = in[2];
+  const TensorDesc &G = out[0], &L = out[1], &LP = out[2], &CP = out[3], &S2 = out[4];
+  if (dt(P) != DType::kF32 && dt(P) != DType::kBF16) return false;
+  const bool bf = dt(P) == DType::kBF16;
+  if (dt(T) != DType::kF32 || dt(G) != dt(P)) return false;
+  for (const TensorDesc* t : {&P, &T, &G})
+    if (!t->contiguous || t->rank != 2) return false;
+  if (!same_shape(P, T) || !same_shape(P, G)) return false;
+  const int64_t M = P.shape[0], N = P.shape[1];
+  const int VEC = bf ? kMseColsumVecBf16 : 4;
+  if (M < 1 || N < 1 || N % VEC) return false;
+  if (dt(S) != DType::kI32 || numel_of(S) != 1 || S2.data != S.data || dt(S2) != DType::kI32) return false;
+  if (dt(L) != DType::kF32 || numel_of(L) != 1) return false;
+  if (dt(CP) != DType::kF32 || !CP.contiguous || CP.rank != 2 || CP.shape[1] != N) return false;
+  const int64_t parts = CP.shape[0];
+  if (parts < 1 || M % parts) return false;  // every partial row covers M / P rows
+  const int64_t gx = (N + 64 * VEC - 1) / (64 * VEC);
+  if (gx * parts > INT32_MAX || parts > 65535) return false;
+  if (dt(LP) != DType::kF32 || !LP.contiguous || numel_of(LP) < gx * parts) return false;
+  return aligned(P.data, 16) && aligned(G.data, 16) && aligned(T.data, 16);
+}
+bool mse_colsum_sup(const TensorDesc* i, int ni, const TensorDesc* o, int no, const void* a) {
+  return mse_colsum_check(i, ni, o, no, a);
+}
+Status mse_colsum_launch(const TensorDesc* in, int ni, TensorDesc* out, int no, const void* a, void*,
+                         size_t, void* stream) {
+  if (!mse_colsum_check(in, ni, out, no, a)) return Status::InvalidArgument;
+  const MscsAttr m = read_mscs(a);
+  hipStream_t s = as_stream(stream);
+  const bool bf = dt(in[0]) == DType::kBF16;
+  const int64_t M = in[0].shape[0], N = in[0].shape[1], n = M * N;
+  const int64_t parts = out[3].shape[0], rpp = M / parts;
+  const float sc = m.scale > 0.0f ? m.scale : 2.0f / (float)n;
+  constexpr int VB = kMseColsumVecBf16;  // bf16 columns per lane
+  const int vec = bf ? VB : 4;
+  const unsigned gx = (unsigned)((N + 64 * vec - 1) / (64 * vec));
+  const dim3 grid(gx, (unsigned)parts);
+  float* lp = (float*)out[2].data;
+  if (bf)
+    mse_colsum_kernel<true, VB, kMseColsumUnroll><<<grid, 256, 0, s>>>(
+        in[0].data, (const float*)in[1].data, out[0].data, lp, (float*)out[3].data, (int32_t*)in[2].data, m.inc,
+        M, N, rpp, sc);
+  else
+    mse_colsum_kernel<false, 4, kMseColsumUnroll><<<grid, 256, 0, s>>>(
+        in[0].data, (const float*)in[1].data, out[0].data, lp, (float*)out[3].data, (int32_t*)in[2].data, m.inc,
+        M, N, rpp, sc);
+  mse_loss_grad_pass2<<<1, 1024, 0, s>>>(lp, (int)(gx * parts), (float*)out[1].data, 1.0 / (double)n);
+  return launch_status("mse_colsum_v0");
+}
+
+// ---------------------------------------------------------------------------
 // gelu (tanh) forward and backward, f32 and bf16 storage, fp32 math.
 //   gelu:     X -> Y
 //   gelu_bwd: (dOut, Z) -> dZ = dOut * gelu'(Z)
@@ -894,6 +1082,9 @@ KernelVariant make_mse_grad_f16_variant() {
 }
 KernelVariant make_mse_loss_grad_variant() {
   return make("mse_loss_grad", mse_loss_launch, mse_loss_sup);
+}
+KernelVariant make_mse_colsum_variant() {
+  return make("mse_colsum", mse_colsum_launch, mse_colsum_sup);
 }
 KernelVariant make_gelu_f32_variant() { return make("gelu_f32", gelu_f32_launch, gelu_f32_sup); }
 KernelVariant make_gelu_bf16_variant() {

@@ -1317,7 +1317,7 @@ EpiAttr read_epi_attr(const void* attr) {
   return e;
 }
 
-bool epi_kind_valid(int k) { return k >= AICF_EPI_BIAS_RELU && k <= AICF_EPI_DGELU_COLSUM; }
+bool epi_kind_valid(int k) { return k >= AICF_EPI_BIAS_RELU && k <= AICF_EPI_DGELU_PARTIALS; }
 
 // gemm/launcher.cu:116-148: A[M,K] . B[K,N] -> C[M,N] with positive strides.
 bool gemm_views_ok(const TensorDesc& A0, const TensorDesc& B0, const TensorDesc& C0, bool ta,
@@ -1636,16 +1636,19 @@ bool epi_check(const TensorDesc* in, int ni, const TensorDesc* out, int no, cons
   if (c_rowmajor && !is_contig_2d_rowmajor(out[0])) return false;
   const View2D C = view2d(out[0], false);
   const TensorDesc& X = in[2];
-  if (e.kind == AICF_EPI_DGELU_COLSUM) {
-    // outputs (C, db [N] f32, workspace [P >= M/256, N] f32), bf16 output
-    if (no != 3 || dout != DType::kBF16 || !is_contig_2d_rowmajor(out[0])) return false;
+  if (e.kind == AICF_EPI_DGELU_COLSUM || e.kind == AICF_EPI_DGELU_PARTIALS) {
+    // outputs (C, db [N] f32, workspace [P >= M/256, N] f32), or (C,
+    // partials [P >= M/256, N] f32); bf16 output
+    const bool fin = e.kind == AICF_EPI_DGELU_COLSUM;
+    if (no != (fin ? 3 : 2) || dout != DType::kBF16 || !is_contig_2d_rowmajor(out[0])) return false;
     if (dt(X) != dout || X.rank != 2 || X.shape[0] != C.rows || X.shape[1] != C.cols) return false;
     if (X.stride[1] != 1 || X.stride[0] <= 0) return false;
-    const TensorDesc &D = out[1], &W = out[2];
-    if (dt(D) != DType::kF32 || !D.contiguous || D.rank != 1 || D.shape[0] != C.cols) return false;
+    const TensorDesc &D = out[1], &W = out[fin ? 2 : 1];
+    if (fin && (dt(D) != DType::kF32 || !D.contiguous || D.rank != 1 || D.shape[0] != C.cols)) return false;
     if (dt(W) != DType::kF32 || !W.contiguous || W.rank != 2 || W.shape[1] != C.cols ||
         W.shape[0] < C.rows / 256)
       return false;
+    if (!fin && W.shape[0] != C.rows / 256) return false;  // its reader sums every row
     // only the bf16 256 x 256-tile path carries the column sums: accept
     // exactly the calls it runs (M, N multiples of 256, so the workspace
     // has at least one row; K of 64; aligned operands)
@@ -1691,6 +1694,7 @@ Status epi_launch_common(const TensorDesc* in, int no, TensorDesc* out, const vo
     case AICF_EPI_GELU: p.act = ACT_GELU; break;
     case AICF_EPI_DGELU: p.act = ACT_DGELU; break;
     case AICF_EPI_DGELU_COLSUM: p.act = ACT_DGELU; break;
+    case AICF_EPI_DGELU_PARTIALS: p.act = ACT_DGELU; break;
   }
   const bool with_bias = e.kind == AICF_EPI_BIAS_RELU || e.kind == AICF_EPI_BIAS ||
                          e.kind == AICF_EPI_BIAS_GELU;
@@ -1699,12 +1703,16 @@ Status epi_launch_common(const TensorDesc* in, int no, TensorDesc* out, const vo
     p.bias_s = X.stride[0];
     p.bias_f32 = dt(X) == DType::kF32 ? 1 : 0;
   }
-  if (e.kind == AICF_EPI_DGELU || e.kind == AICF_EPI_DGELU_COLSUM) {
+  if (e.kind == AICF_EPI_DGELU || e.kind == AICF_EPI_DGELU_COLSUM || e.kind == AICF_EPI_DGELU_PARTIALS) {
     p.aux = const_cast<void*>(X.data);
     p.aux_rs = X.stride[0];
   } else if (no == 2) {
     p.aux = out[1].data;
     p.aux_rs = out[1].stride[0];
+  }
+  if (e.kind == AICF_EPI_DGELU_PARTIALS) {  // the column sums are finished by a later op
+    p.colsum = (float*)out[1].data;
+    return dispatch_gemm(p, din, dout, as_stream(stream));
   }
   if (e.kind == AICF_EPI_DGELU_COLSUM) {
     p.colsum = (float*)out[2].data;

@@ -519,6 +519,164 @@ KernelVariant make(const char* name, LaunchFn l, SupportedFn s, uint32_t schema 
   return v;
 }
 
+// ---------------------------------------------------------------------------
+// colsum_adamw (no reference counterpart): the bias tail of the MLP step.
+// inputs (C_0 .. C_{T-1} column partials f32 [R_t, N_t], P, M, V f32 [n],
+// step i32), outputs (G f32 [n], P, M, V in place, Wb bf16 [n]) with
+// n = sum N_t.  Element j of tensor t's range (offset o_t = N_0 + .. +
+// N_{t-1}) gets g = the sum over r of C_t[r][j - o_t], taken in the order of
+// the column-sum finish kernel (four row strides of 4, combined
+// (s0 + s1) + (s2 + s3)), so g equals that kernel's output bit for bit; g
+// is stored in G and AdamW (adamw.hpp) is applied to P[j], M[j], V[j] with
+// it, bf16(P[j]) stored in Wb.  Attr CADW <i fffff>: T, lr, b1, b2, eps, wd.
+// ---------------------------------------------------------------------------
+constexpr int kColsumAdamMax = 8;
+
+struct ColsumAdamWParams {
+  const float* part[kColsumAdamMax];
+  int64_t rows[kColsumAdamMax];
+  int64_t cols[kColsumAdamMax];
+  int64_t off[kColsumAdamMax + 1];
+  int T;
+  int64_t n;
+  float* G;
+  float* P;
+  float* M;
+  float* V;
+  uint16_t* Wb;
+  const int32_t* step;
+  AdamWArgs a;
+};
+
+// 64 elements per workgroup: wave w sums rows w, w + 4, .. of the element's
+// partials (16 rows at a time as (a0 + a1) + (a2 + a3)), the four sums are
+// combined (s0 + s1) + (s2 + s3) in LDS -- the finish kernel's layout and
+// order -- and wave 0 applies AdamW.  A workgroup's 64 elements may span two
+// tensors.
+__global__ __launch_bounds__(256) void colsum_adamw_kernel(ColsumAdamWParams q) {
+  __shared__ float red[4][64];
+  __shared__ float sh[2];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  if (threadIdx.x < 64) {
+    const AdamWScalars t = adamw_scalars(q.step, q.a);
+    if (threadIdx.x == 0) {
+      sh[0] = t.step;
+      sh[1] = t.ibc2;
+    }
+  }
+  const int64_t j = (int64_t)blockIdx.x * 64 + lane;
+  float s = 0.0f;
+  if (j < q.n) {
+    int t = 0;
+    while (t + 1 < q.T && j >= q.off[t + 1]) ++t;
+    const int64_t N = q.cols[t], R = q.rows[t];
+    const float* c = q.part[t] + (j - q.off[t]);
+    int64_t r = w;
+    for (; r + 12 < R; r += 16) {
+      const float a0 = c[r * N], a1 = c[(r + 4) * N], a2 = c[(r + 8) * N], a3 = c[(r + 12) * N];
+      s += (a0 + a1) + (a2 + a3);
+    }
+    for (; r < R; r += 4) s += c[r * N];
+  }
+  red[w][lane] = s;
+  __syncthreads();
+  if (w != 0 || j >= q.n) return;
+  const AdamWScalars sc{sh[0], sh[1]};
+  const float g = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
+  q.G[j] = g;
+  float p = q.P[j], m = q.M[j], v = q.V[j];
+  adamw_elem(p, g, m, v, sc, q.a);
+  q.P[j] = p;
+  q.M[j] = m;
+  q.V[j] = v;
+  q.Wb[j] = f32_to_bf16(p);
+}
+
+struct CadwAttr {
+  int T = 0;
+  AdamWArgs a{};
+  bool ok = false;
+};
+CadwAttr read_cadw(const void* attr) {
+  CadwAttr c;
+  const AttrBlob& b = blob(attr);
+  if (!attr || b.schema_id != AICF_SCHEMA_CADW || !payload_ok(b, 24)) return c;
+  c.T = field<int32_t>(b, 0);
+  const float lr = field<float>(b, 4), b1 = field<float>(b, 8), b2 = field<float>(b, 12);
+  const float eps = field<float>(b, 16), wd = field<float>(b, 20);
+  if (c.T < 1 || c.T > kColsumAdamMax || lr != lr || b1 != b1 || b2 != b2 || eps != eps || wd != wd) return c;
+  c.a = AdamWArgs{lr, b1, b2, eps, wd, 1.0f - b1, 1.0f - b2, 1.0f - lr * wd};
+  c.ok = true;
+  return c;
+}
+
+// whether the byte ranges of two contiguous tensors (f32, i32 or 16-bit) meet
+bool overlaps(const TensorDesc& x, const TensorDesc& y) {
+  auto bytes = [](const TensorDesc& t) {
+    return (uintptr_t)(numel_of(t) * (dt(t) == DType::kF32 || dt(t) == DType::kI32 ? 4 : 2));
+  };
+  const uintptr_t a0 = (uintptr_t)x.data, a1 = a0 + bytes(x);
+  const uintptr_t b0 = (uintptr_t)y.data, b1 = b0 + bytes(y);
+  return a0 < b1 && b0 < a1;
+}
+
+bool colsum_adamw_fill(const TensorDesc* in, int ni, const TensorDesc* out, int no, const void* attr,
+                       ColsumAdamWParams* qp) {
+  const CadwAttr c = read_cadw(attr);
+  if (!c.ok || !in || !out || ni != c.T + 4 || no != 5) return false;
+  ColsumAdamWParams q{};
+  q.T = c.T;
+  q.a = c.a;
+  int64_t n = 0;
+  for (int t = 0; t < c.T; ++t) {
+    const TensorDesc& C = in[t];
+    if (dt(C) != DType::kF32 || !C.contiguous || C.rank != 2 || C.shape[0] < 1 || C.shape[1] < 1) return false;
+    q.part[t] = (const float*)C.data;
+    q.rows[t] = C.shape[0];
+    q.cols[t] = C.shape[1];
+    q.off[t] = n;
+    n += C.shape[1];
+  }
+  q.off[c.T] = n;
+  const TensorDesc &P = in[c.T], &M = in[c.T + 1], &V = in[c.T + 2], &S = in[c.T + 3];
+  const TensorDesc &G = out[0], &Po = out[1], &Mo = out[2], &Vo = out[3], &W = out[4];
+  for (const TensorDesc* x : {&P, &M, &V, &G})
+    if (dt(*x) != DType::kF32 || !x->contiguous || numel_of(*x) != n) return false;
+  if (dt(W) != DType::kBF16 || !W.contiguous || numel_of(W) != n) return false;
+  if (!i32_scalar_contig(S)) return false;
+  if (Po.data != P.data || Mo.data != M.data || Vo.data != V.data) return false;  // in place
+  if (!same_shape(Po, P) || !same_shape(Mo, M) || !same_shape(Vo, V)) return false;
+  // the outputs are written where nothing else is read or written
+  const TensorDesc* w[5] = {&G, &P, &M, &V, &W};
+  for (int x = 0; x < 5; ++x) {
+    for (int y = x + 1; y < 5; ++y)
+      if (overlaps(*w[x], *w[y])) return false;
+    for (int t = 0; t < c.T; ++t)
+      if (overlaps(*w[x], in[t])) return false;
+    if (overlaps(*w[x], S)) return false;
+  }
+  q.n = n;
+  q.G = (float*)G.data;
+  q.P = (float*)P.data;
+  q.M = (float*)M.data;
+  q.V = (float*)V.data;
+  q.Wb = (uint16_t*)W.data;
+  q.step = (const int32_t*)S.data;
+  if (qp) *qp = q;
+  return true;
+}
+bool colsum_adamw_supported(const TensorDesc* in, int ni, const TensorDesc* out, int no, const void* a) {
+  return colsum_adamw_fill(in, ni, out, no, a, nullptr);
+}
+Status colsum_adamw_launch(const TensorDesc* in, int ni, TensorDesc* out, int no, const void* attr, void*,
+                           size_t, void* stream) {
+  ColsumAdamWParams q{};
+  if (!colsum_adamw_fill(in, ni, out, no, attr, &q)) return Status::InvalidArgument;
+  const unsigned blocks = (unsigned)((q.n + 63) / 64);
+  colsum_adamw_kernel<<<blocks, 256, 0, as_stream(stream)>>>(q);
+  return launch_status("colsum_adamw_f32_v0");
+}
+
 }  // namespace
 
 KernelVariant make_adam_step_f32_variant() {
@@ -526,6 +684,9 @@ KernelVariant make_adam_step_f32_variant() {
 }
 KernelVariant make_adamw_step_f32_variant() {
   return make("adamw_step_f32_vec4", adamw_launch, adamw_supported, AICF_SCHEMA_ADAM);
+}
+KernelVariant make_colsum_adamw_f32_variant() {
+  return make("colsum_adamw_f32", colsum_adamw_launch, colsum_adamw_supported, AICF_SCHEMA_CADW);
 }
 KernelVariant make_biascorr_variant() {
   return make("bias_corr_f32", bias_corr_launch, bias_corr_supported, AICF_SCHEMA_BCOR);

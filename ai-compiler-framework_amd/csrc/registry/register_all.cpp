@@ -71,6 +71,9 @@ KernelVariant make_gemm_adamw_bf16_variant();
 KernelVariant make_xent_head_f32_variant();
 KernelVariant make_grad_group_f32_variant();
 KernelVariant make_adamw_multi_f32_variant();
+// eltwise.hip / optim.hip (step tail)
+KernelVariant make_mse_colsum_variant();
+KernelVariant make_colsum_adamw_f32_variant();
 
 void register_all_kernels_into(KernelRegistry& R) {
   if (std::getenv("AICF_VERBOSE")) std::fprintf(stderr, "[aicf] register_all: gfx950 backend\n");
@@ -171,6 +174,8 @@ void register_all_kernels_into(KernelRegistry& R) {
   reg(OpKind::XentHead, make_xent_head_f32_variant(), 0, "xent_head_f32_v0");
   reg(OpKind::GradGroup, make_grad_group_f32_variant(), 0, "grad_group_f32_v0");
   reg(OpKind::AdamWMulti, make_adamw_multi_f32_variant(), 0, "adamw_multi_f32_v0");
+  reg(OpKind::MseColsum, make_mse_colsum_variant(), 0, "mse_colsum_v0");
+  reg(OpKind::ColsumAdamW, make_colsum_adamw_f32_variant(), 0, "colsum_adamw_f32_v0");
 }
 
 }  // namespace aicf::hip

@@ -161,6 +161,8 @@ const char* opkind_name(OpKind k) {
     case OpKind::XentHead: return "xent_head";
     case OpKind::GradGroup: return "grad_group";
     case OpKind::AdamWMulti: return "adamw_multi";
+    case OpKind::MseColsum: return "mse_colsum";
+    case OpKind::ColsumAdamW: return "colsum_adamw";
     case OpKind::_Count: break;
   }
   return "unknown";

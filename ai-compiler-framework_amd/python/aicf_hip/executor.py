@@ -62,6 +62,7 @@ OPNAME_TO_KIND: Dict[str, int] = {
     "gelu": int(_C.OpKind.EltwiseGelu), "transpose": int(_C.OpKind.Transpose),
     "gemm_adamw": int(_C.OpKind.GemmAdamW), "xent_head": int(_C.OpKind.XentHead),
     "grad_group": int(_C.OpKind.GradGroup), "adamw_multi": int(_C.OpKind.AdamWMulti),
+    "mse_colsum": int(_C.OpKind.MseColsum), "colsum_adamw": int(_C.OpKind.ColsumAdamW),
 }
 
 
@@ -77,6 +78,8 @@ SCHEMA_MSEG = _fourcc_le(b"MSEG")
 SCHEMA_RRED = _fourcc_le(b"RRED")
 SCHEMA_GADW = _fourcc_le(b"GADW")
 SCHEMA_GGRP = _fourcc_le(b"GGRP")
+SCHEMA_MSCS = _fourcc_le(b"MSCS")
+SCHEMA_CADW = _fourcc_le(b"CADW")
 SCHEMA_GEMM = int.from_bytes(b"GEMM", "big")
 SCHEMA_RSUM = int.from_bytes(b"RSUM", "big")
 
@@ -94,7 +97,8 @@ def epilogue_kind(attrs: Dict[str, Any]) -> int:
     act = str(attrs.get("epilogue_act", "relu")).lower()
     bias = bool(attrs.get("epilogue_bias", True))
     if act == "dgelu":
-        return 6 if attrs.get("epilogue_colsum", False) else 5
+        cs = attrs.get("epilogue_colsum", False)
+        return 7 if cs == "partials" else 6 if cs else 5
     if act == "gelu":
         return 3 if bias else 4
     if act in ("none", ""):
@@ -104,10 +108,12 @@ def epilogue_kind(attrs: Dict[str, Any]) -> int:
 
 def warmup_attrs(op: str, attrs: Dict[str, Any]) -> Dict[str, Any]:
     """Attributes of an op under AICF_WARMUP=1 (exec.py:423-431): every Adam
-    update runs with lr 0, and a grad_group's step_inc job adds 0 (the copy
-    the warmup makes of step_inc)."""
-    if op in ("adam_step", "adamw_step", "gemm_adamw", "adamw_multi"):
+    update runs with lr 0, and a grad_group's step_inc job and mse_colsum's
+    step increment add 0 (the copy the warmup makes of step_inc)."""
+    if op in ("adam_step", "adamw_step", "gemm_adamw", "adamw_multi", "colsum_adamw"):
         return dict(attrs, lr=0.0)
+    if op == "mse_colsum":  # its step_inc part adds 0
+        return dict(attrs, step_inc=0)
     if op == "grad_group":
         return dict(attrs, jobs=[[j[0], j[1], j[2], j[3], 0 if j[0] == 3 else j[4], j[5]]
                                  for j in attrs.get("jobs", [])])
@@ -125,6 +131,12 @@ def pack_attrs(op: str, attrs: Dict[str, Any]) -> Tuple[int, bytes]:
     if op == "gemm_adamw":
         return SCHEMA_GADW, struct.pack("<iifffff", int(bool(a.get("transA", False))),
                                         int(bool(a.get("transB", False))), float(a.get("lr", 1e-3)),
+                                        float(a.get("beta1", 0.9)), float(a.get("beta2", 0.999)),
+                                        float(a.get("eps", 1e-8)), float(a.get("weight_decay", 0.0)))
+    if op == "mse_colsum":
+        return SCHEMA_MSCS, struct.pack("<fi", float(a.get("scale", 0.0)), int(a.get("step_inc", 1)))
+    if op == "colsum_adamw":
+        return SCHEMA_CADW, struct.pack("<ifffff", int(a["tensors"]), float(a.get("lr", 1e-3)),
                                         float(a.get("beta1", 0.9)), float(a.get("beta2", 0.999)),
                                         float(a.get("eps", 1e-8)), float(a.get("weight_decay", 0.0)))
     if op == "grad_group":

@@ -28,6 +28,11 @@ compile-time rewrites of the reference pipeline:
   independent small jobs (fp32 GEMMs with few tiles, column sums, the loss
   mean, step_inc) become one grad_group launch; consecutive adamw_step ops
   sharing step and hyperparameters become one adamw_multi launch.
+* StageG  fuse_step_tail (not in the reference; opt-in, after StageC' and
+  StageE): the loss and bias tail of a large MSE step in two launches: the
+  MSE loss, the last bias's column sums (as partials) and step_inc become one
+  mse_colsum op; the dGELU GEMMs keep their column sums as partials (GEPI
+  kind 7); the bias AdamW step finishes all of them (colsum_adamw).
 * StageB  apply_kernel_selection (reference kernel_select.py:22-142 and the
   vec2/half2 upgrades of plan.py:371-444): pins a kernel_id on every op.
 
@@ -47,7 +52,8 @@ _PRIMITIVES = {
     "copy", "copy_saved", "copy_aux", "grad_zero", "adam_step", "step_inc", "bias_corr",
     "sgd_step", "gelu", "gelu_bwd", "softmax_xent", "row_softmax", "row_reduce", "mse_loss",
     "adamw_step", "layernorm_fwd", "layernorm_bwd", "batchnorm_fwd", "batchnorm_bwd",
-    "transpose", "gemm_adamw", "xent_head", "grad_group", "adamw_multi",
+    "transpose", "gemm_adamw", "xent_head", "grad_group", "adamw_multi", "mse_colsum",
+    "colsum_adamw",
 }
 
 _ALIASES = {"adamstep": "adam_step", "stepinc": "step_inc", "biascorr": "bias_corr",
@@ -357,6 +363,10 @@ def pick_kernel_id(ir: IRGraph, it: Dict[str, Any]) -> Optional[str]:
         return "grad_group_f32_v0"
     if op == "adamw_multi":
         return "adamw_multi_f32_v0"
+    if op == "mse_colsum":
+        return "mse_colsum_v0"
+    if op == "colsum_adamw":
+        return "colsum_adamw_f32_v0"
     if op in ("layernorm_fwd", "layernorm_bwd"):
         return f"{op}_{'f16' if f16 else 'f32'}_v0"
     if op in ("batchnorm_fwd", "batchnorm_bwd"):
@@ -542,6 +552,123 @@ def fuse_colsum_into_dgelu(ir: IRGraph, lowered: Lowered) -> Lowered:
         g["attrs"]["epilogue_colsum"] = True
         drop.add(j)
     return [it for j, it in enumerate(out) if j not in drop]
+
+
+# ---------------------------------------------------------------- StageG
+MAX_COLSUM_ADAMW = 8
+
+
+def fuse_step_tail(ir: IRGraph, lowered: Lowered) -> Lowered:
+    """StageG (not in the reference): for a step with
+        mse_loss(y, t) -> (dY, loss, ws);  reduce_sum(dY) -> (db_L, P_ws)
+        gemm_epilogue dGELU + column sums (dz, db_l, ws_l) for the hidden biases
+        step_inc(step);  adamw_step over the range the db's tile
+    the tail becomes
+        mse_colsum(y, t, step) -> (dY, loss, ws, C_L, step)   at the loss
+        gemm_epilogue dGELU + partials (dz, C_l)               (GEPI kind 7)
+        colsum_adamw(C_1 .. C_L, P, M, V, step) -> (G, P, M, V, Wb)
+    with C_* new fp32 partial values: C_L [P, N] (the reduce_sum's workspace
+    rows, so its column sums are that op's bits), C_l [M / 256, N] (the
+    GEMM's 256-row tiles, finished in the order of the finish kernel, so db_l
+    and the updates are the unfused tail's bits).  The step counter is
+    incremented by the loss op, before every reader of it.  Anything that
+    does not match leaves the list unchanged."""
+    k = _kind
+    low = [dict(it, inputs=list(it["inputs"]), outputs=list(it["outputs"]), attrs=dict(it.get("attrs", {})))
+           for it in lowered]
+    ml = [i for i, it in enumerate(low) if k(it) == "mse_loss" and len(it["outputs"]) == 3]
+    ad = [i for i, it in enumerate(low) if k(it) == "adamw_step" and len(it["outputs"]) == 4]
+    si = [i for i, it in enumerate(low) if k(it) == "step_inc"]
+    if len(ml) != 1 or len(ad) != 1 or len(si) != 1:
+        return lowered
+    im, ia, iss = ml[0], ad[0], si[0]
+    dY = int(low[im]["outputs"][0])
+    step = int(low[iss]["inputs"][0])
+    adam = low[ia]
+    if int(adam["inputs"][4]) != step or int(low[iss]["outputs"][0]) != step or not im < iss < ia:
+        return lowered
+    sY = ir.values[dY].shape
+    if len(sY) != 2:
+        return lowered
+    Mrows, N = int(sY[0]), int(sY[1])
+    # the last bias: reduce_sum(dY) with a [P, N] workspace
+    rs = [i for i, it in enumerate(low) if k(it) == "reduce_sum" and it["inputs"] == [dY]
+          and len(it["outputs"]) == 2 and int(it["attrs"].get("axis", 0)) == 0]
+    if len(rs) != 1:
+        return lowered
+    ir_ = rs[0]
+    dbL, wsL = (int(x) for x in low[ir_]["outputs"])
+    P = int(ir.values[wsL].shape[0]) if len(ir.values[wsL].shape) == 2 else 0
+    # bf16 gradients: the partition of the two-pass bf16 column sum (its bits)
+    if P < 1 or Mrows % P or Mrows < 2 * P or N % 8 or not _is(_dt(ir, dY), "bfloat16"):
+        return lowered
+    # nothing between the loss and step_inc touches the step counter, and
+    # nothing between the loss and the reduce_sum writes dY
+    for it in low[im + 1:iss]:
+        if step in it["inputs"] or step in it["outputs"]:
+            return lowered
+    for it in low[im + 1:ir_]:
+        if any(_base(ir, int(o)) == _base(ir, dY) for o in it["outputs"]):
+            return lowered
+    # the hidden biases: dGELU GEMMs with column sums
+    dg = [i for i, it in enumerate(low) if k(it) == "gemm_epilogue" and it["attrs"].get("epilogue_colsum") is True
+          and len(it["outputs"]) == 3]
+    db_of = {dbL: None}
+    for i in dg:
+        db_of[int(low[i]["outputs"][1])] = i
+    # the bias step's range is tiled by the db values, in order
+    Pv, Gv, Mv, Vv, _ = (int(x) for x in adam["inputs"])
+    Wv = int(adam["outputs"][3])
+    gb, s = _base_and_offset(ir, Gv)
+    n = _numel(ir, Gv)
+    spans = sorted((_base_and_offset(ir, d)[1], d) for d in db_of)
+    if len(spans) > MAX_COLSUM_ADAMW or any(_base(ir, d) != gb for d in db_of):
+        return lowered
+    pos = s
+    for off, d in spans:
+        if off != pos or len(ir.values[d].shape) != 1:
+            return lowered
+        pos += _numel(ir, d)
+    if pos != s + n:
+        return lowered
+    # the db values are read by nothing else (the bias step reads G)
+    for it in low:
+        if any(int(x) in db_of for x in it["inputs"]):
+            return lowered
+    dev = ir.values[dY].device
+    part = {}
+    part[dbL] = ir.new_value(name=f"{ir.values[dbL].name}.partials", shape=(P, N), dtype="torch.float32",
+                             device=dev).id
+    for d, i in db_of.items():
+        if i is None:
+            continue
+        dz = int(low[i]["outputs"][0])
+        rows, cols = (int(x) for x in ir.values[dz].shape)
+        if rows % 256 or cols != _numel(ir, d):
+            return lowered
+        part[d] = ir.new_value(name=f"{ir.values[d].name}.partials", shape=(rows // 256, cols),
+                               dtype="torch.float32", device=dev).id
+    y, t = (int(x) for x in low[im]["inputs"])
+    loss, ws = int(low[im]["outputs"][1]), int(low[im]["outputs"][2])
+    msc = _item("mse_colsum", [y, t, step], [dY, loss, ws, part[dbL], step], dict(low[im]["attrs"]))
+    for d, i in db_of.items():
+        if i is not None:
+            low[i]["outputs"] = [int(low[i]["outputs"][0]), part[d]]
+            low[i]["attrs"]["epilogue_colsum"] = "partials"
+    hyper = {kk: adam["attrs"][kk] for kk in ("lr", "beta1", "beta2", "eps", "weight_decay") if kk in adam["attrs"]}
+    cad = _item("colsum_adamw", [part[d] for _, d in spans] + [Pv, Mv, Vv, step], [Gv, Pv, Mv, Vv, Wv],
+                dict(hyper, tensors=len(spans)))
+    out: Lowered = []
+    for i, it in enumerate(low):
+        if i == im:
+            out.append(msc)
+        elif i in (ir_, iss):
+            continue
+        elif i == ia:
+            out.append(cad)
+        else:
+            out.append(it)
+    return out
 
 
 # ---------------------------------------------------------------- StageF
@@ -790,12 +917,12 @@ def fuse_small_step(ir: IRGraph, lowered: Lowered) -> Lowered:
 def compile_lowered(ir: IRGraph, *, fuse: bool = True, fuse_bias: bool = False,
                     nt_layout: Any = False, nt_min_flops: float = 2.0 ** 30,
                     fuse_optimizer: bool = False, fuse_colsum: bool = False,
-                    fuse_small: bool = False) -> Lowered:
-    """StageA -> StageC -> (StageC') -> (StageD) -> (StageE) -> (StageF) -> StageB.
+                    fuse_small: bool = False, fuse_tail: bool = False) -> Lowered:
+    """StageA -> StageC -> (StageC') -> (StageD) -> (StageE) -> (StageF) -> (StageG) -> StageB.
     nt_layout: False (no StageD), True / "all" (transpose every M/N-contiguous
     16-bit operand) or "cost" (transpose only where that is cheaper than
     reading it in place); fuse_colsum: StageC'; fuse_optimizer: StageE;
-    fuse_small: StageF."""
+    fuse_small: StageF; fuse_tail: StageG."""
     low = lower_to_backend_ops(ir)
     if fuse:
         low = fuse_gemm_epilogue(ir, low, fuse_bias=fuse_bias)
@@ -808,6 +935,8 @@ def compile_lowered(ir: IRGraph, *, fuse: bool = True, fuse_bias: bool = False,
         low = fuse_optimizer_into_gemms(ir, low)
     if fuse_small:
         low = fuse_small_step(ir, low)
+    if fuse_tail:
+        low = fuse_step_tail(ir, low)
     return apply_kernel_selection(ir, low)
 
 

@@ -121,7 +121,7 @@ def build_mlp_mse(B: int = 8192, D: int = 4096, L: int = 4, *, lr: float = 1e-3,
                   beta1: float = 0.9, beta2: float = 0.999, eps: float = 1e-8,
                   weight_decay: float = 0.0, dead_dx: bool = True, nt_layout="cost",
                   nt_min_flops: float = 2.0 ** 30, fuse_optimizer: bool = False,
-                  fuse_colsum: bool = False, device: str = "cuda:0"):
+                  fuse_colsum: bool = False, fuse_tail: bool = False, device: str = "cuda:0"):
     """bf16 activations/weights, fp32 master parameters in one flat buffer.
     The GEMM kernel reads M/N-contiguous operands in place; StageD
     (nt_layout) may still insert explicit transposes: "cost" where a
@@ -131,7 +131,8 @@ def build_mlp_mse(B: int = 8192, D: int = 4096, L: int = 4, *, lr: float = 1e-3,
     layer's weights in its epilogue (StageE); the flat step then covers the
     biases only.  fuse_colsum: the bias gradients of the hidden layers are
     column-summed in the epilogue of the dGELU GEMM that produces their
-    input (StageC')."""
+    input (StageC').  fuse_tail: the loss, the bias gradients' column-sum
+    finishes, step_inc and the bias AdamW in two launches (StageG)."""
     ir = IRGraph(name=f"mlp_mse_{B}x{D}x{L}")
     lay = FlatLayout(D, L)
     nv = lambda n, s, dt=F32, view=None: ir.new_value(name=n, shape=s, dtype=dt,  # noqa: E731
@@ -182,7 +183,7 @@ def build_mlp_mse(B: int = 8192, D: int = 4096, L: int = 4, *, lr: float = 1e-3,
             attrs={"lr": lr, "beta1": beta1, "beta2": beta2, "eps": eps,
                    "weight_decay": weight_decay})
     lowered = compile_lowered(ir, fuse_bias=True, nt_layout=nt_layout, nt_min_flops=nt_min_flops,
-                              fuse_optimizer=fuse_optimizer, fuse_colsum=fuse_colsum)
+                              fuse_optimizer=fuse_optimizer, fuse_colsum=fuse_colsum, fuse_tail=fuse_tail)
     plan = build_binding_plan(ir, opts=PlanOptions(param_names={"flat.params"}))
     return ir, lowered, plan
 

@@ -357,13 +357,13 @@ def bench_adam(C, n=1 << 28, steps=10):
 
 
 # ------------------------------------------------------------------ MLP
-def bench_mlp(B, D, L, steps, warmup, dead_dx=True, fuse_optimizer=False, fuse_colsum=False):
+def bench_mlp(B, D, L, steps, warmup, dead_dx=True, fuse_optimizer=False, fuse_colsum=False, fuse_tail=False):
     import torch
 
     from aicf_hip import mlp
 
     ir, lowered, plan = mlp.build_mlp_mse(B, D, L, dead_dx=dead_dx, fuse_optimizer=fuse_optimizer,
-                                          fuse_colsum=fuse_colsum)
+                                          fuse_colsum=fuse_colsum, fuse_tail=fuse_tail)
     ex = mlp.make_executor(ir, lowered, plan)
     inputs, params = mlp.init_mlp_mse(B, D, L)
     ex.build_env(inputs=inputs, params=params, reuse_static=False)
@@ -412,14 +412,16 @@ def gemm_role(op, attrs, n_out):
         return "dW + AdamW"
     if op == "gemm":
         return "dX (first layer)"
-    kind = epilogue_kind(attrs)  # GEPI kinds: 5 dGELU, 6 dGELU + column sums, 3 bias+GELU, 1 bias
-    return {5: "dX with dGELU", 6: "dX with dGELU", 3: "fwd bias+GELU (+Z)"}.get(kind, "fwd bias (last layer)")
+    kind = epilogue_kind(attrs)  # GEPI: 5 dGELU, 6/7 dGELU + column sums / partials, 3 bias+GELU, 1 bias
+    return {5: "dX with dGELU", 6: "dX with dGELU", 7: "dX with dGELU",
+            3: "fwd bias+GELU (+Z)"}.get(kind, "fwd bias (last layer)")
 
 
-def build_step(B, D, L, fuse_optimizer=True, fuse_colsum=True):
+def build_step(B, D, L, fuse_optimizer=True, fuse_colsum=True, fuse_tail=True):
     from aicf_hip import mlp
 
-    ir, lowered, plan = mlp.build_mlp_mse(B, D, L, fuse_optimizer=fuse_optimizer, fuse_colsum=fuse_colsum)
+    ir, lowered, plan = mlp.build_mlp_mse(B, D, L, fuse_optimizer=fuse_optimizer, fuse_colsum=fuse_colsum,
+                                          fuse_tail=fuse_tail)
     ex = mlp.make_executor(ir, lowered, plan)
     inputs, params = mlp.init_mlp_mse(B, D, L)
     ex.build_env(inputs=inputs, params=params, reuse_static=False)
@@ -431,13 +433,13 @@ def step_gemm_times(ex, iters, warmup=2):
     """Average ms per launch of each GEMM op of the step, HIP events on
     torch's current stream around `iters` launches of the op on the step's own
     tensors, after one eager pass over the step (so every activation holds
-    this step's values; the flat AdamW over the biases, which no GEMM reads,
-    is left out)."""
+    this step's values; the AdamW over the biases, which no GEMM reads, is
+    left out)."""
     import torch
 
     s = torch.cuda.current_stream()
     for i, o in enumerate(ex.ops):
-        if o[0] != "adamw_step":
+        if o[0] not in ("adamw_step", "colsum_adamw"):
             ex.launch_op(i, stream=s.cuda_stream)
     torch.cuda.synchronize()
     res = []
@@ -1351,7 +1353,7 @@ def main():
         vendor_compare(C)
         return
 
-    res = bench_mlp(B, D, L, args.steps, args.warmup, fuse_optimizer=True, fuse_colsum=True)
+    res = bench_mlp(B, D, L, args.steps, args.warmup, fuse_optimizer=True, fuse_colsum=True, fuse_tail=True)
     log(f"[bench] mlp {res}")
 
     # dominant kernel: gemm_nt_kernel, the step's 12 GEMM launches (~88% of
@@ -1443,13 +1445,20 @@ def main():
             "note": "same step with the reference's op split: dW GEMMs write the fp32 gradient, one "
                     "streaming AdamW over all parameters, bias gradients by separate column sums"}
         log(f"[bench] mlp reference op split {uf}")
-        nd = bench_mlp(B, D, L, args.steps, args.warmup, dead_dx=False, fuse_optimizer=True, fuse_colsum=True)
+        nd = bench_mlp(B, D, L, args.steps, args.warmup, dead_dx=False, fuse_optimizer=True, fuse_colsum=True,
+                       fuse_tail=True)
         comps["mlp_step_without_dead_input_dx"] = {
             "value": round(nd["steps_per_s"], 3), "unit": "steps/s", "ms": round(nd["ms"], 4),
             "gemms_per_step": nd["gemms"],
             "note": "same step with the first layer's input gradient (never consumed) removed; "
                     "the headline keeps it, as the reference's lowering emits it"}
         log(f"[bench] mlp without dead dX {nd}")
+        nt = bench_mlp(B, D, L, args.steps, args.warmup, fuse_optimizer=True, fuse_colsum=True, fuse_tail=False)
+        comps["mlp_step_without_tail_fusion"] = {
+            "value": round(nt["steps_per_s"], 3), "unit": "steps/s", "ms": round(nt["ms"], 4), "ops": nt["ops"],
+            "note": "the headline plan with the loss and bias tail unfused (mse_loss, reduce_sum, step_inc, "
+                    "column-sum finishes and the bias AdamW as separate launches); same parameters bit for bit"}
+        log(f"[bench] mlp without tail fusion {nt}")
         c1 = bench_c1()
         c1["reference_lowering"] = bench_c1(fuse_small=False)
         comps["c1_mlp_fp32_64x784x256x10_step"] = c1

@@ -77,7 +77,12 @@ extern "C" {
 #define AICF_OP_GRAD_GROUP 26    /* independent small jobs in one launch: GEMMs, column sums, a loss
                                     mean, the step counter (schema GGRP) */
 #define AICF_OP_ADAMW_MULTI 27   /* (P, G, M, V) x T, step -> (P, M, V) x T: AdamW over T tensors (schema ADAM) */
-#define AICF_OP_COUNT 28
+#define AICF_OP_MSE_COLSUM 28    /* pred, target, step -> dPred, loss, loss partials, column partials of
+                                    dPred [P, N], step (+1): MSE loss and gradient, the gradient's
+                                    column sums over P row blocks, the step counter (schema MSCS) */
+#define AICF_OP_COLSUM_ADAMW 29  /* T column-partial tensors [R_t, N_t], P, M, V, step -> G, P, M, V, Wb:
+                                    G = the column sums (concatenated), AdamW on P with it (schema CADW) */
+#define AICF_OP_COUNT 30
 
 /*
  * Attribute schema ids (numeric ABI).  The reference mixes big-endian fourccs
@@ -99,9 +104,11 @@ extern "C" {
                                        out0, f0, f1 (type 0 GEMM f0,f1 = transA,transB; 1 column sum;
                                        2 mean; 3 step counter += f0) */
 #define AICF_SCHEMA_GADW 0x57444147u /* appended: b"GADW" little-endian, <ii fffff> transA, transB, lr, b1, b2, eps, wd */
+#define AICF_SCHEMA_MSCS 0x5343534Du /* appended: b"MSCS" little-endian, <f i> gradient scale (<= 0: 2/n), step += i (0 or 1) */
+#define AICF_SCHEMA_CADW 0x57444143u /* appended: b"CADW" little-endian, <i fffff> T, lr, b1, b2, eps, wd */
 
 /* GEPI epilogue kinds.  0..2 are the values core_v2/exec.py:223-252 packs;
- * 3..6 are appended (no counterpart in the reference). */
+ * 3..7 are appended (no counterpart in the reference). */
 #define AICF_EPI_BIAS_RELU 0
 #define AICF_EPI_BIAS 1
 #define AICF_EPI_RELU 2
@@ -110,6 +117,8 @@ extern "C" {
 #define AICF_EPI_DGELU 5      /* out = acc * gelu_tanh'(Z), input 2 is Z[M,N] */
 #define AICF_EPI_DGELU_COLSUM 6 /* as 5, plus outputs db[N] f32 = column sums of out, and a f32
                                    workspace [P, N] with P >= M/256 (no reference counterpart) */
+#define AICF_EPI_DGELU_PARTIALS 7 /* as 5, plus output [M/256, N] f32: row t of it is the column sums of
+                                     out's 256-row block t (finished by a later COLSUM_ADAMW) */
 
 /*
  * Replaces tensor_desc.hpp:88-158 (struct TensorDesc).  Field order, types
