@@ -1170,8 +1170,9 @@ def stats_report(stats_csv, trace_csv, steps):
         "```",
         "",
         f"Process contents: warmup + {steps} timed replays of the captured step (batch 8192, 4 x 4096^2, "
-        "GELU, MSE, AdamW in the dW GEMMs' epilogue), then the roofline measurement: one eager pass "
-        "over the step and 12 launches of each of its 12 GEMM ops.",
+        "GELU, MSE, AdamW in the dW GEMMs' epilogue, the loss and bias tail in mse_colsum and "
+        "colsum_adamw), then the roofline measurement: one eager pass over the step and 12 launches of "
+        "each of its 12 GEMM ops.",
         "`gemm_nt_kernel<IN, OUT, ACT, BM, BN, WM, WN, AKC, BKC, S>`: IN 2 = bf16; OUT 2 = bf16, 0 = fp32; "
         "ACT 0 none, 2 GELU (+ pre-activation store), 3 dGELU, 4 AdamW; WM x WN waves; AKC/BKC operand "
         "K-contiguous (false: M/N-contiguous, read in place through transposing LDS reads); S LDS stages.",
