@@ -236,3 +236,37 @@ def test_c5_fused_optimizer_plan_bit_identical_at_full_shape(C):
         torch.cuda.empty_cache()
     for k in outs[0]:
         assert torch.equal(outs[0][k], outs[1][k]), k
+
+
+def test_c5_tail_plan_bit_identical_at_full_shape(C):
+    """C5 at its full shape with the loss and bias tail in two launches
+    (StageG) against the same plan without it, one replay each from the same
+    start: all 67,125,248 parameters, both moments, the bf16 shadow, the bias
+    gradients and the step counter bit for bit, the loss (summed in another
+    order) to 1e-6."""
+    from aicf_hip import mlp
+
+    B, D, L = 8192, 4096, 4
+    outs = []
+    for tail in (True, False):
+        ir, lowered, plan = mlp.build_mlp_mse(B, D, L, fuse_optimizer=True, fuse_colsum=True, fuse_tail=tail)
+        assert ("mse_colsum" in [it["op"] for it in lowered]) == tail
+        ex = mlp.make_executor(ir, lowered, plan)
+        inputs, params = mlp.init_mlp_mse(B, D, L)
+        ex.build_env(inputs=inputs, params=params, reuse_static=False)
+        mlp.refresh_shadow(ex)
+        ex.capture(inputs=inputs, params=params, reuse_static=True)
+        ex.replay(1)
+        torch.cuda.synchronize()
+        b0 = mlp.FlatLayout(D, L).b_off(1)
+        o = {k: ex.value(k).cpu().clone() for k in ("flat.params", "opt.m.flat", "opt.v.flat", "wb.flat", "opt.step")}
+        o["bias_grads"] = ex.value("grad.flat")[b0:b0 + L * D].cpu().clone()
+        o["loss"] = float(ex.value("loss").item())
+        outs.append(o)
+        ex.reset_graph()
+        del ex
+        torch.cuda.empty_cache()
+    assert abs(outs[0].pop("loss") - outs[1]["loss"]) <= 1e-6 * abs(outs[1].pop("loss"))
+    for k in outs[0]:
+        assert torch.equal(outs[0][k], outs[1][k]), k
+    assert int(outs[0]["opt.step"].item()) == 1
