@@ -1522,8 +1522,16 @@ Status run_gemm(GemmParams& p, hipStream_t s) {
     // us, x 512: 42.7 vs 46).  The GELU epilogues stay on 256 x 256 (x 512:
     // 45 vs 48-50 us).  K-contiguous operands only; the others keep 256.
     if (p.K <= 512 && (p.act == ACT_NONE || p.act == ACT_RELU) && tiles128 >= 256 &&
-        nt_eligible<IN, OUT>(p, 128, 128, false))
+        (p.K <= 256 || IN == IN_F32) && nt_eligible<IN, OUT>(p, 128, 128, false))
       return run_nt<IN, OUT, 128, 128, 2, 2, false>(p, s);
+    // Other 16-bit GEMMs with K <= 512 and at least one 256 x 256 tile per
+    // CU: the 8-wave persistent tiles (8192 x 4096 x 512: 41.4 vs 46.0 us
+    // none, 48.0 vs 52.5 GELU; x 256 with GELU: 38.4 vs 42.2 us against the
+    // 4-wave 256 x 256 tiles, same bits).
+    if constexpr (IN != IN_F32) {
+      if (p.K <= 512 && tiles256 >= 256 && nt_eligible<IN, OUT>(p, 256, 256, MN))
+        return run_nt<IN, OUT, 256, 256, 2, 4, MN>(p, s);
+    }
     if (tiles256 >= 128 && nt_eligible<IN, OUT>(p, 256, 256, MN)) return run_nt256<IN, OUT>(p, s);
     // 16-bit operands with at least 16 K-steps: small tiles take deeper
     // pipelines (a K-step is a few hundred cycles of MFMA work per wave, less

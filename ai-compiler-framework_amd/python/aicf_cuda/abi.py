@@ -46,6 +46,8 @@ SIGNATURES = {
                                                      ctypes.c_int32, ctypes.c_void_p]),
     "aicf_diag_mfma_loop": (ctypes.c_int32, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_uint32,
                                              ctypes.c_void_p]),
+    "aicf_diag_mfma_loop_form": (ctypes.c_int32, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
+                                                  ctypes.c_uint32, ctypes.c_int32, ctypes.c_void_p]),
     "aicf_mse_loss_grad_noalloc": (ctypes.c_int32, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                                     ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32,
                                                     ctypes.c_float, ctypes.c_void_p]),

@@ -464,12 +464,14 @@ def bench_copy_ceiling(C, elems=1 << 29, iters=10, warmup=2):
     return {"gbs": 4.0 * elems / (ms * 1e-3) / 1e9, "ms": ms}
 
 
-def bench_mfma_ceiling(waves_per_simd=4, iters=20000, launches=8, warm=4):
-    """Sustained rate of the register-only MFMA loop (aicf_diag_mfma_loop:
-    v_mfma_f32_32x32x16_bf16 on random operands, no memory traffic): the
-    power-limited MFMA ceiling of this part, the practical upper bound of any
-    bf16 GEMM on it.  `warm` launches (~14 ms each) bring the board to its
-    power-limited steady state before the timed ones."""
+def bench_mfma_ceiling(form=16, waves_per_simd=4, iters=20000, launches=8, warm=4):
+    """Sustained rate of the register-only MFMA loop (aicf_diag_mfma_loop_form
+    on random operands, no memory traffic): form 16 is v_mfma_f32_16x16x32_bf16,
+    the instruction the bf16 GEMM kernels issue, form 32 is
+    v_mfma_f32_32x32x16_bf16.  The higher of the two is the power-limited MFMA
+    ceiling of this part, the practical upper bound of any bf16 GEMM on it.
+    `warm` launches (~14 ms each) bring the board to its power-limited steady
+    state before the timed ones."""
     import ctypes
 
     import torch
@@ -481,21 +483,21 @@ def bench_mfma_ceiling(waves_per_simd=4, iters=20000, launches=8, warm=4):
     blocks = cus * waves_per_simd  # 4 waves per workgroup, one per SIMD
     out = torch.zeros(1, device="cuda")
     s = torch.cuda.current_stream()
-    flops = blocks * 4.0 * iters * 8 * 2 * 32 * 32 * 16
+    flops = blocks * 4.0 * iters * (1 << 18)  # 2^18 flop per wave and round in either form
     times = []
     for k in range(warm + launches):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(s)
-        st = lib.aicf_diag_mfma_loop(ctypes.c_void_p(out.data_ptr()), blocks, iters, k + 1,
-                                     ctypes.c_void_p(s.cuda_stream))
+        st = lib.aicf_diag_mfma_loop_form(ctypes.c_void_p(out.data_ptr()), blocks, iters, k + 1, form,
+                                          ctypes.c_void_p(s.cuda_stream))
         e1.record(s)
         torch.cuda.synchronize()
         if st != 0:
-            raise RuntimeError(f"aicf_diag_mfma_loop failed: status {st}")
+            raise RuntimeError(f"aicf_diag_mfma_loop_form failed: status {st}")
         if k >= warm:
             times.append(e0.elapsed_time(e1))
     ms = sum(times) / len(times)
-    return {"tflops": flops / (ms * 1e-3) / 1e12, "ms": ms}
+    return {"tflops": flops / (ms * 1e-3) / 1e12, "ms": ms, "form": form}
 
 
 # ------------------------------------------------------------------ CPU baseline
@@ -1379,14 +1381,17 @@ def main():
                 "measured": "HIP events around 10 launches of each GEMM op of the step on the step's "
                             "own tensors (torch's current stream), after the timed replays"}
     log(f"[bench] roofline step gemms {times}")
-    ceil = bench_mfma_ceiling()
+    ceils = {f: bench_mfma_ceiling(form=f) for f in (16, 32)}
+    ceil = max(ceils.values(), key=lambda c: c["tflops"])
     roofline["power_limited_mfma_ceiling"] = round(ceil["tflops"], 1)
     roofline["frac_of_ceiling"] = round(achieved / ceil["tflops"], 4)
-    log(f"[bench] register-only MFMA loop {ceil}")
+    log(f"[bench] register-only MFMA loops {ceils}")
 
     comps = {"mfma_register_loop_bf16": {
         "value": round(ceil["tflops"], 1), "unit": "TFLOP/s", "frac": round(ceil["tflops"] / PEAK_BF16_TFLOPS, 4),
-        "note": "v_mfma_f32_32x32x16_bf16 on random register operands, no memory traffic: the "
+        "by_form": {f"{f}x{f}x{512 // f}": round(c["tflops"], 1) for f, c in ceils.items()},
+        "note": "the faster of v_mfma_f32_16x16x32_bf16 (the GEMMs' instruction) and "
+                "v_mfma_f32_32x32x16_bf16 on random register operands, no memory traffic: the "
                 "power-limited MFMA ceiling of this part, measured in this run"}}
     if not args.no_components:
         gg = bench_gemm(C, 8192, 8192, 8192)

@@ -206,6 +206,14 @@ int32_t aicf_mse_loss_grad_noalloc(const void* pred, const float* target, void* 
  * to keep the loop.  Returns AICF_STATUS_*. */
 int32_t aicf_diag_mfma_loop(float* out, int32_t blocks, int32_t iters, uint32_t seed, void* stream);
 
+/* Measurement aid, no counterpart in the reference: as aicf_diag_mfma_loop
+ * with the MFMA form chosen by `form`: 32 (v_mfma_f32_32x32x16_bf16, as
+ * above) or 16 (16 independent v_mfma_f32_16x16x32_bf16 per round, the form
+ * the bf16 GEMM kernels issue; the same 2^18 flop per wave and round).
+ * AICF_STATUS_INVALID_ARGUMENT for any other form. */
+int32_t aicf_diag_mfma_loop_form(float* out, int32_t blocks, int32_t iters, uint32_t seed, int32_t form,
+                                 void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Registry introspection (replaces KernelRegistry::variants_snapshot and    */
 /* find_by_id, registry/registry.hpp:39-42)                                  */

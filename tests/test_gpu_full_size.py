@@ -96,11 +96,13 @@ def test_c3_adamw_2p28_ten_steps_bit_exact_on_a_sample(C):
     assert int(step.item()) == 10
 
 
-# (dtype, M, N, K, act): every C4 shape; GEPI kinds 1 bias only, 0 bias+ReLU, 3 bias+GELU
+# (dtype, M, N, K, act): every C4 shape, and K = 512; GEPI kinds 1 bias only, 0 bias+ReLU, 3 bias+GELU
 C4_CASES = [
     ("bf16", 8192, 8192, 8192, "gelu"), ("bf16", 8192, 8192, 8192, "none"),
     ("bf16", 4096, 4096, 4096, "relu"), ("bf16", 1024, 1024, 1024, "gelu"),
     ("bf16", 8192, 4096, 256, "relu"), ("bf16", 8192, 4096, 11008, "gelu"),
+    # K <= 512 on the 8-wave persistent 256 x 256 tiles (two tiles per workgroup)
+    ("bf16", 8192, 4096, 256, "gelu"), ("bf16", 8192, 4096, 512, "none"),
     ("fp32", 8192, 8192, 8192, "gelu"), ("fp32", 4096, 4096, 4096, "relu"),
     ("fp32", 1024, 1024, 1024, "none"), ("fp32", 8192, 4096, 256, "gelu"),
     ("fp32", 8192, 4096, 11008, "relu"),

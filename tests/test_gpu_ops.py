@@ -848,3 +848,15 @@ def test_diag_mfma_loop_runs_and_rate_is_plausible(C):
         torch.cuda.synchronize()
     tflops = blocks * 4.0 * iters * 8 * 32768 / (e0.elapsed_time(e1) * 1e-3) / 1e12
     assert 300.0 < tflops < 2600.0, tflops
+    # the 16 x 16 x 32 form: same flop per round, rejected forms
+    assert lib.aicf_diag_mfma_loop_form(ctypes.c_void_p(out.data_ptr()), 4, 10, 1, 8, None) == \
+        abi.STATUS_INVALID_ARGUMENT
+    for k in range(3):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        assert lib.aicf_diag_mfma_loop_form(ctypes.c_void_p(out.data_ptr()), blocks, iters, k + 1, 16,
+                                            ctypes.c_void_p(s.cuda_stream)) == abi.STATUS_OK
+        e1.record(s)
+        torch.cuda.synchronize()
+    tflops16 = blocks * 4.0 * iters * 16 * 16384 / (e0.elapsed_time(e1) * 1e-3) / 1e12
+    assert 300.0 < tflops16 < 2600.0, tflops16
