@@ -817,12 +817,14 @@ using template_int_t = std::integral_constant<int, V>;
 // Schedule of one MFMA sub-step of the NT kernel: MFMA t is followed by its
 // FPER fragments' LDS reads (front-loaded, so the last reads still have
 // several MFMAs to land before the next sub-step needs them) and by its
-// share of the NV loads (load u after MFMA t when t*NV/NMF <= u <
-// (t+1)*NV/NMF).  sched_group_barrier masks: 0x008 MFMA, 0x100 DS read,
-// 0x020 VMEM read.
-template <int TM, int TN, int ES, bool AKC, bool BKC, int MS>
+// share of the NV loads, spread over the first LSPAN MFMAs (load u after
+// MFMA t when t*NV/LSPAN <= u < (t+1)*NV/LSPAN).  sched_group_barrier masks:
+// 0x008 MFMA, 0x100 DS read, 0x020 VMEM read.
+template <int TM, int TN, int ES, bool AKC, bool BKC, int MS, int LSPAN>
 struct NTSched {
   static constexpr int NMF = TM * TN * (ES == 4 ? 4 : 1);  // MFMAs per sub-step
+  static_assert(LSPAN >= 1 && LSPAN <= NMF, "loads spread over the sub-step's MFMAs");
+  static constexpr int load_lo(int t, int nv) { return t < LSPAN ? t * nv / LSPAN : nv; }
   static constexpr int NFR = TM + TN;                      // fragments per sub-step
   static constexpr int FPER = (NFR + NMF - 1) / NMF;       // fragments per MFMA
   // 16 x 16 blocks (RECYCLE): the MFMAs run A-fragment-major (t -> block
@@ -843,7 +845,7 @@ struct NTSched {
   template <bool R, int NV, int T>
   static __device__ __forceinline__ void step() {
     constexpr int nds = R ? ds_after(T) : 0;
-    constexpr int vlo = T * NV / NMF, vhi = (T + 1) * NV / NMF;
+    constexpr int vlo = load_lo(T, NV), vhi = load_lo(T + 1, NV);
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
     if constexpr (nds > 0) __builtin_amdgcn_sched_group_barrier(0x100, nds, 0);
     if constexpr (vhi > vlo) __builtin_amdgcn_sched_group_barrier(0x020, vhi - vlo, 0);
@@ -1073,7 +1075,13 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt_kernel(NTParams p) {
   //     RECYCLE; fp32 runs 4 MFMAs per block and sub-step, t / (TM * TN)
   //     selecting the fragment element;
   //   load u: 1 KB direct-to-LDS block u of the wave (A blocks first).
-  using Sched = NTSched<TM, TN, ES, AKC, BKC, MS>;
+  // The 8-wave tiles with 16-bit operands spread a K-step's loads over the
+  // first 3/4 of the first sub-step's MFMAs, the others over all of them
+  // (step 2.85 -> 2.79 ms, same bits; spans of 5/8 and 7/8, a later start,
+  // or loads in both sub-steps were slower, and 3/4 on the 4-wave tiles
+  // slowed 8192^3).
+  constexpr int NMF_ = TM * TN * (ES == 4 ? 4 : 1);
+  using Sched = NTSched<TM, TN, ES, AKC, BKC, MS, NW == 8 && ES == 2 ? NMF_ * 3 / 4 : NMF_>;
   constexpr bool RECYCLE = Sched::RECYCLE;
   auto read_one = [&](const uint8_t* st, int kk, int buf, int f) {
     const int chunk = ((kk * CPS + fh) ^ rsw) * 16;
@@ -1124,7 +1132,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt_kernel(NTParams p) {
       }
       if constexpr (nv > 0) {
 #pragma unroll
-        for (int u = vlo + t * nv / NMF; u < vlo + (t + 1) * nv / NMF; ++u) load_one(lkt, lst, u);
+        for (int u = vlo + Sched::load_lo(t, nv); u < vlo + Sched::load_lo(t + 1, nv); ++u) load_one(lkt, lst, u);
       }
     }
     Sched::template pin<decltype(R)::value, ASM_LDS ? 0 : nv>();  // asm loads are in no sched group
