@@ -47,12 +47,31 @@ def _cs() -> int:
     return torch.cuda.current_stream().cuda_stream
 
 
-def time_launches(fn, iters: int, warmup: int, stream=None, graph: bool = False) -> float:
+WARM_S = 0.05  # seconds of back-to-back work before a timed region
+
+
+def _warm(launch, warm_s: float) -> None:
+    """Keep the GPU busy with `launch` for warm_s seconds: after an idle gap
+    the clock takes tens of milliseconds to return to its loaded steady state,
+    and a few warmup calls of a sub-millisecond kernel time the ramp."""
+    import torch
+
+    t0 = time.perf_counter()
+    while True:
+        for _ in range(4):
+            launch()
+        torch.cuda.synchronize()
+        if time.perf_counter() - t0 >= warm_s:
+            return
+
+
+def time_launches(fn, iters: int, warmup: int, stream=None, graph: bool = False, warm_s: float = WARM_S) -> float:
     """Average milliseconds per call of fn(), HIP events on `stream`
-    (torch's current stream by default).  graph: the `iters` calls are
-    captured into one graph (fn launches on torch's current stream) and the
-    graph is timed, so that kernels of a few microseconds are timed back to
-    back on the device rather than at the rate the host issues them."""
+    (torch's current stream by default), after `warmup` calls and then at
+    least warm_s seconds of calls.  graph: the `iters` calls are captured into
+    one graph (fn launches on torch's current stream) and the graph is timed,
+    so that kernels of a few microseconds are timed back to back on the device
+    rather than at the rate the host issues them."""
     import torch
 
     if graph:
@@ -67,6 +86,7 @@ def time_launches(fn, iters: int, warmup: int, stream=None, graph: bool = False)
                 fn()
         g.replay()
         torch.cuda.synchronize()
+        _warm(g.replay, warm_s)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         rs = torch.cuda.current_stream()  # replay() launches on torch's current stream
         e0.record(rs)
@@ -79,6 +99,7 @@ def time_launches(fn, iters: int, warmup: int, stream=None, graph: bool = False)
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    _warm(fn, warm_s)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(s)
     for _ in range(iters):
