@@ -739,31 +739,49 @@ def mfma_report(counter_csv, trace_csv, pattern):
     return lines
 
 
-def vendor_compare(C):
-    """Our bf16 GEMM and torch.matmul (hipBLASLt) on the same operands:
-    8192^3 NT, the step's 8192x4096x4096 NT, and the step's dW layout
-    (dZ^T . H, K = 8192; ours writes fp32, hipBLASLt bf16).  Per shape, four
-    alternating groups of 5 launches (ours, vendor, ours, vendor), so that
-    neither library always runs on a cooler or hotter part.  The program
-    profiled for the MFMA comparison."""
+# Shape sets of --vendor-compare: (M, N, K) NT shapes, launches per group,
+# whether the step's dW layout follows, and the report's description.
+VENDOR_SETS = {
+    "large": {"shapes": ((8192, 8192, 8192), (8192, 4096, 4096)), "group": 5, "dw": True,
+              "desc": "8192^3 NT, 8192x4096x4096 NT (the step's forward layout), dW = dZ^T.H with K = 8192 "
+                      "(fp32 out for ours, bf16 for hipBLASLt)"},
+    "small": {"shapes": ((1024, 1024, 1024), (8192, 4096, 256), (8192, 4096, 512)), "group": 100, "dw": False,
+              "desc": "the C4 shapes with few tiles or short K: 1024^3, 8192x4096x256 and 8192x4096x512 NT, "
+                      "plain bf16 out (no bias)"},
+}
+
+
+def vendor_compare(C, shape_set="large"):
+    """Our bf16 GEMM and torch.matmul (hipBLASLt) on the same operands, over
+    the shapes of VENDOR_SETS[shape_set] (the large set adds the step's dW
+    layout, dZ^T . H with K = 8192; ours writes fp32, hipBLASLt bf16).  Per
+    shape, four alternating groups of launches (ours, vendor, ours, vendor),
+    so that neither library always runs on a cooler or hotter part.  The
+    program profiled for the counter comparisons."""
     import torch
 
+    vs = VENDOR_SETS[shape_set]
     g = torch.Generator(device="cuda")
     g.manual_seed(9)
 
     def alternate(ours, vendor):
         for _ in range(2):
             for fn in (ours, vendor):
-                for _ in range(5):
+                for _ in range(vs["group"]):
                     fn()
 
-    for (M, N, K) in ((8192, 8192, 8192), (8192, 4096, 4096)):
+    for (M, N, K) in vs["shapes"]:
         X = torch.randn((M, K), device="cuda", generator=g).to(torch.bfloat16)
         W = torch.randn((N, K), device="cuda", generator=g).to(torch.bfloat16)
         Y = torch.empty((M, N), device="cuda", dtype=torch.bfloat16)
         alternate(lambda: C.launch_by_id("gemm_bf16_mfma_v0", C.OpKind.Gemm, [X, W], [Y], 0,
                                          struct.pack("<ii", 0, 1)),
                   lambda: torch.matmul(X, W.t(), out=Y))
+    if not vs["dw"]:
+        torch.cuda.synchronize()
+        log(f"[bench] vendor-compare ({shape_set}): {len(vs['shapes'])} shapes x 2 x ({vs['group']} ours, "
+            f"{vs['group']} torch.matmul) launches")
+        return
     dZ = torch.randn((8192, 4096), device="cuda", generator=g).to(torch.bfloat16)
     H = torch.randn((8192, 4096), device="cuda", generator=g).to(torch.bfloat16)
     dW = torch.empty((4096, 4096), device="cuda")
@@ -844,7 +862,7 @@ VENDOR_PASSES = [
 ]
 
 
-def pmc_compare_report(*paths):
+def pmc_compare_report(*paths, shape_set="large"):
     """Per-flop counter comparison of our bf16 GEMM and hipBLASLt on the same
     operands, from the two rocprofv3 --pmc passes of --vendor-compare
     (VENDOR_PASSES, each with --kernel-trace): arguments are counter_csv,
@@ -866,12 +884,16 @@ def pmc_compare_report(*paths):
             for row in csv.DictReader(f):
                 dur[int(row["Dispatch_Id"])] = (int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) * 1e-9
         groups = OrderedDict()
+        per_shape = 4 * VENDOR_SETS[shape_set]["group"]  # GEMM launches per shape, both libraries
+        i = 0
         for d in sorted(cnt):
             n, grid = meta[d]
             if not ("gemm_nt" in n or "Cijk" in n) or d not in dur:
                 continue
             short = n.replace("void aicf::hip::(anonymous namespace)::", "").split("(")[0][:64]
-            groups.setdefault((("ours " if "gemm_nt" in n else "hipBLASLt ") + short, grid), []).append(d)
+            lib = ("ours " if "gemm_nt" in n else "hipBLASLt ") + short
+            groups.setdefault((lib, grid, i // per_shape), []).append(d)
+            i += 1
         out = OrderedDict()
         for key, ds in groups.items():
             ds = ds[1:] if len(ds) > 4 else ds
@@ -892,17 +914,17 @@ def pmc_compare_report(*paths):
         "Commands (GPU box, repo root; one rocprofv3 run per counter pass):",
         "```",
     ]
+    flag = "" if shape_set == "large" else f" --vendor-set {shape_set}"
     for i, pas in enumerate(VENDOR_PASSES):
         lines.append(f"rocprofv3 --pmc {pas} --kernel-trace --output-format csv -d gpurun_out/pmc_v{i + 1} -o run "
-                     "-- python3 bench.py --vendor-compare")
+                     f"-- python3 bench.py --vendor-compare{flag}")
     lines += [
         "python3 bench.py --pmc-compare-report gpurun_out/pmc_v1/run_counter_collection.csv "
         "gpurun_out/pmc_v1/run_kernel_trace.csv gpurun_out/pmc_v2/run_counter_collection.csv "
-        "gpurun_out/pmc_v2/run_kernel_trace.csv",
+        f"gpurun_out/pmc_v2/run_kernel_trace.csv{flag}",
         "```",
         "",
-        "Shapes: 8192^3 NT, 8192x4096x4096 NT (the step's forward layout), dW = dZ^T.H with K = 8192 "
-        "(fp32 out for ours, bf16 for hipBLASLt).  clock = GRBM_GUI_ACTIVE per XCD / duration; MFMA busy = "
+        f"Shapes: {VENDOR_SETS[shape_set]['desc']}.  clock = GRBM_GUI_ACTIVE per XCD / duration; MFMA busy = "
         "SQ_VALU_MFMA_BUSY_CYCLES / (GUI cycles per XCD x 1024 SIMDs); per-GFLOP columns divide by the "
         "flops the MFMA counter saw (SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512).  LDS conflict = "
         "SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE; TA / TD busy = busy cycles summed over the 256 CUs' units "
@@ -914,7 +936,7 @@ def pmc_compare_report(*paths):
         "|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|",
     ]
     for key, m in p1.items():
-        name, grid = key
+        name, grid, _shape = key
         gui = m["GRBM_GUI_ACTIVE"] / 8.0
         us = m["_us"]
         gf = m["SQ_INSTS_VALU_MFMA_MOPS_BF16"] * 512.0 / 1e9
@@ -1320,6 +1342,8 @@ def main():
                          "[, MFMA counters, kernel trace]) and exit")
     ap.add_argument("--stats-report", nargs=3, metavar=("STATS_CSV", "TRACE_CSV", "STEPS"),
                     help="summarise a rocprofv3 --kernel-trace --stats run of the step and exit")
+    ap.add_argument("--vendor-set", choices=sorted(VENDOR_SETS), default="large",
+                    help="shape set of --vendor-compare and --pmc-compare-report")
     ap.add_argument("--vendor-compare", action="store_true",
                     help="our GEMM and torch.matmul on the same shapes (for rocprofv3 --pmc)")
     ap.add_argument("--pmc-compare-report", nargs=4, metavar="CSV",
@@ -1341,7 +1365,7 @@ def main():
         pmc_mfma_compare_report(*args.pmc_mfma_compare_report)
         return
     if args.pmc_compare_report:
-        pmc_compare_report(*args.pmc_compare_report)
+        pmc_compare_report(*args.pmc_compare_report, shape_set=args.vendor_set)
         return
     if args.c1_trace_report:
         c1_trace_report(*args.c1_trace_report)
@@ -1374,7 +1398,7 @@ def main():
         print(json.dumps({"four_launch": bench_c1(steps=50), "reference_lowering": bench_c1(steps=50, fuse_small=False)}))
         return
     if args.vendor_compare:
-        vendor_compare(C)
+        vendor_compare(C, args.vendor_set)
         return
 
     res = bench_mlp(B, D, L, args.steps, args.warmup, fuse_optimizer=True, fuse_colsum=True, fuse_tail=True)
