@@ -173,6 +173,67 @@ __global__ __launch_bounds__(256) void colsum_finish_kernel(const float* __restr
   if (w == 0 && col < N) out[col] = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
 }
 
+// One-output column sum without a partials buffer (the reference's
+// signature): every workgroup owns a narrow column block for all rows, so the
+// grid has N / (kNarrowLanes * VEC) workgroups instead of N / (64 * VEC).  A
+// row segment of the block is kNarrowLanes 16-byte vectors (32 bytes); the 256
+// threads hold 256 / kNarrowLanes row slots, each summing rows slot, slot +
+// 128, ... with 4 loads in flight, and the slots are added in LDS by a
+// fixed-order tree (deterministic).  Consecutive column blocks, which share
+// 128-byte lines, are given to workgroups on one XCD (workgroup i runs on
+// XCD i % 8), so each line is fetched into one L2.  [8192, 4096] bf16: 16.6
+// us (4 lanes, 8 loads, no remap: 25.6 us; 1 lane: 23.3 us).
+constexpr int kNarrowLanes = 2;
+constexpr int kNarrowSlots = 256 / kNarrowLanes;
+
+template <typename TI, bool BF16IN, bool OUT_F16>
+__global__ __launch_bounds__(256) void colsum_narrow_kernel(const TI* __restrict__ x, void* __restrict__ out,
+                                                            int64_t M, int64_t N) {
+  constexpr int VEC = 16 / sizeof(TI);
+  constexpr int CB = kNarrowLanes * VEC;  // columns per workgroup
+  constexpr int UNROLL = 4;
+  __shared__ float red[kNarrowSlots][CB + 1];
+  const int slot = (int)threadIdx.x / kNarrowLanes, v = (int)threadIdx.x % kNarrowLanes;
+  int bid = blockIdx.x;  // column block: XCD-contiguous when the grid is a multiple of 8
+  if ((gridDim.x & 7) == 0) bid = (bid & 7) * (gridDim.x >> 3) + (bid >> 3);
+  const int64_t c0 = (int64_t)bid * CB + v * VEC;
+  float acc[VEC];
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) acc[e] = 0.0f;
+  if (c0 < N) {  // N % VEC == 0: the whole vector is in range
+    int64_t r = slot;
+    for (; r + (UNROLL - 1) * kNarrowSlots < M; r += UNROLL * kNarrowSlots) {
+      uint4 q[UNROLL];
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u)
+        q[u] = *reinterpret_cast<const uint4*>(x + (r + u * kNarrowSlots) * N + c0);
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) add_vec16<TI, BF16IN>(acc, q[u]);
+    }
+    for (; r < M; r += kNarrowSlots) add_vec16<TI, BF16IN>(acc, *reinterpret_cast<const uint4*>(x + r * N + c0));
+  }
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) red[slot][v * VEC + e] = acc[e];
+  __syncthreads();
+  for (int half = kNarrowSlots / 2; half > 0; half >>= 1) {  // slot i += slot i + half
+    for (int t = (int)threadIdx.x; t < half * CB; t += 256) {
+      const int i = t / CB, c = t % CB;
+      red[i][c] += red[i + half][c];
+    }
+    __syncthreads();
+  }
+  if ((int)threadIdx.x < CB) {
+    const int64_t col = (int64_t)bid * CB + threadIdx.x;
+    if (col < N) {
+      const float sum = red[0][threadIdx.x];
+      if constexpr (OUT_F16)
+        ((uint16_t*)out)[col] = f32_to_f16(sum);
+      else
+        ((float*)out)[col] = sum;
+    }
+  }
+}
+
 // RSUM axis attribute (reduce_sum/launcher.cu:75-85): default 0.
 int64_t read_rsum_axis(const void* attr) {
   const AttrBlob& a = blob(attr);
@@ -213,6 +274,13 @@ Status colsum_run(const void* x, void* out, float* partial, int64_t P, int64_t M
     parts = (M + rpp - 1) / rpp;
   } else {
     partial = nullptr;
+  }
+  const int64_t gn = (N + kNarrowLanes * VEC - 1) / (kNarrowLanes * VEC);
+  if (vec && !partial && gn <= INT32_MAX) {
+    // one output, no partials: narrow column blocks over all rows (a
+    // [8192, 4096] bf16 sum on 8 workgroups of 512 columns took 133 us)
+    colsum_narrow_kernel<TI, BF16IN, OUT_F16><<<(unsigned)gn, 256, 0, s>>>((const TI*)x, out, M, N);
+    return launch_status(what);
   }
   if (vec)
     colsum_vec_kernel<TI, BF16IN, OUT_F16><<<dim3(gx, (unsigned)parts), 256, 0, s>>>(

@@ -315,11 +315,12 @@ def bench_mse(C, rows, cols, iters=20, warmup=3):
     return {"ms": ms, "gbs": nbytes / (ms * 1e-3) / 1e9, "buffer_sets": len(sets)}
 
 
-def bench_colsum(C, rows, cols, iters=20, warmup=3):
+def bench_colsum(C, rows, cols, iters=20, warmup=3, partials=True):
     """Bias gradient of the train step: column sum of dY [rows, cols] bf16 ->
     fp32 [cols] (2 bytes per element read), with the [64, cols] partials
     buffer the lowered step passes (two passes: 64 row slices, then their
-    fixed-order sum)."""
+    fixed-order sum), or, partials=False, with the reference's one output
+    (one pass over narrow column blocks)."""
     import torch
 
     g = torch.Generator(device="cuda")
@@ -332,8 +333,8 @@ def bench_colsum(C, rows, cols, iters=20, warmup=3):
     def fn():
         x, o, part = sets[k[0] % len(sets)]
         k[0] += 1
-        C.launch_by_id("reduce_sum_keep_lastdim_bf16_to_f32_v0", C.OpKind.ReduceSum, [x], [o, part], 0, b"",
-                       _cs())
+        C.launch_by_id("reduce_sum_keep_lastdim_bf16_to_f32_v0", C.OpKind.ReduceSum, [x],
+                       [o, part] if partials else [o], 0, b"", _cs())
 
     ms = time_launches(fn, iters, warmup, graph=True)
     nbytes = 2 * rows * cols + 4 * cols
@@ -1479,6 +1480,11 @@ def main():
                                              "frac": round(cs["gbs"] / PEAK_HBM_GBS, 4),
                                              "ms": round(cs["ms"], 5)}
         log(f"[bench] colsum {cs}")
+        cs1 = bench_colsum(C, B, D, partials=False)
+        comps[f"colsum_bf16_f32_{B}x{D}_one_output"] = {"value": round(cs1["gbs"], 1), "unit": "GB/s",
+                                                        "frac": round(cs1["gbs"] / PEAK_HBM_GBS, 4),
+                                                        "ms": round(cs1["ms"], 5)}
+        log(f"[bench] colsum one output {cs1}")
         ad = bench_adam(C)
         comps["adamw_2^28"] = {"value": round(ad["gbs"], 1), "unit": "GB/s",
                                "frac": round(ad["gbs"] / PEAK_HBM_GBS, 4), "ms": round(ad["ms"], 4)}

@@ -310,6 +310,30 @@ def test_reduce_sum_columns(C):
     assert orc.rel_err(h(o1), ref) < 1e-5
 
 
+@pytest.mark.parametrize("rows,cols", [(1, 8), (3, 96), (129, 4104), (1000, 256), (4097, 520), (8192, 96)])
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+def test_reduce_sum_one_output_narrow_blocks(C, rows, cols, dt):
+    """The reference's one-output column sum (no partials buffer) on narrow
+    column blocks over all rows: single rows, column counts that are not a
+    multiple of a block or of 8 blocks (no XCD remap), and long columns, vs
+    the fp64 column sum of the same stored values."""
+    x = rng(rows * 7 + cols).standard_normal((rows, cols)).astype(np.float32)
+    if dt == "f32":
+        t, ref = g(x), orc.colsum_f64(x)
+        kid = "reduce_sum_keep_lastdim_f32_v0"
+    elif dt == "bf16":
+        xb = orc.bf16_bits_from_f32(x)
+        t, ref = g(xb, torch.bfloat16), orc.colsum_f64(orc.bf16_bits_to_f32(xb).reshape(rows, cols))
+        kid = "reduce_sum_keep_lastdim_bf16_to_f32_v0"
+    else:
+        xh = x.astype(np.float16)
+        t, ref = g(xh.view(np.uint16)), orc.colsum_f64(xh.astype(np.float32))
+        kid = "reduce_sum_keep_lastdim_f16_to_f32_v0"
+    o = torch.full((cols,), float("nan"), device="cuda")
+    C.launch_by_id(kid, C.OpKind.ReduceSum, [t], [o])
+    assert orc.rel_err(h(o), ref) < 1e-5
+
+
 @pytest.mark.parametrize("cols,rows", [(128, 64), (1024, 64), (8192, 64), (32768, 16), (1000, 64), (64, 64),
                                        (2048, 64), (4096, 64), (256, 37), (128, 37), (1024, 37), (512, 5),
                                        (16384, 3)])
