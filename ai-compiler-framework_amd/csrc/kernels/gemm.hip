@@ -835,7 +835,8 @@ struct NTSched {
   static constexpr bool RECYCLE = MS == 16;
   static constexpr int ds_instrs(int lo, int hi) {
     int n = 0;
-    for (int r = lo; r < hi && r < NFR; ++r) n += r < TM ? (AKC ? 1 : 2) : (BKC ? 1 : 2);
+    constexpr int MN_READS = ES == 4 ? 4 : 2;  // LDS reads of an M/N-contiguous fragment
+    for (int r = lo; r < hi && r < NFR; ++r) n += r < TM ? (AKC ? 1 : MN_READS) : (BKC ? 1 : MN_READS);
     return n;
   }
   static constexpr int ds_after(int t) {
@@ -882,8 +883,12 @@ struct NTSched {
 // Loads are buffer loads straight into LDS with per-lane offsets fixed for
 // the whole K loop (the K advance is the scalar offset); the host checks that
 // the bytes a resource spans fit a signed 32-bit offset.
-template <int MS>
+// fp32 (ES 4): a fragment read takes one row k and the row k + 4 in the two
+// halves of the wave (32 consecutive floats each), so rows k and k + 4 sit
+// 8 chunks (32 banks) apart.
+template <int MS, int ES = 2>
 __device__ __forceinline__ int nt_mn_swizzle(int k) {
+  if constexpr (ES == 4) return 8 * ((k >> 2) & 1);
   return MS == 16 ? ((4 * (k & 3)) ^ (2 * ((k >> 3) & 1))) : 4 * (k & 3);
 }
 
@@ -894,7 +899,7 @@ struct NTOperand {
   static constexpr int ROWB = BMN * ES;              // MN-contiguous row bytes
   static constexpr int CPR = ROWB / 16;              // chunks per MN-contiguous row
   static_assert(BYTES % (1024 * NW) == 0, "load blocks must split evenly over waves");
-  static_assert(KC || (ES == 2 && CPR >= 16), "MN-contiguous tiles: 16-bit, >= 16 chunks per row");
+  static_assert(KC || CPR >= 16, "MN-contiguous tiles: >= 16 chunks per row");
 
   i32x4_t rsrc;
   int voff[BLOCKS];
@@ -924,10 +929,10 @@ __device__ __forceinline__ void nt_operand_init(NTOperand<KC, BMN, NW, ES>& o, c
     for (int t = 0; t < o.BLOCKS; ++t) {
       const int q = wave + t * NW;
       const int k = q * RPB + lane / CPR;
-      const int c = (lane % CPR) ^ nt_mn_swizzle<MS>(k);
-      o.voff[t] = (k * (int)ld + c * 8) * 2;
+      const int c = (lane % CPR) ^ nt_mn_swizzle<MS, ES>(k);
+      o.voff[t] = k * (int)ld * ES + c * 16;
     }
-    o.soff_step = 64 * (int)ld * 2;
+    o.soff_step = 128 * (int)ld;  // 128 / ES K-rows per stage
   }
 }
 
@@ -967,7 +972,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt_kernel(NTParams p) {
   constexpr int MS = ES == 2 ? 16 : 32;
   constexpr int KS = MS == 16 ? 2 : 4;  // MFMA sub-steps per K-step
   constexpr int CPS = 64 / MS;          // 16-byte chunks of a 128-byte K-row per sub-step
-  constexpr int KPS = 16 * CPS / 2;     // K-rows of an MN-contiguous stage per sub-step (16-bit)
+  constexpr int KPS = ES == 4 ? 8 : 16 * CPS / 2;  // K-rows of an MN-contiguous stage per sub-step
   constexpr int NW = WM * WN;
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int TM = WTM / MS, TN = WTN / MS;
@@ -1025,29 +1030,46 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt_kernel(NTParams p) {
     else
       return ((((mb >> 3) ^ nt_mn_swizzle<MS>(tr_row)) + ((i16 >> 1) & 1)) * 16) + 8 * (i16 & 1);
   };
+  // fp32 M/N-contiguous: lane (fr, fh) holds element mb + fr of K-rows
+  // 4 fh .. 4 fh + 3 of the sub-step (four 4-byte reads, one per K-row);
+  // the row swizzle of those rows is 8 fh
+  auto mn32_off = [&](int mb, int rowb) {
+    const int m = mb + fr;
+    return 4 * fh * rowb + (((m >> 2) ^ (8 * fh)) * 16) + (m & 3) * 4;
+  };
   int a_off[TM], b_off[TN];
 #pragma unroll
   for (int j = 0; j < TM; ++j) {
     const int mb = wm * WTM + j * MS;
-    a_off[j] = AKC ? (mb + fr) * 128 : tr_row * (BM * 2) + tr_col(mb);
+    if constexpr (AKC) a_off[j] = (mb + fr) * 128;
+    else a_off[j] = ES == 4 ? mn32_off(mb, BM * ES) : tr_row * (BM * 2) + tr_col(mb);
   }
 #pragma unroll
   for (int i = 0; i < TN; ++i) {
     const int nb = wn * WTN + i * MS;
-    b_off[i] = A_BYTES + (BKC ? (nb + fr) * 128 : tr_row * (BN * 2) + tr_col(nb));
+    if constexpr (BKC) b_off[i] = A_BYTES + (nb + fr) * 128;
+    else b_off[i] = A_BYTES + (ES == 4 ? mn32_off(nb, BN * ES) : tr_row * (BN * 2) + tr_col(nb));
   }
 
   typedef short v4i16 __attribute__((ext_vector_type(4)));
   auto tr_frag = [&](const uint8_t* addr, int rowb) -> u16x8 {
-    const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)addr);
-    const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)(addr + 4 * rowb));
-    u16x8 f;
+    if constexpr (ES == 4) {  // fp32: four K-rows, one float each
+      f32x4 v;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      f[e] = (uint16_t)lo[e];
-      f[e + 4] = (uint16_t)hi[e];
+      for (int e = 0; e < 4; ++e) v[e] = *reinterpret_cast<const float*>(addr + e * rowb);
+      return __builtin_bit_cast(u16x8, v);
+    } else {
+      const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)addr);
+      const v4i16 hi =
+          __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)(addr + 4 * rowb));
+      u16x8 f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        f[e] = (uint16_t)lo[e];
+        f[e + 4] = (uint16_t)hi[e];
+      }
+      return f;
     }
-    return f;
   };
 
   u16x8 fa[2][TM], fb[2][TN];
@@ -1416,8 +1438,9 @@ Status run_nt_layout(const GemmParams& g, hipStream_t s) {
 }
 
 // Operand layouts: K-contiguous ([MN][K]) on every tile configuration;
-// MN-contiguous ([K][MN], read through the transposing LDS loads) on the
-// 256 x 256 configuration (MN_OK).
+// MN-contiguous ([K][MN], read through the transposing LDS loads for 16-bit
+// operands, one 4-byte read per K-row for fp32) on the 256 x 256
+// configuration (MN_OK).
 template <int IN, int OUT, int BM, int BN, int WM, int WN, bool MN_OK, int S = 2>
 Status run_nt(const GemmParams& g, hipStream_t s) {
   const bool akc = g.a_mode == LD_KCONTIG, bkc = g.b_mode == LD_KCONTIG;
@@ -1449,17 +1472,16 @@ Status run_nt256(const GemmParams& g, hipStream_t s) {
         return run_nt_act<IN, OUT, ACT_GELU, 256, 256, 2, 2, true, true>(g, s);
     }
   }
-  return run_nt<IN, OUT, 256, 256, 2, 4, IN != IN_F32>(g, s);
+  return run_nt<IN, OUT, 256, 256, 2, 4, true>(g, s);
 }
 
-// The NT fast path applies to 16-bit operands that are each K-contiguous
-// ([MN][K]) or, on the 256 x 256 tiles, MN-contiguous ([K][MN]), with 16-byte
+// The NT fast path applies to 16-bit and fp32 operands that are each
+// K-contiguous ([MN][K]) or, on the 256 x 256 tiles, MN-contiguous ([K][MN]), with 16-byte
 // aligned bases and rows; C (and the aux matrix) have unit column stride with
 // 16-byte aligned rows, bias is contiguous, and the shape tiles exactly.
 template <int IN, int OUT>
 bool nt_eligible(const GemmParams& p, int BM, int BN, bool mn_ok) {
   constexpr int ES = IN == IN_F32 ? 4 : 2;
-  mn_ok = mn_ok && ES == 2;  // the transposing LDS read is 16-bit
   auto operand_ok = [&](int mode, int64_t ld_k, int64_t ld_mn, int64_t rows_mn) {
     if (mode == LD_KCONTIG) return (ld_k * ES) % 16 == 0 && rows_mn * ld_k * ES < INT32_MAX;
     if (mode == LD_MNCONTIG && mn_ok) return (ld_mn * ES) % 16 == 0 && p.K * ld_mn * ES < INT32_MAX;
@@ -1520,7 +1542,7 @@ Status run_gemm(GemmParams& p, hipStream_t s) {
     }
   }
   {
-    constexpr bool MN = IN != IN_F32;
+    constexpr bool MN = true;
     const int64_t tiles256 = (p.M / 256) * (p.N / 256);
     const int64_t tiles128 = (p.M / 128) * (p.N / 128);
     // K <= 512 (at most 8 K-steps) with a one-output epilogue (none, bias,

@@ -577,6 +577,27 @@ def test_gemm_f32_tiled_paths(C, M, N, K):
     assert np.all(h(o)[want == 0] == 0)
 
 
+@pytest.mark.parametrize("K", [32, 96, 288])
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (True, True), (False, True)])
+def test_gemm_f32_256_tiles_all_operand_layouts(C, ta, tb, K):
+    """fp32 on the 256x256 tiles with each operand K-contiguous or
+    M/N-contiguous (one 4-byte LDS read per K-row), including the reference's
+    default layout (no transposes: A [M, K], B [K, N]); plain and with the
+    bias+GELU epilogue, vs the fp64 oracle.  K = 32 is one K-step; 96 and
+    288 odd counts."""
+    M, N = 2048, 4096  # 128 tiles of 256 x 256
+    r = rng(K + 2 * ta + tb + 1000)
+    A = r.uniform(-1, 1, (K, M) if ta else (M, K)).astype(np.float32)
+    B = (r.uniform(-1, 1, (N, K) if tb else (K, N)) / np.sqrt(K)).astype(np.float32)
+    bias = r.uniform(-1, 1, N).astype(np.float32)
+    ref = _gemm_ref(A, B, ta, tb)
+    o = torch.empty((M, N), device="cuda")
+    C.op_call(int(C.OpKind.Gemm), [g(A), g(B)], [o], 0, struct.pack("<ii", ta, tb), 0)
+    assert orc.rel_err(h(o), ref) < 1e-4
+    C.op_call(int(C.OpKind.GemmEpilogue), [g(A), g(B), g(bias)], [o], GEPI, struct.pack("<iii", ta, tb, 3), 0)
+    assert orc.rel_err(h(o), orc.gelu_f64(ref + bias[None, :])) < 1e-4
+
+
 @pytest.mark.parametrize("relu", [1, 0])
 @pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, True)])
 def test_gemm_epilogue_f32_gpel(C, relu, ta, tb):
