@@ -129,6 +129,8 @@ def _written_vgprs(line: str) -> set[int]:
         return set()
     if mnem.startswith(("v_cmp", "v_readlane", "v_readfirstlane")):
         return set()
+    if re.search(r"\blds\b", line.split(";")[0]) and "_load" in mnem:
+        return set()  # a direct-to-LDS load writes LDS; its first VGPR is the lane offset it reads
     return _vgprs(ops[0])
 
 
@@ -208,6 +210,8 @@ def test_asm_offset_guard_flags_a_planted_write(asm):
     labels2 = {ln.split(":")[0]: i for i, ln in enumerate(planted) if ln.startswith(".LBB")}
     assert _first_write_before_drain(planted, start, reg, labels2) == start
     assert _written_vgprs("\tds_read_b128 v[4:7], v1 offset:16") == {4, 5, 6, 7}
+    assert _written_vgprs("\tbuffer_load_dwordx4 v3, s[0:3], s16 offen lds") == set()
+    assert _written_vgprs("\tbuffer_load_dwordx4 v[4:7], v3, s[0:3], 0 offen") == {4, 5, 6, 7}
     assert _written_vgprs("\tds_write_b128 v1, v[4:7]") == set()
     assert _is_vm_drain("\ts_waitcnt vmcnt(0) lgkmcnt(0)") and not _is_vm_drain("\ts_waitcnt vmcnt(3)")
 
