@@ -141,6 +141,32 @@ C4_SHAPES = [(1024, 1024, 1024), (4096, 4096, 4096), (8192, 8192, 8192),
 C4_ACTS = {"none": 1, "relu": 0, "gelu": 3}
 
 
+def bench_layouts(C, n=4096, iters=10):
+    """Plain GEMM C[n,n] = op(A) . op(B) at n^3 in the four operand layouts of
+    the reference's gemm op (transA, transB), bf16 and fp32: every layout is
+    read in place, none is transposed first."""
+    import torch
+
+    out = {}
+    for dt, kid in (("bf16", "gemm_bf16_mfma_v0"), ("fp32", "gemm_f32_naive_v0")):
+        tdt = torch.bfloat16 if dt == "bf16" else torch.float32
+        g = torch.Generator(device="cuda")
+        g.manual_seed(n + 5)
+        A = ((torch.rand((n, n), device="cuda", generator=g) * 2 - 1) / math.sqrt(n)).to(tdt)
+        B = ((torch.rand((n, n), device="cuda", generator=g) * 2 - 1) / math.sqrt(n)).to(tdt)
+        Y = torch.empty((n, n), device="cuda", dtype=tdt)
+        peak = PEAK_BF16_TFLOPS if dt == "bf16" else PEAK_FP32_TFLOPS
+        for ta in (0, 1):
+            for tb in (0, 1):
+                pay = struct.pack("<ii", ta, tb)
+                fn = lambda: C.launch_by_id(kid, C.OpKind.Gemm, [A, B], [Y], 0, pay, _cs())  # noqa: E731
+                ms = time_launches(fn, iters, 2)
+                tf = 2.0 * n ** 3 / (ms * 1e-3) / 1e12
+                out[f"gemm_{dt}_{n}^3_{'T' if ta else 'N'}{'T' if tb else 'N'}"] = {
+                    "value": round(tf, 2), "unit": "TFLOP/s", "frac": round(tf / peak, 4), "ms": round(ms, 4)}
+    return out
+
+
 def bench_c4(C, dtype="bf16", shapes=C4_SHAPES, acts=("none", "relu", "gelu"), iters=10):
     """X~U(-1,1)/sqrt(K) [M,K], W [N,K], b [N]; act(X.W^T + b).  bf16: bf16 in,
     fp32 accumulate, bf16 out; fp32: fp32 throughout."""
@@ -1524,6 +1550,9 @@ def main():
             c4 = bench_c4(C, dt, shapes)
             comps.update(c4)
             log(f"[bench] c4 {dt} {c4}")
+        lay = bench_layouts(C)
+        comps.update(lay)
+        log(f"[bench] layouts {lay}")
 
     cpu = None
     if not args.no_cpu:
