@@ -446,7 +446,17 @@ __device__ void raw_buffer_load_lds(i32x4_t rsrc, __attribute__((address_space(3
                                     int size, int voffset, int soffset, int offset,
                                     int aux) __asm("llvm.amdgcn.raw.buffer.load.lds");
 // The same load written as inline asm (M0 = LDS address, set by the
-// compiler through the constraint; the nop covers the M0 -> LDS-DMA hazard).
+// compiler through the constraint).  The compiler's hazard recognizer does
+// not see the vector-memory instruction inside the asm, so the asm covers the
+// hazards of its scalar operands itself: a VMEM read of an SGPR that a VALU
+// instruction wrote (v_readfirstlane / v_readlane into the resource words or
+// the scalar offset) needs 5 wait states, and the M0 write one; s_nop 4
+// provides 5.  (With s_nop 0 a build whose scheduler placed a
+// v_readfirstlane of the resource base right before the asm ended in a GPU
+// memory fault.)  PAD: the loads of a tile's first stages, which follow the
+// resource set-up; the K loop's loads (scalar offsets from SALU adds) keep
+// s_nop 0 for the M0 write, and a codegen test checks every asm load's wait
+// states against the VALU writes before it.
 // The compiler does not know that it writes LDS, so it adds no vmcnt wait in
 // front of the LDS reads that follow it: it cannot prove that a transposing
 // ds_read_b64_tr_b16 does not alias an in-flight direct-to-LDS load, and
@@ -454,12 +464,19 @@ __device__ void raw_buffer_load_lds(i32x4_t rsrc, __attribute__((address_space(3
 // kernel orders every LDS read of a stage after that stage's loads itself
 // (s_waitcnt 0 + barrier at the top of each K-step).  The memory clobber
 // keeps the loads in program order with the LDS reads.
+template <bool PAD>
 __device__ __forceinline__ void asm_buffer_load_lds(i32x4_t rsrc, uint32_t lds_addr, int voffset,
                                                     int soffset) {
-  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
-               :
-               : "v"(voffset), "s"(rsrc), "s"(soffset), "{m0}"(lds_addr)
-               : "memory");
+  if constexpr (PAD)
+    asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+                 :
+                 : "v"(voffset), "s"(rsrc), "s"(soffset), "{m0}"(lds_addr)
+                 : "memory");
+  else
+    asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+                 :
+                 : "v"(voffset), "s"(rsrc), "s"(soffset), "{m0}"(lds_addr)
+                 : "memory");
 }
 __device__ __forceinline__ i32x4_t buffer_rsrc(const void* base, uint32_t bytes) {
   struct __attribute__((packed)) Rsrc {
@@ -994,7 +1011,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt_kernel(NTParams p) {
   // places by itself.
   constexpr bool ASM_LDS = !(AKC && BKC);
   constexpr int NVM = opa.BLOCKS + opb.BLOCKS;  // loads per wave and K-step
-  auto load_one = [&](int kt, int stage, int u) {
+  auto load_one = [&](int kt, int stage, int u, auto PAD) {
     uint8_t* base = smem + stage * STAGE;
     const bool is_a = u < opa.BLOCKS;
     uint8_t* dst = is_a ? base + (wave_s + u * NW) * 1024 : base + A_BYTES + (wave_s + (u - opa.BLOCKS) * NW) * 1024;
@@ -1002,13 +1019,13 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt_kernel(NTParams p) {
     const int voff = is_a ? opa.voff[u] : opb.voff[u - opa.BLOCKS];
     const int soff = kt * (is_a ? opa.soff_step : opb.soff_step);
     if constexpr (ASM_LDS)
-      asm_buffer_load_lds(rsrc, (uint32_t)(uintptr_t)dst, voff, soff);
+      asm_buffer_load_lds<decltype(PAD)::value>(rsrc, (uint32_t)(uintptr_t)dst, voff, soff);
     else
       raw_buffer_load_lds(rsrc, (__attribute__((address_space(3))) unsigned*)dst, 16, voff, soff, 0, 0);
   };
   auto issue_loads = [&](int kt, int stage) {
 #pragma unroll
-    for (int u = 0; u < NVM; ++u) load_one(kt, stage, u);
+    for (int u = 0; u < NVM; ++u) load_one(kt, stage, u, std::true_type{});
   };
 
   nt_acc_t<MS> acc[TN][TM];
@@ -1154,7 +1171,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt_kernel(NTParams p) {
       }
       if constexpr (nv > 0) {
 #pragma unroll
-        for (int u = vlo + Sched::load_lo(t, nv); u < vlo + Sched::load_lo(t + 1, nv); ++u) load_one(lkt, lst, u);
+        for (int u = vlo + Sched::load_lo(t, nv); u < vlo + Sched::load_lo(t + 1, nv); ++u)
+          load_one(lkt, lst, u, std::false_type{});
       }
     }
     Sched::template pin<decltype(R)::value, ASM_LDS ? 0 : nv>();  // asm loads are in no sched group
@@ -1270,6 +1288,17 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt_kernel(NTParams p) {
         substep(Rd{}, z, z, 0, nx, 1, 1, 0, 0);
       }
     }
+  }
+  if constexpr (ASM_LDS) {
+    // The asm loads are hidden from the compiler's hazard tracking: once the
+    // loop has issued its last one, their lane offsets are dead to it and
+    // their registers could be reused while those loads are in flight.  Wait
+    // for them here and keep the offsets live up to this point.
+    __builtin_amdgcn_s_waitcnt(0);
+#pragma unroll
+    for (int t = 0; t < opa.BLOCKS; ++t) asm volatile("" ::"v"(opa.voff[t]));
+#pragma unroll
+    for (int t = 0; t < opb.BLOCKS; ++t) asm volatile("" ::"v"(opb.voff[t]));
   }
   if (kt + 1 < nk) {
     __builtin_amdgcn_s_waitcnt(0);
@@ -1439,16 +1468,16 @@ Status run_nt_layout(const GemmParams& g, hipStream_t s) {
 
 // Operand layouts: K-contiguous ([MN][K]) on every tile configuration;
 // MN-contiguous ([K][MN], read through the transposing LDS loads for 16-bit
-// operands, one 4-byte read per K-row for fp32) on the 256 x 256
-// configuration (MN_OK).
+// operands, one 4-byte read per K-row for fp32) where MN_OK (rows of at
+// least 16 chunks: 256 x 256 and 128 x 128, and 64 x 64 for fp32).
 template <int IN, int OUT, int BM, int BN, int WM, int WN, bool MN_OK, int S = 2>
 Status run_nt(const GemmParams& g, hipStream_t s) {
   const bool akc = g.a_mode == LD_KCONTIG, bkc = g.b_mode == LD_KCONTIG;
   if (akc && bkc) return run_nt_layout<IN, OUT, BM, BN, WM, WN, true, true, S>(g, s);
   if constexpr (MN_OK) {
-    if (akc) return run_nt_layout<IN, OUT, BM, BN, WM, WN, true, false>(g, s);
-    if (bkc) return run_nt_layout<IN, OUT, BM, BN, WM, WN, false, true>(g, s);
-    return run_nt_layout<IN, OUT, BM, BN, WM, WN, false, false>(g, s);
+    if (akc) return run_nt_layout<IN, OUT, BM, BN, WM, WN, true, false, S>(g, s);
+    if (bkc) return run_nt_layout<IN, OUT, BM, BN, WM, WN, false, true, S>(g, s);
+    return run_nt_layout<IN, OUT, BM, BN, WM, WN, false, false, S>(g, s);
   }
   return Status::Internal;  // excluded by nt_eligible
 }
@@ -1476,7 +1505,8 @@ Status run_nt256(const GemmParams& g, hipStream_t s) {
 }
 
 // The NT fast path applies to 16-bit and fp32 operands that are each
-// K-contiguous ([MN][K]) or, on the 256 x 256 tiles, MN-contiguous ([K][MN]), with 16-byte
+// K-contiguous ([MN][K]) or, where the caller allows it (mn_ok: the 256 x 256
+// and 128 x 128 tiles, and fp32 64 x 64), MN-contiguous ([K][MN]), with 16-byte
 // aligned bases and rows; C (and the aux matrix) have unit column stride with
 // 16-byte aligned rows, bias is contiguous, and the shape tiles exactly.
 template <int IN, int OUT>
@@ -1568,20 +1598,32 @@ Status run_gemm(GemmParams& p, hipStream_t s) {
     // than a load's latency).  128 x 128 with 4 stages needs all of LDS, so
     // only where one workgroup per CU is all the grid gives anyway.
     const bool deep = IN != IN_F32 && p.K >= 16 * (128 / (IN == IN_F32 ? 4 : 2));
-    if (tiles128 >= 128 && nt_eligible<IN, OUT>(p, 128, 128, false)) {
+    // 128 x 128 tiles read every operand layout; 64 x 64 tiles M/N-contiguous
+    // operands in fp32 only (a 16-bit row of 64 elements is 8 chunks, fewer
+    // than the transposing reads' swizzle spans), so 16-bit M/N-contiguous
+    // problems with fewer than 128 tiles of 128 x 128 stay on 128 x 128
+    // (2048^3 bf16 NN 112.6 -> 19.8 us, 1024^3 27.4 -> 11.0 us; fp32 1024^3
+    // NN 53.8 -> 19.7 us against the general-stride kernel)
+    constexpr bool MN64 = IN == IN_F32;
+    if (tiles128 >= 128 && nt_eligible<IN, OUT>(p, 128, 128, true)) {
       if constexpr (IN != IN_F32) {
-        if (deep && tiles128 <= 256) return run_nt<IN, OUT, 128, 128, 2, 2, false, 4>(p, s);
+        if (deep && tiles128 <= 256) return run_nt<IN, OUT, 128, 128, 2, 2, true, 4>(p, s);
       }
-      return run_nt<IN, OUT, 128, 128, 2, 2, false>(p, s);
+      return run_nt<IN, OUT, 128, 128, 2, 2, true>(p, s);
     }
     // fewer tiles than CUs at 128x128: 64x64 tiles (4 waves of 32x32)
-    if (nt_eligible<IN, OUT>(p, 64, 64, false)) {
+    if (nt_eligible<IN, OUT>(p, 64, 64, MN64)) {
       if constexpr (IN != IN_F32) {
-        if (deep) return run_nt<IN, OUT, 64, 64, 2, 2, false, 8>(p, s);
+        if (deep) return run_nt<IN, OUT, 64, 64, 2, 2, MN64, 8>(p, s);
       }
-      return run_nt<IN, OUT, 64, 64, 2, 2, false>(p, s);
+      return run_nt<IN, OUT, 64, 64, 2, 2, MN64>(p, s);
     }
-    if (nt_eligible<IN, OUT>(p, 128, 128, false)) return run_nt<IN, OUT, 128, 128, 2, 2, false>(p, s);
+    if (nt_eligible<IN, OUT>(p, 128, 128, true)) {
+      if constexpr (IN != IN_F32) {
+        if (deep) return run_nt<IN, OUT, 128, 128, 2, 2, true, 4>(p, s);
+      }
+      return run_nt<IN, OUT, 128, 128, 2, 2, true>(p, s);
+    }
   }
   // Large problems: 128x128 workgroup tiles (4 waves, 64x64 per wave).
   // Smaller ones: 64x64 tiles so that enough workgroups exist.

@@ -264,3 +264,82 @@ def test_deep_pipeline_keeps_loads_in_flight(asm, kernel, vm):
     waits = [l.strip() for l in main[0] if "s_waitcnt" in l and "vmcnt" in l]
     assert waits == [f"s_waitcnt vmcnt({vm}) lgkmcnt(0)"], waits
     assert sum("s_barrier" in l for l in main[0]) == 1
+
+
+# The inline-asm LDS loads also hide their scalar operands (buffer resource,
+# scalar offset) from the hazard recognizer: a vector-memory read of an SGPR
+# written by a VALU instruction (v_readfirstlane, v_readlane, a v_cmp into an
+# SGPR pair) needs 5 wait states in between, which the compiler does not count
+# for an asm block.  Every such load must have 5 wait states (its own s_nop
+# included) after the last VALU write of an SGPR it reads.
+VMEM_SGPR_WAIT_STATES = 5
+
+
+def _sgprs(tok: str) -> set[int]:
+    m = re.match(r"^s\[(\d+):(\d+)\]$", tok.strip())
+    if m:
+        return set(range(int(m.group(1)), int(m.group(2)) + 1))
+    m = re.match(r"^s(\d+)$", tok.strip())
+    return {int(m.group(1))} if m else set()
+
+
+def asm_load_sgpr_hazards(lines: list[str], need: int = VMEM_SGPR_WAIT_STATES) -> list[tuple[int, str, str]]:
+    """(line, VALU instruction, asm load) for each asm direct-to-LDS load with
+    fewer than `need` wait states after a VALU write of an SGPR it reads,
+    looking back along the fall-through path.  A label reached before `need`
+    wait states is reported too (other paths lead there), as ("label", load)."""
+    out = []
+    for i, ln in enumerate(lines):
+        if "ASMSTART" not in ln:
+            continue
+        j, block = i + 1, []
+        while j < len(lines) and "ASMEND" not in lines[j]:
+            block.append(lines[j].split(";")[0].strip())
+            j += 1
+        load = [b for b in block if b.startswith("buffer_load") and re.search(r"\blds\b", b)]
+        if not load:
+            continue
+        ops = [o.strip() for o in load[0].split(None, 1)[1].replace(" offen lds", "").split(",")]
+        used = set().union(*(_sgprs(o) for o in ops[1:]))
+        ws = 0
+        for b in block:
+            if b.startswith("buffer_load"):
+                break
+            ws += int(b.split()[1]) + 1 if b.startswith("s_nop") else (1 if b else 0)
+        k = i - 1
+        while ws < need and k >= 0:
+            s = lines[k].split(";")[0].strip()
+            k -= 1
+            if not s or s.startswith("."):
+                continue
+            if s.endswith(":"):
+                out.append((i, "label " + s, load[0]))
+                break
+            mnem = s.split()[0]
+            if mnem.startswith("s_nop"):
+                ws += int(s.split()[1]) + 1
+                continue
+            if mnem.startswith("v_") and len(s.split(None, 1)) > 1:
+                if _sgprs(s.split(None, 1)[1].split(",")[0]) & used:
+                    out.append((i, s, load[0]))
+            ws += 1
+    return out
+
+
+def test_asm_lds_loads_wait_for_valu_written_sgprs(asm):
+    lines = asm.splitlines()
+    hazards = asm_load_sgpr_hazards(lines)
+    assert not hazards, hazards[:4]
+    n = sum(1 for ln in lines if re.search(r"buffer_load_dwordx4\s+v\d+,\s*s\[\d+:\d+\],\s*s\d+\s+offen\s+lds", ln))
+    assert n > 100, n
+
+
+def test_asm_sgpr_hazard_check_flags_a_planted_write():
+    lines = ["\tv_readfirstlane_b32 s5, v3", "\t;;#ASMSTART", "\ts_nop 0",
+             "\tbuffer_load_dwordx4 v182, s[4:7], s42 offen lds", "\t;;#ASMEND"]
+    assert len(asm_load_sgpr_hazards(lines)) == 1
+    lines[2] = "\ts_nop 4"
+    assert asm_load_sgpr_hazards(lines) == []
+    far = ["\tv_readfirstlane_b32 s42, v3", "\ts_add_i32 s1, s1, 1", "\ts_add_i32 s2, s2, 1",
+           "\t;;#ASMSTART", "\ts_nop 1", "\tbuffer_load_dwordx4 v182, s[4:7], s42 offen lds", "\t;;#ASMEND"]
+    assert len(asm_load_sgpr_hazards(far)) == 1  # 2 + 2 wait states < 5

@@ -598,6 +598,36 @@ def test_gemm_f32_256_tiles_all_operand_layouts(C, ta, tb, K):
     assert orc.rel_err(h(o), orc.gelu_f64(ref + bias[None, :])) < 1e-4
 
 
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("M,N,K", [(1024, 1024, 1024), (2048, 2048, 256), (1024, 512, 2048), (512, 256, 64)])
+@pytest.mark.parametrize("ta,tb", [(False, False), (True, False), (True, True)])
+def test_gemm_small_tiles_mn_contiguous_operands(C, ta, tb, M, N, K, dt):
+    """Problems with fewer than 128 tiles of 256 x 256 in the layouts with an
+    M/N-contiguous operand: 128 x 128 tiles (4 LDS stages for 16-bit with
+    >= 16 K-steps), and 64 x 64 tiles for fp32 (1024^3, 512 x 256), plain
+    and with bias+ReLU, vs the fp64 oracle."""
+    r = rng(M + N + K + 4 * ta + 2 * tb + (dt == "bf16"))
+    A = r.uniform(-1, 1, (K, M) if ta else (M, K)).astype(np.float32)
+    B = (r.uniform(-1, 1, (N, K) if tb else (K, N)) / np.sqrt(K)).astype(np.float32)
+    bias = r.uniform(-1, 1, N).astype(np.float32)
+    if dt == "bf16":
+        Ab, Bb = orc.bf16_bits_from_f32(A), orc.bf16_bits_from_f32(B)
+        A = orc.bf16_bits_to_f32(Ab).reshape(A.shape)
+        B = orc.bf16_bits_to_f32(Bb).reshape(B.shape)
+        ta_, tb_ = g(Ab, torch.bfloat16), g(Bb, torch.bfloat16)
+        o = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+        back, tol = (lambda t: orc.bf16_bits_to_f32(h(t)).reshape(M, N)), 1e-2
+    else:
+        ta_, tb_ = g(A), g(B)
+        o = torch.empty((M, N), device="cuda")
+        back, tol = h, 1e-4
+    ref = _gemm_ref(A, B, ta, tb)
+    C.op_call(int(C.OpKind.Gemm), [ta_, tb_], [o], 0, struct.pack("<ii", ta, tb), 0)
+    assert orc.rel_err(back(o), ref) < tol
+    C.op_call(int(C.OpKind.GemmEpilogue), [ta_, tb_, g(bias)], [o], GEPI, struct.pack("<iii", ta, tb, 0), 0)
+    assert orc.rel_err(back(o), np.maximum(ref + bias[None, :], 0)) < tol
+
+
 @pytest.mark.parametrize("relu", [1, 0])
 @pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, True)])
 def test_gemm_epilogue_f32_gpel(C, relu, ta, tb):
