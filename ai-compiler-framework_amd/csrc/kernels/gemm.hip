@@ -1579,10 +1579,14 @@ Status run_gemm(GemmParams& p, hipStream_t s) {
     // ReLU): a 256 x 256 tile's loads and stores are no longer covered by its
     // MFMA work, and 128 x 128 tiles, two workgroups per CU, overlap one
     // tile's epilogue with another's K loop (8192 x 4096 x 256: 30.5 vs 36
-    // us, x 512: 42.7 vs 46).  The GELU epilogues stay on 256 x 256 (x 512:
-    // 45 vs 48-50 us).  K-contiguous operands only; the others keep 256.
-    if (p.K <= 512 && (p.act == ACT_NONE || p.act == ACT_RELU) && tiles128 >= 256 &&
-        (p.K <= 256 || IN == IN_F32) && nt_eligible<IN, OUT>(p, 128, 128, false))
+    // us, x 512: 42.7 vs 46).  16-bit bias+GELU without the pre-activation
+    // output too at K <= 256 (x 256: 33.4 vs 36.5 us on the 8-wave 256 x 256
+    // tiles); at K = 512 GELU stays on 256 x 256 (45 vs 48-50 us).
+    // K-contiguous operands only; the others keep 256.
+    const bool one_out = p.act == ACT_NONE || p.act == ACT_RELU ||
+                         (IN != IN_F32 && p.act == ACT_GELU && !p.aux && p.K <= 256);
+    if (p.K <= 512 && one_out && tiles128 >= 256 && (p.K <= 256 || IN == IN_F32) &&
+        nt_eligible<IN, OUT>(p, 128, 128, false))
       return run_nt<IN, OUT, 128, 128, 2, 2, false>(p, s);
     // Other 16-bit GEMMs with K <= 512 and at least one 256 x 256 tile per
     // CU: the 8-wave persistent tiles (8192 x 4096 x 512: 41.4 vs 46.0 us
