@@ -902,10 +902,16 @@ struct NTSched {
 // the bytes a resource spans fit a signed 32-bit offset.
 // fp32 (ES 4): a fragment read takes one row k and the row k + 4 in the two
 // halves of the wave (32 consecutive floats each), so rows k and k + 4 sit
-// 8 chunks (32 banks) apart.
-template <int MS, int ES = 2>
+// 8 chunks (32 banks) apart.  16-bit rows of 8 chunks (64-wide tiles): a
+// transposing read's 32-lane pass covers rows {0-3, 8-11} (+ 16 k) with 32
+// bytes each; rows of one parity share a 128-byte bank half, so the four of
+// them take the four 32-byte slots: chunk pair XOR (bit 1, bit 3) of k.
+// Every form keeps rows k and k + 4 (k % 8 < 4) alike, as the fragment's
+// second read (4 rows on) reuses the first one's column.
+template <int MS, int ES = 2, int CPR = 16>
 __device__ __forceinline__ int nt_mn_swizzle(int k) {
   if constexpr (ES == 4) return 8 * ((k >> 2) & 1);
+  if constexpr (CPR == 8) return 2 * (((k >> 1) & 1) | (((k >> 3) & 1) << 1));
   return MS == 16 ? ((4 * (k & 3)) ^ (2 * ((k >> 3) & 1))) : 4 * (k & 3);
 }
 
@@ -916,7 +922,7 @@ struct NTOperand {
   static constexpr int ROWB = BMN * ES;              // MN-contiguous row bytes
   static constexpr int CPR = ROWB / 16;              // chunks per MN-contiguous row
   static_assert(BYTES % (1024 * NW) == 0, "load blocks must split evenly over waves");
-  static_assert(KC || CPR >= 16, "MN-contiguous tiles: >= 16 chunks per row");
+  static_assert(KC || CPR >= 16 || (ES == 2 && CPR == 8), "MN-contiguous tiles: >= 16 chunks per row, or 8 (16-bit)");
 
   i32x4_t rsrc;
   int voff[BLOCKS];
@@ -946,7 +952,7 @@ __device__ __forceinline__ void nt_operand_init(NTOperand<KC, BMN, NW, ES>& o, c
     for (int t = 0; t < o.BLOCKS; ++t) {
       const int q = wave + t * NW;
       const int k = q * RPB + lane / CPR;
-      const int c = (lane % CPR) ^ nt_mn_swizzle<MS, ES>(k);
+      const int c = (lane % CPR) ^ nt_mn_swizzle<MS, ES, CPR>(k);
       o.voff[t] = k * (int)ld * ES + c * 16;
     }
     o.soff_step = 128 * (int)ld;  // 128 / ES K-rows per stage
@@ -1041,11 +1047,13 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt_kernel(NTParams p) {
   // 32 x 32: groups 0/1 take MN + 0/16 of K-rows 0-7, groups 2/3 K-rows
   // 8-15; 16 x 16: group g takes K-rows 8 g .. 8 g + 7 of the same 16 MN
   const int tr_row = MS == 32 ? (8 * (g16 >> 1) + (i16 >> 2)) : (8 * g16 + (i16 >> 2));
-  auto tr_col = [&](int mb) {  // byte offset of the lane's 8-byte piece in a K-row
+  // byte offset of the lane's 8-byte piece in a K-row of `cpr` chunks
+  auto tr_col = [&](int mb, auto CPR_) {
+    constexpr int cpr = decltype(CPR_)::value;
     if constexpr (MS == 32)
       return ((((mb >> 3) ^ (4 * ((i16 >> 2) & 3))) + 2 * (g16 & 1) + ((i16 >> 1) & 1)) * 16) + 8 * (i16 & 1);
     else
-      return ((((mb >> 3) ^ nt_mn_swizzle<MS>(tr_row)) + ((i16 >> 1) & 1)) * 16) + 8 * (i16 & 1);
+      return ((((mb >> 3) ^ nt_mn_swizzle<MS, 2, cpr>(tr_row)) + ((i16 >> 1) & 1)) * 16) + 8 * (i16 & 1);
   };
   // fp32 M/N-contiguous: lane (fr, fh) holds element mb + fr of K-rows
   // 4 fh .. 4 fh + 3 of the sub-step (four 4-byte reads, one per K-row);
@@ -1059,13 +1067,13 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_nt_kernel(NTParams p) {
   for (int j = 0; j < TM; ++j) {
     const int mb = wm * WTM + j * MS;
     if constexpr (AKC) a_off[j] = (mb + fr) * 128;
-    else a_off[j] = ES == 4 ? mn32_off(mb, BM * ES) : tr_row * (BM * 2) + tr_col(mb);
+    else a_off[j] = ES == 4 ? mn32_off(mb, BM * ES) : tr_row * (BM * 2) + tr_col(mb, template_int_t<BM * 2 / 16>{});
   }
 #pragma unroll
   for (int i = 0; i < TN; ++i) {
     const int nb = wn * WTN + i * MS;
     if constexpr (BKC) b_off[i] = A_BYTES + (nb + fr) * 128;
-    else b_off[i] = A_BYTES + (ES == 4 ? mn32_off(nb, BN * ES) : tr_row * (BN * 2) + tr_col(nb));
+    else b_off[i] = A_BYTES + (ES == 4 ? mn32_off(nb, BN * ES) : tr_row * (BN * 2) + tr_col(nb, template_int_t<BN * 2 / 16>{}));
   }
 
   typedef short v4i16 __attribute__((ext_vector_type(4)));
@@ -1602,13 +1610,10 @@ Status run_gemm(GemmParams& p, hipStream_t s) {
     // than a load's latency).  128 x 128 with 4 stages needs all of LDS, so
     // only where one workgroup per CU is all the grid gives anyway.
     const bool deep = IN != IN_F32 && p.K >= 16 * (128 / (IN == IN_F32 ? 4 : 2));
-    // 128 x 128 tiles read every operand layout; 64 x 64 tiles M/N-contiguous
-    // operands in fp32 only (a 16-bit row of 64 elements is 8 chunks, fewer
-    // than the transposing reads' swizzle spans), so 16-bit M/N-contiguous
-    // problems with fewer than 128 tiles of 128 x 128 stay on 128 x 128
-    // (2048^3 bf16 NN 112.6 -> 19.8 us, 1024^3 27.4 -> 11.0 us; fp32 1024^3
-    // NN 53.8 -> 19.7 us against the general-stride kernel)
-    constexpr bool MN64 = IN == IN_F32;
+    // 128 x 128 and 64 x 64 tiles read every operand layout (2048^3 bf16 NN
+    // 112.6 -> 19.8 us, fp32 1024^3 NN 53.8 -> 19.7 us against the
+    // general-stride kernel)
+    constexpr bool MN64 = true;
     if (tiles128 >= 128 && nt_eligible<IN, OUT>(p, 128, 128, true)) {
       if constexpr (IN != IN_F32) {
         if (deep && tiles128 <= 256) return run_nt<IN, OUT, 128, 128, 2, 2, true, 4>(p, s);
