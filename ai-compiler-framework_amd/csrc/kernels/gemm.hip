@@ -1594,8 +1594,12 @@ Status run_gemm(GemmParams& p, hipStream_t s) {
     const bool one_out = p.act == ACT_NONE || p.act == ACT_RELU ||
                          (IN != IN_F32 && p.act == ACT_GELU && !p.aux && p.K <= 256);
     if (p.K <= 512 && one_out && tiles128 >= 256 && (p.K <= 256 || IN == IN_F32) &&
-        nt_eligible<IN, OUT>(p, 128, 128, false))
+        nt_eligible<IN, OUT>(p, 128, 128, false)) {
+      // 16-bit: 8 waves of 64 x 32 (8192 x 4096 x 256: 28.3 vs 29.4-31.3 us
+      // none, 33.7 vs 35.2-36.0 GELU against 4 waves of 64 x 64)
+      if constexpr (IN != IN_F32) return run_nt<IN, OUT, 128, 128, 2, 4, false>(p, s);
       return run_nt<IN, OUT, 128, 128, 2, 2, false>(p, s);
+    }
     // Other 16-bit GEMMs with K <= 512 and at least one 256 x 256 tile per
     // CU: the 8-wave persistent tiles (8192 x 4096 x 512: 41.4 vs 46.0 us
     // none, 48.0 vs 52.5 GELU; x 256 with GELU: 38.4 vs 42.2 us against the
