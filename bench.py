@@ -1091,13 +1091,14 @@ def pmc_report(fetch_csv, write_csv, mfma_csv=None, trace_csv=None):
 SR, SC = 16384, 32768
 STREAMING = [
     ("row softmax (+max, +sum) 16384x1024 f32", "row_reg_kernel<128, 2, 0>", 8 * SR * 1024 + 8 * SR),
-    ("row softmax (+max, +sum) 16384x8192 f32", "row_reg_kernel<512, 4, 0>", 8 * SR * 8192 + 8 * SR),
+    ("row softmax (+max, +sum) 16384x8192 f32", "row_reg_kernel<128, 16, 0>", 8 * SR * 8192 + 8 * SR),
     ("row softmax (+max, +sum) 16384x32768 f32", "row_reg_kernel<512, 16, 0>", 8 * SR * SC + 8 * SR),
     ("row sum 16384x32768 f32", "row_reg_kernel<512, 16, 1>", 4 * SR * SC + 4 * SR),
     ("row max 16384x32768 f32", "row_reg_kernel<512, 16, 2>", 4 * SR * SC + 4 * SR),
-    ("softmax xent fwd+bwd 16384x8192 f32", "row_reg_kernel<512, 4, 3>", 8 * SR * 8192 + 16 * SR),
+    ("softmax xent fwd+bwd 16384x8192 f32", "row_reg_kernel<128, 16, 3>", 8 * SR * 8192 + 16 * SR),
     ("mse loss+grad 8192x4096 (bf16 p, f32 t, bf16 grad)", "mse_loss_grad_oneshot", 8 * 8192 * 4096),
     ("bias grad colsum 8192x4096 bf16 -> f32", "colsum_vec_kernel", 2 * 8192 * 4096 + 4 * 4096),
+    ("column sum, one output 8192x4096 bf16 -> f32", "colsum_narrow_kernel", 2 * 8192 * 4096 + 4 * 4096),
     ("AdamW 2^28 f32 (P,G,M,V in; P,M,V out)", "adamw_vec4_kernel", 28 * (1 << 28)),
 ]
 
@@ -1141,6 +1142,8 @@ def streaming_only(C):
     o, opart = torch.empty(4096, device="cuda"), torch.empty((64, 4096), device="cuda")
     for _ in range(3):
         C.launch_by_id("reduce_sum_keep_lastdim_bf16_to_f32_v0", C.OpKind.ReduceSum, [d], [o, opart])
+    for _ in range(3):
+        C.launch_by_id("reduce_sum_keep_lastdim_bf16_to_f32_v0", C.OpKind.ReduceSum, [d], [o])
     del pb, t, d
     n = 1 << 28
     P = torch.randn(n, device="cuda", generator=g) * 0.02
@@ -1157,7 +1160,7 @@ def streaming_only(C):
     for _ in range(3):
         C.launch_by_id("copy_bf16_v0", C.OpKind.Copy, [xc], [yc], 0, b"")
     torch.cuda.synchronize()
-    log("[bench] streaming-only: 9 kernels x 3 dispatches, 3 calibration copies")
+    log("[bench] streaming-only: 10 kernels x 3 dispatches, 3 calibration copies")
 
 
 def pmc_streaming_report(fetch_csv, write_csv):
