@@ -57,6 +57,25 @@ inline bool is_contig_2d_rowmajor(const TensorDesc& t) {
 
 inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
+// Byte range [lo, hi) that a view with non-negative strides can touch.
+struct Span {
+  uintptr_t lo, hi;
+};
+inline Span span_of(const TensorDesc& t) {
+  const int64_t es = dt(t) == DType::kF32 || dt(t) == DType::kI32 ? 4 : 2;
+  int64_t last = 0;
+  for (int i = 0; i < t.rank && i < AICF_MAX_RANK; ++i) {
+    if (t.shape[i] <= 0) return {0, 0};  // touches nothing
+    last += (t.shape[i] - 1) * t.stride[i];
+  }
+  const uintptr_t lo = reinterpret_cast<uintptr_t>(t.data);
+  return {lo, lo + (uintptr_t)((last + 1) * es)};
+}
+inline bool overlap(const Span& a, const Span& b) { return a.lo < b.hi && b.lo < a.hi; }
+// Whether two views can touch a common byte (a written view against one the
+// same kernel reads or writes).
+inline bool views_overlap(const TensorDesc& a, const TensorDesc& b) { return overlap(span_of(a), span_of(b)); }
+
 // Flatten leading dims into M, keep the last dim as N (rank >= 2).
 inline bool rows_cols(const TensorDesc& t, int64_t* M, int64_t* N) {
   if (t.rank < 2 || t.rank > AICF_MAX_RANK) return false;

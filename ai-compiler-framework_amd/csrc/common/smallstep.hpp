@@ -24,8 +24,11 @@ struct SmallGemm {
   int relu;           // relu(acc + bias)
 };
 
-// Output tiles (16 x 16) below which the dispatcher uses small_gemm_f32.
-constexpr int64_t kSmallGemmMaxTiles = 4096;
+// The GEMM dispatcher sends an fp32 problem with fewer than this many
+// 64 x 64 output tiles to small_gemm_f32 (at most 127 such tiles, i.e. 2032
+// tiles of 16 x 16); the lowering's gradient-group jobs use the same bound
+// (SMALL_GEMM_MAX_TILES64 in python/aicf_hip/lower.py).
+constexpr int64_t kSmallGemmMaxTiles64 = 128;
 
 // True when small_gemm_f32 takes the problem (sizes within int range, unit
 // column stride of C).

@@ -876,6 +876,15 @@ bool mse_colsum_check(const TensorDesc* in, int ni, const TensorDesc* out, int n
   const int64_t gx = (N + 64 * VEC - 1) / (64 * VEC);
   if (gx * parts > INT32_MAX || parts > 65535) return false;
   if (dt(LP) != DType::kF32 || !LP.contiguous || numel_of(LP) < gx * parts) return false;
+  // the written buffers (the step counter aside, updated in place) touch
+  // nothing the kernel reads and not each other
+  const TensorDesc* w[4] = {&G, &L, &LP, &CP};
+  for (int x = 0; x < 4; ++x) {
+    for (int y = x + 1; y < 4; ++y)
+      if (views_overlap(*w[x], *w[y])) return false;
+    for (const TensorDesc* r : {&P, &T, &S})
+      if (views_overlap(*w[x], *r)) return false;
+  }
   return aligned(P.data, 16) && aligned(G.data, 16) && aligned(T.data, 16);
 }
 bool mse_colsum_sup(const TensorDesc* i, int ni, const TensorDesc* o, int no, const void* a) {

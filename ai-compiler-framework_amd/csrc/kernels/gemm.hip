@@ -1560,7 +1560,7 @@ Status run_gemm(GemmParams& p, hipStream_t s) {
     // over the waves of a workgroup reaches more CUs than any tiled
     // configuration, and reads every operand layout in place
     const int64_t tiles64 = ((p.M + 63) / 64) * ((p.N + 63) / 64);
-    if (tiles64 < 128 && (p.act == ACT_NONE || p.act == ACT_RELU) && p.c_cs == 1 && !p.aux) {
+    if (tiles64 < kSmallGemmMaxTiles64 && (p.act == ACT_NONE || p.act == ACT_RELU) && p.c_cs == 1 && !p.aux) {
       SmallGemm g{};
       g.A = (const float*)p.A;
       g.B = (const float*)p.B;

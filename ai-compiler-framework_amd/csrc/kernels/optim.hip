@@ -610,16 +610,6 @@ CadwAttr read_cadw(const void* attr) {
   return c;
 }
 
-// whether the byte ranges of two contiguous tensors (f32, i32 or 16-bit) meet
-bool overlaps(const TensorDesc& x, const TensorDesc& y) {
-  auto bytes = [](const TensorDesc& t) {
-    return (uintptr_t)(numel_of(t) * (dt(t) == DType::kF32 || dt(t) == DType::kI32 ? 4 : 2));
-  };
-  const uintptr_t a0 = (uintptr_t)x.data, a1 = a0 + bytes(x);
-  const uintptr_t b0 = (uintptr_t)y.data, b1 = b0 + bytes(y);
-  return a0 < b1 && b0 < a1;
-}
-
 bool colsum_adamw_fill(const TensorDesc* in, int ni, const TensorDesc* out, int no, const void* attr,
                        ColsumAdamWParams* qp) {
   const CadwAttr c = read_cadw(attr);
@@ -650,10 +640,10 @@ bool colsum_adamw_fill(const TensorDesc* in, int ni, const TensorDesc* out, int 
   const TensorDesc* w[5] = {&G, &P, &M, &V, &W};
   for (int x = 0; x < 5; ++x) {
     for (int y = x + 1; y < 5; ++y)
-      if (overlaps(*w[x], *w[y])) return false;
+      if (views_overlap(*w[x], *w[y])) return false;
     for (int t = 0; t < c.T; ++t)
-      if (overlaps(*w[x], in[t])) return false;
-    if (overlaps(*w[x], S)) return false;
+      if (views_overlap(*w[x], in[t])) return false;
+    if (views_overlap(*w[x], S)) return false;
   }
   q.n = n;
   q.G = (float*)G.data;

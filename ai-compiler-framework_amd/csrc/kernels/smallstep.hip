@@ -335,10 +335,13 @@ bool xent_head_sup(const TensorDesc* in, int ni, const TensorDesc* out, int no, 
       return false;
   if (!i32_vec(out[2], B) || !f32_vec(out[3], B) || !f32_rows(out[4], B, K) || !f32_rows(out[5], B, K))
     return false;
-  // the written tensors may not alias what the kernel still reads
-  for (int o = 0; o < 6; ++o)
+  // the written tensors touch nothing the kernel reads and not each other
+  for (int o = 0; o < 6; ++o) {
     for (int i = 0; i < 5; ++i)
-      if (out[o].data == in[i].data) return false;
+      if (views_overlap(out[o], in[i])) return false;
+    for (int q = o + 1; q < 6; ++q)
+      if (views_overlap(out[o], out[q])) return false;
+  }
   return B <= INT32_MAX;
 }
 
@@ -474,19 +477,6 @@ bool read_group(const void* attr, int ni, int no, GroupRec* recs, int* n) {
   *n = cnt;
   return true;
 }
-
-// Byte range a view can touch (positive strides).
-struct Span {
-  uintptr_t lo, hi;
-};
-Span span_of(const TensorDesc& t) {
-  const int es = dt(t) == DType::kF32 || dt(t) == DType::kI32 ? 4 : 2;
-  int64_t last = 0;
-  for (int i = 0; i < t.rank; ++i) last += (t.shape[i] - 1) * t.stride[i];
-  const uintptr_t lo = reinterpret_cast<uintptr_t>(t.data);
-  return {lo, lo + (uintptr_t)((last + 1) * es)};
-}
-bool overlap(const Span& a, const Span& b) { return a.lo < b.hi && b.lo < a.hi; }
 
 bool group_fill(const TensorDesc* in, int ni, const TensorDesc* out, int no, const void* attr,
                 GroupArgs* ga) {

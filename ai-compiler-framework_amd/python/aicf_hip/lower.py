@@ -41,7 +41,7 @@ format the reference executor consumes (lower.py:9-21, exec.py:393-453).
 """
 from __future__ import annotations
 
-from typing import Any, Dict, List, Optional
+from typing import Any, Dict, Iterable, List, Optional
 
 from .ir import IRGraph
 
@@ -558,6 +558,11 @@ def fuse_colsum_into_dgelu(ir: IRGraph, lowered: Lowered) -> Lowered:
 MAX_COLSUM_ADAMW = 8
 
 
+# bf16 columns per lane of the mse_colsum kernel (kMseColsumVecBf16 in
+# csrc/kernels/eltwise.hip)
+MSE_COLSUM_VEC_BF16 = 8
+
+
 def fuse_step_tail(ir: IRGraph, lowered: Lowered) -> Lowered:
     """StageG (not in the reference): for a step with
         mse_loss(y, t) -> (dY, loss, ws);  reduce_sum(dY) -> (db_L, P_ws)
@@ -631,9 +636,10 @@ def fuse_step_tail(ir: IRGraph, lowered: Lowered) -> Lowered:
         pos += _numel(ir, d)
     if pos != s + n:
         return lowered
-    # the db values are read by nothing else (the bias step reads G)
-    for it in low:
-        if any(int(x) in db_of for x in it["inputs"]):
+    # the db values are read by nothing but the bias step this replaces (it
+    # reads G, which is the one db value itself when there is one layer)
+    for i, it in enumerate(low):
+        if i != ia and any(int(x) in db_of for x in it["inputs"]):
             return lowered
     dev = ir.values[dY].device
     part = {}
@@ -650,6 +656,12 @@ def fuse_step_tail(ir: IRGraph, lowered: Lowered) -> Lowered:
                                dtype="torch.float32", device=dev).id
     y, t = (int(x) for x in low[im]["inputs"])
     loss, ws = int(low[im]["outputs"][1]), int(low[im]["outputs"][2])
+    # mse_colsum writes one loss partial per workgroup: ceil(N / (64 lanes x
+    # MSE_COLSUM_VEC_BF16 columns)) x P; mse_loss's buffer may be smaller
+    need = -(-N // (64 * MSE_COLSUM_VEC_BF16)) * P
+    if _numel(ir, ws) < need or not _f32(ir, ws):
+        ws = ir.new_value(name=f"{ir.values[loss].name}.colsum_partials", shape=(need,), dtype="torch.float32",
+                          device=dev).id
     msc = _item("mse_colsum", [y, t, step], [dY, loss, ws, part[dbL], step], dict(low[im]["attrs"]))
     for d, i in db_of.items():
         if i is not None:
@@ -674,6 +686,10 @@ def fuse_step_tail(ir: IRGraph, lowered: Lowered) -> Lowered:
 # ---------------------------------------------------------------- StageF
 GJ_GEMM, GJ_COLSUM, GJ_MEAN, GJ_STEP = 0, 1, 2, 3
 MAX_GROUP_JOBS = 8
+# fp32 GEMMs with fewer 64 x 64 output tiles than this run on the small-GEMM
+# kernel (kSmallGemmMaxTiles64 in csrc/common/smallstep.hpp, which the GEMM
+# dispatcher uses); only those are grouped as gradient-group jobs
+SMALL_GEMM_MAX_TILES64 = 128
 MAX_ADAMW_TENSORS = 8
 
 
@@ -689,9 +705,27 @@ def _base(ir: IRGraph, vid: int) -> int:
     return _base_and_offset(ir, int(vid))[0]
 
 
-def drop_dead_saves(ir: IRGraph, lowered: Lowered) -> Lowered:
+def _aligned16(ir: IRGraph, vid: int) -> bool:
+    """The value starts 16 bytes into a 16-byte boundary of its buffer: base
+    allocations do; a view (IR views are contiguous, row-major slices of
+    their base) when its element offset, in the base's element size, is a
+    multiple of 16 bytes."""
+    base, off = _base_and_offset(ir, int(vid))
+    es = 2 if "float16" in _dt(ir, base) else 4  # bf16/f16 are 2 bytes, f32/i32 4
+    return (int(off) * es) % 16 == 0
+
+
+def drop_dead_saves(ir: IRGraph, lowered: Lowered, keep: Iterable[int] = ()) -> Lowered:
     """copy_saved(src) -> dst where nothing after the copy writes src (or its
-    base buffer): the readers of dst read src instead and the copy goes."""
+    base buffer): the readers of dst read src instead and the copy goes.
+    Once the copy is gone dst is never written, so the copy stays when
+    anything else could read dst: an op before the copy (it reads the
+    previous step's save), or the caller after the step (dst in `keep`, or
+    bound by the caller as an input or a parameter)."""
+    from .plan import ROLE_STATIC, build_binding_plan
+
+    keep = {int(v) for v in keep}
+    plan = build_binding_plan(ir)
     out = [dict(it, inputs=list(it["inputs"]), outputs=list(it["outputs"])) for it in lowered]
     drop = set()
     for i, it in enumerate(out):
@@ -699,6 +733,10 @@ def drop_dead_saves(ir: IRGraph, lowered: Lowered) -> Lowered:
             continue
         src, dst = int(it["inputs"][0]), int(it["outputs"][0])
         if ir.values[src].view_of or ir.values[dst].view_of:
+            continue
+        if dst in keep or plan.role_of(dst) != ROLE_STATIC:
+            continue
+        if any(int(v) == dst for x in out[:i] for v in x["inputs"]):
             continue
         later = out[i + 1:]
         if any(_base(ir, o) == src for x in later for o in x["outputs"]):
@@ -719,7 +757,9 @@ def _head_shapes_ok(ir: IRGraph, H: int, W: int, b: int, t: int, L: int, S: int)
     C = sh(W)[0]
     return (sh(W) == (C, K) and sh(b) == (C,) and sh(t) == (B,) and sh(L) == (B, C) and sh(S) == (B, K)
             and K % 4 == 0 and 4 <= K <= 2048 and 1 <= C <= 32 and "int32" in _dt(ir, t)
-            and all(_f32(ir, v) for v in (H, W, b, L, S)))
+            and all(_f32(ir, v) for v in (H, W, b, L, S))
+            # xent_head reads H, W and S with 16-byte loads (K % 4 keeps every row aligned)
+            and all(_aligned16(ir, v) for v in (H, W, S)))
 
 
 def fuse_xent_head(ir: IRGraph, lowered: Lowered) -> Lowered:
@@ -763,7 +803,7 @@ def fuse_xent_head(ir: IRGraph, lowered: Lowered) -> Lowered:
             i += 1
             continue
         dH, S, dX = int(out[d]["outputs"][0]), int(out[r]["inputs"][1]), int(out[r]["outputs"][0])
-        if not _head_shapes_ok(ir, H, W, b, t, L, S):
+        if not _head_shapes_ok(ir, H, W, b, t, L, S) or not (_aligned16(ir, dH) and _aligned16(ir, dX)):
             i += 1
             continue
         bases_fixed = {_base(ir, v) for v in (W, S, H, dY, b, t)}
@@ -788,7 +828,10 @@ def fuse_xent_head(ir: IRGraph, lowered: Lowered) -> Lowered:
 
 
 def _job_of(ir: IRGraph, it: Dict[str, Any]) -> Optional[tuple]:
-    """(type, inputs, outputs, f0, f1) when the op can run as a grad_group job."""
+    """(type, inputs, outputs, f0, f1) when the op can run as a grad_group job.
+    The jobs read any offset (the small GEMM falls back to 4-byte loads off a
+    16-byte boundary) and need unit column strides, which IR values (base
+    buffers and contiguous views of them) always have."""
     k = _kind(it)
     ins, outs = [int(x) for x in it["inputs"]], [int(x) for x in it["outputs"]]
     attrs = it.get("attrs", {}) or {}
@@ -799,7 +842,7 @@ def _job_of(ir: IRGraph, it: Dict[str, Any]) -> Optional[tuple]:
         ta, tb = bool(attrs.get("transA", False)), bool(attrs.get("transB", False))
         M = sa[1] if ta else sa[0]
         N = sb[0] if tb else sb[1]
-        if ((M + 63) // 64) * ((N + 63) // 64) >= 128:  # the GEMM dispatcher's small-problem bound
+        if ((M + 63) // 64) * ((N + 63) // 64) >= SMALL_GEMM_MAX_TILES64:
             return None
         return (GJ_GEMM, ins, outs, int(ta), int(tb))
     if k == "reduce_sum" and len(ins) == 1 and len(outs) == 1 and int(attrs.get("axis", 0)) == 0 \
@@ -888,7 +931,9 @@ def fuse_adamw_multi(ir: IRGraph, lowered: Lowered) -> Lowered:
     for it in lowered:
         ok = (_kind(it) == "adamw_step" and len(it["inputs"]) == 5 and len(it["outputs"]) == 3
               and [int(x) for x in it["outputs"]] == [int(it["inputs"][k]) for k in (0, 2, 3)]
-              and all(_f32(ir, int(v)) for v in it["inputs"][:4]))
+              and all(_f32(ir, int(v)) for v in it["inputs"][:4])
+              # adamw_multi moves whole 16-byte vectors (adamw_step has an unaligned fallback)
+              and all(_aligned16(ir, int(v)) for v in it["inputs"][:4]))
         if ok and run:
             used = {_base(ir, int(v)) for r in run for v in r["inputs"][:4]}
             if key(it) != key(run[0]) or len(run) >= MAX_ADAMW_TENSORS or \
@@ -903,10 +948,10 @@ def fuse_adamw_multi(ir: IRGraph, lowered: Lowered) -> Lowered:
     return out
 
 
-def fuse_small_step(ir: IRGraph, lowered: Lowered) -> Lowered:
+def fuse_small_step(ir: IRGraph, lowered: Lowered, keep: Iterable[int] = ()) -> Lowered:
     """StageF: drop_dead_saves -> fuse_xent_head -> group_small_jobs ->
-    fuse_adamw_multi."""
-    low = drop_dead_saves(ir, lowered)
+    fuse_adamw_multi.  keep: values the caller reads after the step."""
+    low = drop_dead_saves(ir, lowered, keep)
     low = fuse_xent_head(ir, low)
     low = group_small_jobs(ir, low)
     low = fuse_adamw_multi(ir, low)
@@ -917,12 +962,14 @@ def fuse_small_step(ir: IRGraph, lowered: Lowered) -> Lowered:
 def compile_lowered(ir: IRGraph, *, fuse: bool = True, fuse_bias: bool = False,
                     nt_layout: Any = False, nt_min_flops: float = 2.0 ** 30,
                     fuse_optimizer: bool = False, fuse_colsum: bool = False,
-                    fuse_small: bool = False, fuse_tail: bool = False) -> Lowered:
+                    fuse_small: bool = False, fuse_tail: bool = False,
+                    keep_values: Iterable[int] = ()) -> Lowered:
     """StageA -> StageC -> (StageC') -> (StageD) -> (StageE) -> (StageF) -> (StageG) -> StageB.
     nt_layout: False (no StageD), True / "all" (transpose every M/N-contiguous
     16-bit operand) or "cost" (transpose only where that is cheaper than
     reading it in place); fuse_colsum: StageC'; fuse_optimizer: StageE;
-    fuse_small: StageF; fuse_tail: StageG."""
+    fuse_small: StageF; fuse_tail: StageG.  keep_values: value ids the caller
+    reads after a step, which the rewrites must keep writing."""
     low = lower_to_backend_ops(ir)
     if fuse:
         low = fuse_gemm_epilogue(ir, low, fuse_bias=fuse_bias)
@@ -934,7 +981,7 @@ def compile_lowered(ir: IRGraph, *, fuse: bool = True, fuse_bias: bool = False,
     if fuse_optimizer:
         low = fuse_optimizer_into_gemms(ir, low)
     if fuse_small:
-        low = fuse_small_step(ir, low)
+        low = fuse_small_step(ir, low, keep_values)
     if fuse_tail:
         low = fuse_step_tail(ir, low)
     return apply_kernel_selection(ir, low)

@@ -8,6 +8,7 @@ from __future__ import annotations
 
 import struct
 
+import numpy as np
 import pytest
 
 from aicf_cuda import abi
@@ -202,3 +203,99 @@ def test_xent_head_refuses_what_the_kernel_cannot_run(lib):
     ins, outs = args()
     ins[3] = d((64,), F32, ptr=4 * MB)  # labels must be int32
     assert call(lib, XENT_HEAD, ins, outs, kid=kid) == INV
+
+
+def _view_params(ir, names, elem_offset):
+    """Re-declare parameters `names` of a built IR as views of one flat fp32
+    buffer, the first one at `elem_offset` elements (the rest follow it)."""
+    import dataclasses
+
+    total = elem_offset + sum(int(np.prod(ir.by_name(n).shape)) for n in names)
+    flat = ir.new_value(name="flat.extra", shape=(total,), dtype="torch.float32", device="cpu")
+    off = elem_offset
+    for n in names:
+        v = ir.by_name(n)
+        ir.values[v.id] = dataclasses.replace(v, view_of=(flat.id, off))
+        off += int(np.prod(v.shape))
+
+
+def _relower(ir):
+    from aicf_hip.lower import compile_lowered
+
+    return compile_lowered(ir, fuse_small=True)
+
+
+def test_small_step_keeps_unaligned_views_off_the_vector_kernels():
+    """adamw_multi and xent_head move 16-byte vectors: a head weight that is
+    a view at an offset of one float keeps adamw_step (which has an unaligned
+    path) and the unfused head; at a 16-byte offset the fusions apply."""
+    from aicf_hip import mlp
+
+    ir, low, _ = mlp.build_mlp_xent(fuse_small=True)
+    _view_params(ir, ["2.W"], 4)  # 16 bytes: still aligned
+    ops = [it["op"] for it in _relower(ir)]
+    assert "xent_head" in ops and ops.count("adamw_multi") == 1 and "adamw_step" not in ops
+    ir, low, _ = mlp.build_mlp_xent(fuse_small=True)
+    _view_params(ir, ["2.W"], 1)
+    ops = [it["op"] for it in _relower(ir)]
+    assert "xent_head" not in ops and "softmax_xent" in ops
+    name = {v.id: v.name for v in ir.values.values()}
+    low = _relower(ir)
+    multi = [it for it in low if it["op"] == "adamw_multi"]
+    fused_params = {name[v] for it in multi for v in it["inputs"][0::4][:-1]}
+    assert "2.W" not in fused_params
+    assert any(it["op"] == "adamw_step" and name[it["inputs"][0]] == "2.W" for it in low)
+
+
+def _save_graph(extra_reader_before=False, dst_name="relu0_saved"):
+    """relu(x) -> h; copy_saved(h) -> s; relu_bwd(d, s) -> dx as a lowered list."""
+    from aicf_hip.ir import IRGraph
+
+    ir = IRGraph(name="saves")
+    nv = lambda n: ir.new_value(name=n, shape=(4, 8), dtype="torch.float32", device="cpu").id  # noqa: E731
+    x, h, s, d_, dx, y = nv("a_in"), nv("h"), nv(dst_name), nv("d_h"), nv("d_a"), nv("y")
+    low = [{"op": "relu", "inputs": [x], "outputs": [h], "attrs": {}}]
+    if extra_reader_before:
+        low.append({"op": "relu", "inputs": [s], "outputs": [y], "attrs": {}})
+    low += [{"op": "copy_saved", "inputs": [h], "outputs": [s], "attrs": {}},
+            {"op": "relu_bwd", "inputs": [d_, s], "outputs": [dx], "attrs": {}}]
+    return ir, low, s, h
+
+
+def test_drop_dead_saves_keeps_copies_something_else_reads():
+    from aicf_hip.lower import drop_dead_saves
+
+    ir, low, s, h = _save_graph()
+    out = drop_dead_saves(ir, low)
+    assert [it["op"] for it in out] == ["relu", "relu_bwd"] and out[1]["inputs"] == [low[2]["inputs"][0], h]
+    # an op before the copy reads the previous step's save: the copy stays
+    ir, low, s, h = _save_graph(extra_reader_before=True)
+    assert [it["op"] for it in drop_dead_saves(ir, low)] == ["relu", "relu", "copy_saved", "relu_bwd"]
+    # the caller reads the save after the step
+    ir, low, s, h = _save_graph()
+    assert "copy_saved" in [it["op"] for it in drop_dead_saves(ir, low, keep=[s])]
+    # a save bound by the caller (an input or parameter name) is not the copy's to drop
+    for nm in ("x", "0.W"):
+        ir, low, s, h = _save_graph(dst_name=nm)
+        assert "copy_saved" in [it["op"] for it in drop_dead_saves(ir, low)], nm
+
+
+def test_xent_head_refuses_partially_overlapping_outputs(lib):
+    kid = "xent_head_f32_v0"
+    B, K, C = 64, 256, 10
+    ins = [d((B, K), ptr=MB), d((C, K), ptr=2 * MB), d((C,), ptr=3 * MB), d((B,), I32, ptr=4 * MB),
+           d((B, K), ptr=5 * MB)]
+
+    def outs():
+        return [d((B, C), ptr=6 * MB), d((B, C), ptr=7 * MB), d((B,), I32, ptr=8 * MB), d((B,), ptr=9 * MB),
+                d((B, K), ptr=10 * MB), d((B, K), ptr=11 * MB)]
+
+    o = outs()
+    o[5] = d((B, K), ptr=5 * MB + 1024)  # dX over the second row onwards of S
+    assert call(lib, XENT_HEAD, ins, o, kid=kid) == INV
+    o = outs()
+    o[1] = d((B, C), ptr=6 * MB + 16)  # dlogits overlapping logits
+    assert call(lib, XENT_HEAD, ins, o, kid=kid) == INV
+    o = outs()
+    o[3] = d((B,), ptr=MB + 4096)  # row loss inside H
+    assert call(lib, XENT_HEAD, ins, o, kid=kid) == INV

@@ -200,3 +200,59 @@ def test_dgelu_partials_epilogue_refusals(lib):
                 GEPI, pay, kid) == INV
     A2, Z2, C2 = d((500, 256), BF16, MB), d((500, 512), BF16, 3 * MB), d((500, 512), BF16, 4 * MB)
     assert call(lib, GEMM_EPILOGUE, [A2, B, Z2], [C2, d((1, 512), F32, 5 * MB)], GEPI, pay, kid) == INV
+
+
+def test_tail_sizes_the_loss_partials_for_wide_rows():
+    """mse_colsum writes ceil(N / 512) x P loss partials (bf16, 64 lanes of 8
+    columns per workgroup); where the loss op's own buffer is smaller (here
+    1024 elements against 32 x 64 = 2048 for N = 16384, P = 64) the tail
+    gets a buffer of its own instead of an op that fails at launch."""
+    from aicf_hip import mlp
+
+    ir, low, _ = mlp.build_mlp_mse(128, 16384, 1, fuse_optimizer=True, fuse_colsum=True, fuse_tail=True,
+                                   device="cpu")
+    assert ir.by_name("mse.partials").shape == (1024,)
+    mc = next(it for it in low if it["op"] == "mse_colsum")
+    ws = ir.values[mc["outputs"][2]]
+    assert ws.name != "mse.partials" and ws.shape == (2048,) and "float32" in ws.dtype
+    # at the benchmark shape the loss op's buffer is large enough and is reused
+    ir, low, _ = _tail(B=512, D=512)
+    mc = next(it for it in low if it["op"] == "mse_colsum")
+    assert ir.values[mc["outputs"][2]].name == "mse.partials"
+
+
+def test_lowering_constants_match_the_kernels():
+    """The lowering's copies of kernel limits are the kernels' own values."""
+    import re
+    from pathlib import Path
+
+    from aicf_hip import lower
+
+    csrc = Path(__file__).resolve().parents[1] / "ai-compiler-framework_amd" / "csrc"
+    elt = (csrc / "kernels" / "eltwise.hip").read_text()
+    hdr = (csrc / "common" / "smallstep.hpp").read_text()
+    assert int(re.search(r"kMseColsumVecBf16\s*=\s*(\d+)", elt).group(1)) == lower.MSE_COLSUM_VEC_BF16
+    assert int(re.search(r"kSmallGemmMaxTiles64\s*=\s*(\d+)", hdr).group(1)) == lower.SMALL_GEMM_MAX_TILES64
+
+
+def test_mse_colsum_refuses_overlapping_outputs(lib):
+    """Written buffers that overlap an input or each other are refused, also
+    when only part of the byte ranges meet."""
+    kid = "mse_colsum_v0"
+    pay = struct.pack("<fi", 0.0, 1)
+    # gradient over the second half of the prediction
+    ins, outs = _mse_args()
+    outs[0] = d((256, 512), BF16, ins[0].data + 256 * 512)
+    assert call(lib, MSE_COLSUM, ins, outs, MSCS, pay, kid) == INV
+    # loss scalar inside the target
+    ins, outs = _mse_args()
+    outs[1] = d((), F32, ins[1].data + 64)
+    assert call(lib, MSE_COLSUM, ins, outs, MSCS, pay, kid) == INV
+    # column partials overlapping the loss partials
+    ins, outs = _mse_args()
+    outs[3] = d((4, 512), F32, outs[2].data + 4000 * 4)
+    assert call(lib, MSE_COLSUM, ins, outs, MSCS, pay, kid) == INV
+    # loss partials over the step counter
+    ins, outs = _mse_args()
+    outs[2] = d((4096,), F32, ins[2].data - 8)
+    assert call(lib, MSE_COLSUM, ins, outs, MSCS, pay, kid) == INV
