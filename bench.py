@@ -48,6 +48,8 @@ def _cs() -> int:
 
 
 WARM_S = 0.05  # seconds of back-to-back work before a timed region
+# The step's clock ramp spans ~50 replays (~150 ms): the headline warms longer.
+STEP_WARM_S = 0.25
 
 
 def _warm(launch, warm_s: float) -> None:
@@ -405,24 +407,36 @@ def bench_adam(C, n=1 << 28, steps=10):
 
 
 # ------------------------------------------------------------------ MLP
-def bench_mlp(B, D, L, steps, warmup, dead_dx=True, fuse_optimizer=False, fuse_colsum=False, fuse_tail=False):
-    import torch
-
+def _make_step(B, D, L, own_graph=False, **plan_kw):
+    """The bf16 MLP step built, initialised (seed 0) and captured."""
     from aicf_hip import mlp
 
-    ir, lowered, plan = mlp.build_mlp_mse(B, D, L, dead_dx=dead_dx, fuse_optimizer=fuse_optimizer,
-                                          fuse_colsum=fuse_colsum, fuse_tail=fuse_tail)
-    ex = mlp.make_executor(ir, lowered, plan)
+    ir, lowered, plan = mlp.build_mlp_mse(B, D, L, **plan_kw)
+    ex = mlp.make_executor(ir, lowered, plan, own_graph=own_graph)
     inputs, params = mlp.init_mlp_mse(B, D, L)
     ex.build_env(inputs=inputs, params=params, reuse_static=False)
     mlp.refresh_shadow(ex)
     ex.capture(inputs=inputs, params=params, reuse_static=True)
+    return ex, lowered
+
+
+def bench_mlp(B, D, L, steps, warmup, warm_s=STEP_WARM_S, **plan_kw):
+    """`warmup` untimed replays, then at least warm_s seconds of back-to-back
+    replays (the clock's loaded steady state, as every component gets), then
+    exactly `steps` replays timed with HIP events on the replay stream,
+    synchronised on both sides."""
+    import torch
+
+    ex, lowered = _make_step(B, D, L, **plan_kw)
     gs = torch.cuda.current_stream()  # graph_launch replays on the caller's stream
     losses = []
     for _ in range(warmup):
         ex.replay(1)
     torch.cuda.synchronize()
     losses.append(float(ex.value("loss").item()))
+    tw = time.perf_counter()
+    _warm(lambda: ex.replay(1), warm_s)
+    warm_ms = (time.perf_counter() - tw) * 1e3
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -437,7 +451,49 @@ def bench_mlp(B, D, L, steps, warmup, dead_dx=True, fuse_optimizer=False, fuse_c
     ngemm = sum(1 for it in lowered if it["op"] in ("gemm", "gemm_epilogue", "gemm_adamw"))
     ex.reset_graph()
     return {"ms": ms, "wall_ms": wall * 1e3 / steps, "steps_per_s": 1e3 / ms, "losses": losses,
-            "finite": finite, "ops": len(lowered), "gemms": ngemm}
+            "finite": finite, "ops": len(lowered), "gemms": ngemm, "warm_ms": warm_ms}
+
+
+# The step in the headline's plan and the plans it is compared with.
+STEP_VARIANTS = {
+    "headline": dict(fuse_optimizer=True, fuse_colsum=True, fuse_tail=True),
+    "without_tail_fusion": dict(fuse_optimizer=True, fuse_colsum=True),
+    "without_dead_input_dx": dict(dead_dx=False, fuse_optimizer=True, fuse_colsum=True, fuse_tail=True),
+    "reference_op_split": dict(),
+}
+
+
+def bench_mlp_alternated(B, D, L, rounds=10, chunk=10, warm_s=STEP_WARM_S):
+    """Every step variant captured on a graph handle of its own, warmed
+    together, then timed in `rounds` rounds of `chunk` replays each,
+    variants alternated (order reversed every other round), so that clock
+    and box state are shared and the plans compare like for like."""
+    import torch
+
+    exs = {k: _make_step(B, D, L, own_graph=True, **kw) for k, kw in STEP_VARIANTS.items()}
+    for ex, _ in exs.values():
+        ex.replay(3)
+    torch.cuda.synchronize()
+    _warm(lambda: [ex.replay(1) for ex, _ in exs.values()], warm_s)
+    s = torch.cuda.current_stream()
+    tot = {k: 0.0 for k in exs}
+    names = list(exs)
+    for r in range(rounds):
+        for k in (names if r % 2 == 0 else names[::-1]):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            exs[k][0].replay(chunk)
+            e1.record(s)
+            torch.cuda.synchronize()
+            tot[k] += e0.elapsed_time(e1)
+    out = {}
+    for k, (ex, lowered) in exs.items():
+        ms = tot[k] / (rounds * chunk)
+        out[k] = {"ms": ms, "steps_per_s": 1e3 / ms, "ops": len(lowered),
+                  "gemms": sum(1 for it in lowered if it["op"] in ("gemm", "gemm_epilogue", "gemm_adamw")),
+                  "loss_after": float(ex.value("loss").item())}
+        ex.close()
+    return out
 
 
 STEP_GEMM_OPS = ("gemm", "gemm_epilogue", "gemm_adamw")
@@ -1431,7 +1487,7 @@ def main():
         vendor_compare(C, args.vendor_set)
         return
 
-    res = bench_mlp(B, D, L, args.steps, args.warmup, fuse_optimizer=True, fuse_colsum=True, fuse_tail=True)
+    res = bench_mlp(B, D, L, args.steps, args.warmup, **STEP_VARIANTS["headline"])
     log(f"[bench] mlp {res}")
 
     # dominant kernel: gemm_nt_kernel, the step's 12 GEMM launches (~88% of
@@ -1525,26 +1581,27 @@ def main():
                 "frac": round(tm["tflops"] / PEAK_BF16_TFLOPS, 4), "ms": round(tm["ms"], 4),
                 "note": "torch.matmul (hipBLASLt) in the same process, reference line only"}
             log(f"[bench] torch.matmul {M_}x{N_}x{K_} {tm}")
-        uf = bench_mlp(B, D, L, args.steps, args.warmup, fuse_optimizer=False, fuse_colsum=False)
-        comps["mlp_step_reference_op_split"] = {
-            "value": round(uf["steps_per_s"], 3), "unit": "steps/s", "ms": round(uf["ms"], 4),
-            "note": "same step with the reference's op split: dW GEMMs write the fp32 gradient, one "
-                    "streaming AdamW over all parameters, bias gradients by separate column sums"}
-        log(f"[bench] mlp reference op split {uf}")
-        nd = bench_mlp(B, D, L, args.steps, args.warmup, dead_dx=False, fuse_optimizer=True, fuse_colsum=True,
-                       fuse_tail=True)
-        comps["mlp_step_without_dead_input_dx"] = {
-            "value": round(nd["steps_per_s"], 3), "unit": "steps/s", "ms": round(nd["ms"], 4),
-            "gemms_per_step": nd["gemms"],
-            "note": "same step with the first layer's input gradient (never consumed) removed; "
-                    "the headline keeps it, as the reference's lowering emits it"}
-        log(f"[bench] mlp without dead dX {nd}")
-        nt = bench_mlp(B, D, L, args.steps, args.warmup, fuse_optimizer=True, fuse_colsum=True, fuse_tail=False)
-        comps["mlp_step_without_tail_fusion"] = {
-            "value": round(nt["steps_per_s"], 3), "unit": "steps/s", "ms": round(nt["ms"], 4), "ops": nt["ops"],
-            "note": "the headline plan with the loss and bias tail unfused (mse_loss, reduce_sum, step_inc, "
-                    "column-sum finishes and the bias AdamW as separate launches); same parameters bit for bit"}
-        log(f"[bench] mlp without tail fusion {nt}")
+        alt = bench_mlp_alternated(B, D, L)
+        notes = {
+            "reference_op_split": "same step with the reference's op split: dW GEMMs write the fp32 gradient, one "
+                                  "streaming AdamW over all parameters, bias gradients by separate column sums",
+            "without_dead_input_dx": "same step with the first layer's input gradient (never consumed) removed; "
+                                     "the headline keeps it, as the reference's lowering emits it",
+            "without_tail_fusion": "the headline plan with the loss and bias tail unfused (mse_loss, reduce_sum, "
+                                   "step_inc, column-sum finishes and the bias AdamW as separate launches); same "
+                                   "parameters bit for bit",
+        }
+        for k, note in notes.items():
+            comps[f"mlp_step_{k}"] = {
+                "value": round(alt[k]["steps_per_s"], 3), "unit": "steps/s", "ms": round(alt[k]["ms"], 4),
+                "ops": alt[k]["ops"], "gemms_per_step": alt[k]["gemms"],
+                "headline_plan_in_the_same_loop_ms": round(alt["headline"]["ms"], 4), "note": note}
+        comps["mlp_step_variants_alternated"] = {
+            "value": round(alt["headline"]["steps_per_s"], 3), "unit": "steps/s",
+            "ms": {k: round(v["ms"], 4) for k, v in alt.items()},
+            "note": "the headline plan and each variant on graph handles of their own, warmed together, then "
+                    "10 rounds of 10 replays each with the variants alternated (order reversed every other round)"}
+        log(f"[bench] mlp variants alternated {alt}")
         c1 = bench_c1()
         c1["reference_lowering"] = bench_c1(fuse_small=False)
         comps["c1_mlp_fp32_64x784x256x10_step"] = c1
@@ -1597,6 +1654,7 @@ def main():
         "cpu_baseline": cpu,
         "components": comps,
         "loss_first_last": res["losses"],
+        "warm_ms": round(res["warm_ms"], 1),
     }
     print(json.dumps(out), flush=True)
 
