@@ -573,8 +573,10 @@ __global__ __launch_bounds__(LPR >= 256 ? LPR : 256) void row_reg_kernel(RowArgs
     }
     if (l == 0) {
       a.argmax[row] = st.i;
-      // loss_i = log(sum exp(z - m)) + m - z[label]
-      a.row_loss[row] = valid ? (logf(st.s) + st.m - st.sx) : __builtin_nanf("");
+      // loss_i = (m - z[label]) + log(sum exp(z - m)): m - z[label] is exact
+      // for close values and >= 0, so nothing cancels after the rounding of
+      // log (added first, a row of -1e4 lost ~1e-3 of log(C))
+      a.row_loss[row] = valid ? ((st.m - st.sx) + logf(st.s)) : __builtin_nanf("");
     }
   }
 }
@@ -644,7 +646,7 @@ __global__ __launch_bounds__(256) void row_loop_kernel(RowArgs a) {
       yr[c] = (__expf(xr[c] - mx) * inv - (c == lab ? 1.0f : 0.0f)) * a.inv_batch;
     if (t == 0) {
       a.argmax[row] = bi;
-      a.row_loss[row] = valid ? (logf(se) + mx - xr[lab]) : __builtin_nanf("");
+      a.row_loss[row] = valid ? ((mx - xr[lab]) + logf(se)) : __builtin_nanf("");
     }
   }
 }

@@ -279,7 +279,7 @@ __global__ __launch_bounds__(64) void xent_head_kernel(XentHeadArgs a) {
   if (lane == 0) {
     a.argmax[row] = am;
     const bool valid = lab >= 0 && lab < a.C;
-    a.row_loss[row] = valid ? (logf(S) + M - zl) : __builtin_nanf("");
+    a.row_loss[row] = valid ? ((M - zl) + logf(S)) : __builtin_nanf("");  // as softmax_xent
   }
 
   // dH = dlogits . W and the ReLU backward against the saved output

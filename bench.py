@@ -568,6 +568,29 @@ def bench_copy_ceiling(C, elems=1 << 29, iters=10, warmup=2):
     return {"gbs": 4.0 * elems / (ms * 1e-3) / 1e9, "ms": ms}
 
 
+def bench_copy_sized(C, read_bytes, iters=20, warmup=3):
+    """The copy kernel (copy_bf16_v0) moving `read_bytes` in and out, timed
+    like the row kernels: a captured graph of back-to-back launches over
+    rotated buffer sets whose working set exceeds the 256 MB MALL.  At sizes
+    where a launch's fixed cost (dispatch, first-load latency, drain) is a
+    large part of its time, this is the practical ceiling of a kernel that
+    reads and writes that many bytes."""
+    import torch
+
+    elems = read_bytes // 2
+    sets = _rotating_sets(lambda: (torch.ones(elems, device="cuda", dtype=torch.bfloat16),
+                                   torch.empty(elems, device="cuda", dtype=torch.bfloat16)), 2 * read_bytes)
+    k = [0]
+
+    def fn():
+        x, y = sets[k[0] % len(sets)]
+        k[0] += 1
+        C.launch_by_id("copy_bf16_v0", C.OpKind.Copy, [x], [y], 0, b"", _cs())
+
+    ms = time_launches(fn, iters, warmup, graph=True)
+    return {"ms": ms, "gbs": 2.0 * read_bytes / (ms * 1e-3) / 1e9}
+
+
 def bench_mfma_ceiling(form=16, waves_per_simd=4, iters=20000, launches=8, warm=4):
     """Sustained rate of the register-only MFMA loop (aicf_diag_mfma_loop_form
     on random operands, no memory traffic): form 16 is v_mfma_f32_16x16x32_bf16,
@@ -1146,7 +1169,12 @@ def pmc_report(fetch_csv, write_csv, mfma_csv=None, trace_csv=None):
 # algorithmic bytes per dispatch).  Shapes follow the benchmark configs.
 SR, SC = 16384, 32768
 STREAMING = [
+    ("row softmax (+max, +sum) 16384x128 f32", "row_reg_kernel<16, 2, 0>", 8 * SR * 128 + 8 * SR),
     ("row softmax (+max, +sum) 16384x1024 f32", "row_reg_kernel<128, 2, 0>", 8 * SR * 1024 + 8 * SR),
+    ("row sum 16384x128 f32", "row_reg_kernel<16, 2, 1>", 4 * SR * 128 + 4 * SR),
+    ("row max 16384x128 f32", "row_reg_kernel<16, 2, 2>", 4 * SR * 128 + 4 * SR),
+    ("row sum 16384x1024 f32", "row_reg_kernel<128, 2, 1>", 4 * SR * 1024 + 4 * SR),
+    ("row max 16384x1024 f32", "row_reg_kernel<128, 2, 2>", 4 * SR * 1024 + 4 * SR),
     ("row softmax (+max, +sum) 16384x8192 f32", "row_reg_kernel<128, 16, 0>", 8 * SR * 8192 + 8 * SR),
     ("row softmax (+max, +sum) 16384x32768 f32", "row_reg_kernel<512, 16, 0>", 8 * SR * SC + 8 * SR),
     ("row sum 16384x32768 f32", "row_reg_kernel<512, 16, 1>", 4 * SR * SC + 4 * SR),
@@ -1167,12 +1195,16 @@ def streaming_only(C):
 
     g = torch.Generator(device="cuda")
     g.manual_seed(8)
-    for cols in (1024, 8192):
+    for cols in (128, 1024, 8192):
         xs = torch.randn((SR, cols), device="cuda", generator=g) * 2.0
         ys = torch.empty_like(xs)
         mxs, sms = torch.empty(SR, device="cuda"), torch.empty(SR, device="cuda")
         for _ in range(3):
             C.op_call(int(C.OpKind.RowSoftmax), [xs], [ys, mxs, sms], 0, b"", 0)
+        if cols <= 1024:
+            for op in (0, 1):
+                for _ in range(3):
+                    C.op_call(int(C.OpKind.RowReduce), [xs], [mxs], RRED, struct.pack("<i", op), 0)
         del xs, ys
     x = torch.randn((SR, SC), device="cuda", generator=g) * 2.0
     y = torch.empty_like(x)
@@ -1216,7 +1248,7 @@ def streaming_only(C):
     for _ in range(3):
         C.launch_by_id("copy_bf16_v0", C.OpKind.Copy, [xc], [yc], 0, b"")
     torch.cuda.synchronize()
-    log("[bench] streaming-only: 10 kernels x 3 dispatches, 3 calibration copies")
+    log(f"[bench] streaming-only: {len(STREAMING)} kernels x 3 dispatches, 3 calibration copies")
 
 
 def pmc_streaming_report(fetch_csv, write_csv):
@@ -1532,12 +1564,15 @@ def main():
         log(f"[bench] gemm 8192^3 {gg}")
         for cols in (128, 1024, 8192, 32768):
             sm = bench_softmax(C, 16384, cols)
+            cs_ = bench_copy_sized(C, 16384 * cols * 4)
             comps[f"softmax_16384x{cols}"] = {"value": round(sm["gbs"], 1), "unit": "GB/s",
                                               "frac": round(sm["gbs"] / PEAK_HBM_GBS, 4),
                                               "ms": round(sm["ms"], 5),
-                                              "buffer_sets": sm["buffer_sets"]}
-            log(f"[bench] softmax {cols} {sm}")
-        for cols in (1024, 8192, 32768):
+                                              "buffer_sets": sm["buffer_sets"],
+                                              "copy_same_bytes_gbs": round(cs_["gbs"], 1),
+                                              "frac_of_copy_same_bytes": round(sm["gbs"] / cs_["gbs"], 4)}
+            log(f"[bench] softmax {cols} {sm} copy of the same bytes {cs_}")
+        for cols in (128, 1024, 8192, 32768):
             for name, op in (("rowmax", 1), ("rowsum", 0)):
                 rr = bench_rowreduce(C, 16384, cols, op)
                 comps[f"{name}_16384x{cols}"] = {"value": round(rr["gbs"], 1), "unit": "GB/s",

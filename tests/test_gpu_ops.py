@@ -389,6 +389,30 @@ def test_softmax_xent(C, B, Ccls):
     assert orc.rel_err(h(rl), rrl) < 1e-5
 
 
+@pytest.mark.parametrize("Ccls", [128, 1024, 1000])  # register-resident rows, and the looping kernel
+def test_softmax_xent_row_loss_of_extreme_rows(C, Ccls):
+    """Rows of equal values far from zero (+-1e4) have row loss log(C) for any
+    label, and rows offset by 1e4 have the loss of the unshifted row: each
+    row's loss against the fp64 oracle row by row (not normwise), so a
+    cancellation after rounding log(S) shows up."""
+    B = 8
+    r = rng(Ccls + 7)
+    z = r.standard_normal((B, Ccls)).astype(np.float32)
+    z[0], z[1] = -1e4, 1e4
+    z[2:5] += np.float32(1e4)
+    z[5:] -= np.float32(1e4)
+    lab = r.integers(0, Ccls, B).astype(np.int32)
+    loss = torch.empty((), device="cuda")
+    dz = torch.empty((B, Ccls), device="cuda")
+    am = torch.empty(B, dtype=torch.int32, device="cuda")
+    rl = torch.empty(B, device="cuda")
+    C.op_call(int(C.OpKind.SoftmaxXent), [g(z), g(lab)], [loss, dz, am, rl], 0, b"", 0)
+    _, _, _, rrl = orc.softmax_xent_f64(z, lab)
+    got = h(rl).astype(np.float64)
+    assert np.abs(got[:2] - np.log(Ccls)).max() <= 2e-6 * np.log(Ccls)
+    assert (np.abs(got - rrl) / np.abs(rrl)).max() < 1e-5
+
+
 # ============================================================== GEMM
 def _gemm_ref(A, B, ta, tb):
     return orc.gemm_f64(A, B, ta, tb)
