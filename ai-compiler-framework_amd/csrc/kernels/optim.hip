@@ -114,17 +114,11 @@ __global__ __launch_bounds__(256) void adamw_vec4_kernel(
   // n % 4 remaining elements one by one (the same expression), so one launch
   // covers any length
   const int64_t n4 = n / 4;
-  // the bias corrections (two fp64 pow) are computed by one wave per block
-  __shared__ float sh[2];
-  if (threadIdx.x < 64) {
-    const AdamWScalars t = adamw_scalars(stepp, a);
-    if (threadIdx.x == 0) {
-      sh[0] = t.step;
-      sh[1] = t.ibc2;
-    }
-  }
-  __syncthreads();
-  const AdamWScalars s{sh[0], sh[1]};
+  // The element loads go out first: they do not depend on the step counter,
+  // whose read and the bias corrections (two fp64 pow, one wave per block)
+  // then overlap them (2^28 parameters: 6.17 -> 6.27 TB/s against the
+  // counter read before the loads; the same bits; a per-wave computation
+  // without the barrier, and two vectors per thread, measured slower).
   const int64_t base = (int64_t)blockIdx.x * (256 * UNROLL) + threadIdx.x;
   f32x4 p[UNROLL], g[UNROLL], m[UNROLL], v[UNROLL];
 #pragma unroll
@@ -137,6 +131,16 @@ __global__ __launch_bounds__(256) void adamw_vec4_kernel(
       v[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(V) + i);
     }
   }
+  __shared__ float sh[2];
+  if (threadIdx.x < 64) {
+    const AdamWScalars t = adamw_scalars(stepp, a);
+    if (threadIdx.x == 0) {
+      sh[0] = t.step;
+      sh[1] = t.ibc2;
+    }
+  }
+  __syncthreads();
+  const AdamWScalars s{sh[0], sh[1]};
 #pragma unroll
   for (int u = 0; u < UNROLL; ++u) {
     const int64_t i = base + (int64_t)u * 256;
