@@ -23,8 +23,7 @@ struct AdamWScalars {
   float step, ibc2;
 };
 
-__device__ __forceinline__ AdamWScalars adamw_scalars(const int32_t* stepp, const AdamWArgs& a) {
-  int t = stepp[0];
+__device__ __forceinline__ AdamWScalars adamw_scalars_at(int t, const AdamWArgs& a) {
   if (t < 1) t = 1;
   const float bc1 = (float)(1.0 - pow((double)a.beta1, (double)t));
   const float bc2 = (float)(1.0 - pow((double)a.beta2, (double)t));
@@ -32,6 +31,10 @@ __device__ __forceinline__ AdamWScalars adamw_scalars(const int32_t* stepp, cons
   s.step = a.lr / bc1;
   s.ibc2 = 1.0f / bc2;
   return s;
+}
+
+__device__ __forceinline__ AdamWScalars adamw_scalars(const int32_t* stepp, const AdamWArgs& a) {
+  return adamw_scalars_at(stepp[0], a);
 }
 
 __device__ __forceinline__ void adamw_elem(float& p, float g, float& m, float& v,

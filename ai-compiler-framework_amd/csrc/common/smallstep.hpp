@@ -22,6 +22,11 @@ struct SmallGemm {
   int64_t a_m, a_k, b_k, b_n, c_m, bias_s;
   int64_t M, N, K;
   int relu;           // relu(acc + bias)
+  // nullptr, or a copy of B written at B's element offsets (B[k * b_k +
+  // n * b_n] -> bcopy[k * b_k + n * b_n]) by the tiles of the first row of
+  // tiles, which read all of B; needs K-contiguous B (b_k == 1, 16-byte
+  // aligned rows)
+  float* bcopy;
 };
 
 // The GEMM dispatcher sends an fp32 problem with fewer than this many

@@ -84,6 +84,9 @@ __device__ __forceinline__ f32x4 sg_tile(const SgJob& j, int64_t m0, int64_t n0,
   const bool mok = m < j.g.M, nok = n < j.g.N;
   const float* ar = j.g.A + (mok ? m : 0) * j.g.a_m;
   const float* br = j.g.B + (nok ? n : 0) * j.g.b_n;
+  // the first row of tiles reads all of B: it also writes B's copy
+  const bool snap = j.g.bcopy != nullptr && m0 == 0 && nok;
+  float* bc = snap ? j.g.bcopy + n * j.g.b_n : nullptr;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   for (int kb0 = split; kb0 < j.kb; kb0 += j.splits * kNB) {
     f32x4 a[kNB], b[kNB];
@@ -99,12 +102,65 @@ __device__ __forceinline__ f32x4 sg_tile(const SgJob& j, int64_t m0, int64_t n0,
       if (kb0 + u * j.splits >= j.kb) break;  // uniform across the wave
 #pragma unroll
       for (int c = 0; c < 4; ++c) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u][c], b[u][c], acc, 0, 0, 0);
+      if (snap) {  // K % 4 == 0 (16-byte loads of B): the four are in range together
+        const int64_t k = (int64_t)(kb0 + u * j.splits) * 16 + 4 * q;
+        if (k < j.g.K) *reinterpret_cast<f32x4*>(bc + k) = b[u];
+      }
     }
   }
   return acc;
 }
 
-__device__ __forceinline__ void sg_store(const SmallGemm& g, int64_t m0, int64_t n0, int lane, f32x4 acc) {
+// AdamW applied where a gradient is stored: P, M, V laid out like the stored
+// gradient (element index of the output), updated in place with adamw_step's
+// element update (csrc/common/adamw.hpp) and the step's bias corrections
+// {lr / bc1, 1 / bc2} as adamw_step derives them, computed once per step by
+// an earlier launch (the head that advances the step counter), so the bits
+// are adamw_step's.  A lane loads its P, M, V elements before its tile's K
+// loop.  The routines take the update by value under a compile-time flag: a
+// pointer that may be null would keep the struct in scratch memory.
+struct StoreAdamW {
+  float* P;
+  float* M;
+  float* V;
+  const float* scal;  // {lr / bc1, 1 / bc2} of this step
+  AdamWArgs a;
+};
+struct AdamWLane {
+  float p[4], m[4], v[4];
+  AdamWScalars s;
+};
+__device__ __forceinline__ void adamw_load(const StoreAdamW& ad, int64_t i, int x, AdamWLane& r) {
+  r.p[x] = ad.P[i];
+  r.m[x] = ad.M[i];
+  r.v[x] = ad.V[i];
+}
+__device__ __forceinline__ void adamw_store(const StoreAdamW& ad, int64_t i, int x, float g, AdamWLane& r) {
+  adamw_elem(r.p[x], g, r.m[x], r.v[x], r.s, ad.a);
+  ad.P[i] = r.p[x];
+  ad.M[i] = r.m[x];
+  ad.V[i] = r.v[x];
+}
+
+// The elements sg_store writes for this lane: C[m0 + 4 q + i][n0 + r].
+__device__ __forceinline__ void sg_adamw_prefetch(const SmallGemm& g, int64_t m0, int64_t n0, int lane,
+                                                  const StoreAdamW& ad, AdamWLane& r) {
+  const int rr = lane & 15, q = lane >> 4;
+  const int64_t n = n0 + rr;
+  r.s = AdamWScalars{ad.scal[0], ad.scal[1]};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t m = m0 + 4 * q + i;
+    if (n < g.N && m < g.M)
+      adamw_load(ad, m * g.c_m + n, i, r);
+    else
+      r.p[i] = r.m[i] = r.v[i] = 0.0f;
+  }
+}
+
+template <bool ADAM>
+__device__ __forceinline__ void sg_store(const SmallGemm& g, int64_t m0, int64_t n0, int lane, f32x4 acc,
+                                         const StoreAdamW& ad, AdamWLane& ar) {
   const int r = lane & 15, q = lane >> 4;
   const int64_t n = n0 + r;
   if (n >= g.N) return;
@@ -116,19 +172,26 @@ __device__ __forceinline__ void sg_store(const SmallGemm& g, int64_t m0, int64_t
     float v = g.bias ? acc[i] + bv : acc[i];
     if (g.relu) v = v > 0.0f ? v : 0.0f;
     g.C[m * g.c_m + n] = v;
+    if constexpr (ADAM) adamw_store(ad, m * g.c_m + n, i, v, ar);
   }
 }
 
 // Workgroup `blk` of a small GEMM: its waves = tpb tiles x splits K parts.
 // The parts of a tile are summed in split order (part 0 + 1 + 2 + ...).
 // `red` is 64 f32x4 of LDS per wave.  Every thread reaches the barrier.
-__device__ __forceinline__ void sg_block(const SgJob& j, int blk, f32x4* red) {
+// ADAM: apply AdamW to the parameter whose gradient the output is (the
+// output is row-major contiguous, so its element index is the parameter's).
+template <bool ADAM>
+__device__ __forceinline__ void sg_block(const SgJob& j, int blk, f32x4* red, const StoreAdamW& ad) {
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int tile = blk * j.tpb + w / j.splits;
   const int split = w % j.splits;
   const bool live = tile < j.tiles;
   const int64_t m0 = live ? (int64_t)(tile / j.tn) * 16 : 0;
   const int64_t n0 = live ? (int64_t)(tile % j.tn) * 16 : 0;
+  AdamWLane ar;
+  const bool upd = ADAM && live && split == 0;
+  if (upd) sg_adamw_prefetch(j.g, m0, n0, lane, ad, ar);
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   if (live) acc = sg_tile(j, m0, n0, split, lane);
   if (j.splits > 1) {
@@ -139,13 +202,13 @@ __device__ __forceinline__ void sg_block(const SgJob& j, int blk, f32x4* red) {
   } else if (!live) {
     return;
   }
-  sg_store(j.g, m0, n0, lane, acc);
+  sg_store<ADAM>(j.g, m0, n0, lane, acc, ad, ar);
 }
 
 template <int NWAVE>
 __global__ __launch_bounds__(64 * NWAVE) void gemm_small_kernel(SgJob j) {
   __shared__ f32x4 red[64 * NWAVE];
-  sg_block(j, blockIdx.x, red);
+  sg_block<false>(j, blockIdx.x, red, StoreAdamW{});
 }
 
 // nwave 4, or 8 for the standalone kernel when K is long enough for 8 splits
@@ -183,18 +246,69 @@ struct XentHeadArgs {
   int64_t B;
   int K, C;
   float inv_batch;
+  // the step counter (nullptr: none), advanced by inc in place by workgroup
+  // B; with scal, that workgroup also writes AdamW's bias corrections of
+  // the advanced step, {lr / bc1, 1 / bc2} (adamw_scalars_at), for a later
+  // launch's updates
+  int32_t* step;
+  int inc;
+  float* scal;
+  AdamWArgs aw;
 };
 
-// Q: 16-byte vectors per lane along K (K <= 256 Q); CM: classes (C <= CM).
-// One wave (one row) per workgroup, so that the rows spread over as many CUs
-// as there are rows.  With Q x CM <= 16 the lane's slice of W is loaded once,
-// together with the row, and serves both the logits and dH.
+// Sums over the wave of x[c] for every class c < CM, in log2(CM) exchange
+// steps that halve the classes a lane carries (it keeps one half and adds
+// its partner's copy of that half), then plain exchanges between the lanes
+// left with the same class.  Lane l returns the sum of class l >> (6 -
+// log2 CM).  Every class is summed in one fixed order.
+template <int CM>
+__device__ __forceinline__ float class_sums(float (&x)[CM], int lane) {
+#pragma unroll
+  for (int n = CM, mask = 32; n > 1; n >>= 1, mask >>= 1) {
+    const bool up = (lane & mask) != 0;
+#pragma unroll
+    for (int i = 0; i < n / 2; ++i) {
+      const float send = up ? x[i] : x[i + n / 2];
+      const float keep = up ? x[i + n / 2] : x[i];
+      x[i] = keep + __shfl_xor(send, mask, 64);
+    }
+  }
+  float v = x[0];
+#pragma unroll
+  for (int mask = 32 / CM; mask > 0; mask >>= 1) v += __shfl_xor(v, mask, 64);
+  return v;
+}
+
+__device__ __forceinline__ float readlane_f(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+// Q: 16-byte vectors per lane along K (K <= 256 Q); CM: classes (C <= CM,
+// 16 or 32).  One wave (one row) per workgroup, so that the rows spread over
+// as many CUs as there are rows.  With Q x CM <= 16 the lane's slice of W is
+// loaded once, together with the row, and serves both the logits and dH.
 template <int Q, int CM>
 __global__ __launch_bounds__(64) void xent_head_kernel(XentHeadArgs a) {
+  static_assert(CM == 16 || CM == 32, "class_sums maps 64 lanes onto 16 or 32 classes");
+  constexpr int SH = CM == 16 ? 2 : 1;  // lane l carries class l >> SH after class_sums
   const int lane = threadIdx.x;
+  if (blockIdx.x == a.B) {  // the step counter's workgroup (launched only with a counter)
+    if (lane == 0) {
+      const int t = a.step[0] + a.inc;
+      a.step[0] = t;
+      if (a.scal) {
+        const AdamWScalars sc = adamw_scalars_at(t, a.aw);
+        a.scal[0] = sc.step;
+        a.scal[1] = sc.ibc2;
+      }
+    }
+    return;
+  }
   const int64_t row = blockIdx.x;
   const int K4 = a.K >> 2;
   constexpr bool PRE = Q * CM <= 16;
+  // every load the row needs is issued here, before the first store (the
+  // outputs alias nothing, but the compiler cannot know that)
   f32x4 wreg[PRE ? Q * CM : 1];
   if constexpr (PRE) {
 #pragma unroll
@@ -213,22 +327,26 @@ __global__ __launch_bounds__(64) void xent_head_kernel(XentHeadArgs a) {
       return reinterpret_cast<const f32x4*>(a.W + (int64_t)c * a.K)[idx];
   };
   const f32x4* hr = reinterpret_cast<const f32x4*>(a.H + row * a.K);
-  f32x4 h[Q];
+  const f32x4* sr = reinterpret_cast<const f32x4*>(a.S + row * a.K);
+  f32x4 h[Q], sv[Q];
 #pragma unroll
   for (int q = 0; q < Q; ++q) {
     const int idx = q * 64 + lane;
     h[q] = idx < K4 ? hr[idx] : f32x4{0.f, 0.f, 0.f, 0.f};
+    sv[q] = idx < K4 ? sr[idx] : f32x4{0.f, 0.f, 0.f, 0.f};
   }
+  const int mycls = lane >> SH;
+  const float mybias = mycls < a.C ? a.bias[mycls] : 0.0f;
   const int lab = a.labels[row];
 
-  // logits: each lane's partial dot products, then a butterfly (every lane
-  // ends with the same bits)
-  float z[CM];
+  // logits: each lane's partial dot products, the class sums, then every
+  // lane reads all logits from the lanes that hold them (the same bits
+  // everywhere)
+  float x[CM];
 #pragma unroll
   for (int c = 0; c < CM; ++c) {
-    z[c] = 0.0f;
+    float p = 0.0f;
     if (c < a.C) {
-      float p = 0.0f;
 #pragma unroll
       for (int q = 0; q < Q; ++q) {
         const int idx = q * 64 + lane;
@@ -240,9 +358,13 @@ __global__ __launch_bounds__(64) void xent_head_kernel(XentHeadArgs a) {
           p = fmaf(h[q][3], w[3], p);
         }
       }
-      z[c] = wave_sum(p) + a.bias[c];
     }
+    x[c] = p;
   }
+  const float zmine = class_sums<CM>(x, lane) + mybias;
+  float z[CM];
+#pragma unroll
+  for (int c = 0; c < CM; ++c) z[c] = readlane_f(zmine, c << SH);
 
   // softmax cross-entropy of the row (first index of the maximum)
   float M = z[0];
@@ -283,7 +405,6 @@ __global__ __launch_bounds__(64) void xent_head_kernel(XentHeadArgs a) {
   }
 
   // dH = dlogits . W and the ReLU backward against the saved output
-  const f32x4* sr = reinterpret_cast<const f32x4*>(a.S + row * a.K);
   f32x4* dhr = reinterpret_cast<f32x4*>(a.dH + row * a.K);
   f32x4* dxr = reinterpret_cast<f32x4*>(a.dX + row * a.K);
 #pragma unroll
@@ -299,7 +420,7 @@ __global__ __launch_bounds__(64) void xent_head_kernel(XentHeadArgs a) {
         for (int i = 0; i < 4; ++i) acc[i] = fmaf(d[c], w[i], acc[i]);
       }
     }
-    const f32x4 s = sr[idx];
+    const f32x4 s = sv[q];
     f32x4 dx;
 #pragma unroll
     for (int i = 0; i < 4; ++i) dx[i] = s[i] > 0.0f ? acc[i] : 0.0f;
@@ -321,8 +442,12 @@ bool i32_vec(const TensorDesc& t, int64_t n) {
 
 // inputs (H [B,K], W [C,K], bias [C], labels [B] i32, S [B,K]);
 // outputs (logits [B,C], dlogits [B,C], argmax [B] i32, row_loss [B], dH [B,K], dX [B,K]).
-bool xent_head_sup(const TensorDesc* in, int ni, const TensorDesc* out, int no, const void*) {
-  if (!in || !out || ni != 5 || no != 6) return false;
+// inputs (H, W, bias, labels, S[, step]); outputs (logits, dlogits, argmax,
+// row loss, dH, dX[, step[, AdamW scalars]]).  step: an int32 counter
+// updated in place; scalars: 2 fp32.  extra: 0, 1 (step) or 2 (step and
+// scalars).
+bool xent_head_check(const TensorDesc* in, int ni, const TensorDesc* out, int no, int extra) {
+  if (!in || !out || ni != (extra ? 6 : 5) || no != 6 + extra) return false;
   if (in[0].rank != 2 || in[1].rank != 2) return false;
   const int64_t B = in[0].shape[0], K = in[0].shape[1], C = in[1].shape[0];
   if (B < 1 || K < 4 || K % 4 || K > 2048 || C < 1 || C > 32) return false;
@@ -335,14 +460,54 @@ bool xent_head_sup(const TensorDesc* in, int ni, const TensorDesc* out, int no, 
       return false;
   if (!i32_vec(out[2], B) || !f32_vec(out[3], B) || !f32_rows(out[4], B, K) || !f32_rows(out[5], B, K))
     return false;
+  if (extra) {  // an int32 scalar (any rank), updated in place
+    const TensorDesc &si = in[5], &so = out[6];
+    if (dt(si) != DType::kI32 || numel_of(si) != 1 || !si.contiguous || so.data != si.data ||
+        dt(so) != DType::kI32 || numel_of(so) != 1)
+      return false;
+  }
+  if (extra == 2 && (dt(out[7]) != DType::kF32 || numel_of(out[7]) != 2 || !out[7].contiguous)) return false;
   // the written tensors touch nothing the kernel reads and not each other
-  for (int o = 0; o < 6; ++o) {
-    for (int i = 0; i < 5; ++i)
-      if (views_overlap(out[o], in[i])) return false;
-    for (int q = o + 1; q < 6; ++q)
+  // (the step counter is read and written by one lane)
+  for (int o = 0; o < no; ++o) {
+    for (int i = 0; i < ni; ++i)
+      if (!(o == 6 && i == 5) && views_overlap(out[o], in[i])) return false;
+    for (int q = o + 1; q < no; ++q)
       if (views_overlap(out[o], out[q])) return false;
   }
-  return B <= INT32_MAX;
+  return B < INT32_MAX;
+}
+
+bool xent_head_sup(const TensorDesc* in, int ni, const TensorDesc* out, int no, const void*) {
+  return xent_head_check(in, ni, out, no, 0);
+}
+
+// Schema XHST <i inc> or <i inc, f lr, f beta1, f beta2>: the step counter
+// advances by inc (1, or 0 for the AICF_WARMUP copy of step_inc); with the
+// hyperparameters the launch also writes AdamW's bias corrections of the
+// advanced step ({lr / bc1, 1 / bc2}, as adamw_step derives them).
+struct XhstAttr {
+  int inc;
+  bool scal;
+  AdamWArgs aw;
+};
+bool read_xhst(const void* attr, XhstAttr* x) {
+  const AttrBlob& b = blob(attr);
+  if (!attr || b.schema_id != AICF_SCHEMA_XHST || !payload_ok(b, 4)) return false;
+  x->inc = field<int32_t>(b, 0);
+  x->scal = payload_ok(b, 16);
+  x->aw = AdamWArgs{};
+  if (x->scal) {
+    const float lr = field<float>(b, 4), b1 = field<float>(b, 8), b2 = field<float>(b, 12);
+    if (lr != lr || b1 != b1 || b2 != b2) return false;
+    x->aw = AdamWArgs{lr, b1, b2, 0.0f, 0.0f, 1.0f - b1, 1.0f - b2, 1.0f};
+  }
+  return x->inc == 0 || x->inc == 1;
+}
+
+bool xent_head_step_sup(const TensorDesc* in, int ni, const TensorDesc* out, int no, const void* attr) {
+  XhstAttr x;
+  return read_xhst(attr, &x) && xent_head_check(in, ni, out, no, x.scal ? 2 : 1);
 }
 
 template <int Q>
@@ -353,10 +518,13 @@ void xent_head_go(const XentHeadArgs& a, unsigned grid, hipStream_t s) {
     xent_head_kernel<Q, 32><<<grid, 64, 0, s>>>(a);
 }
 
-Status xent_head_launch(const TensorDesc* in, int ni, TensorDesc* out, int no, const void* at, void*,
-                        size_t, void* stream) {
-  if (!xent_head_sup(in, ni, out, no, at)) return Status::InvalidArgument;
+Status xent_head_run(const TensorDesc* in, TensorDesc* out, int32_t* step, int inc, float* scal,
+                     const AdamWArgs& aw, void* stream) {
   XentHeadArgs a{};
+  a.step = step;
+  a.inc = inc;
+  a.scal = scal;
+  a.aw = aw;
   a.H = (const float*)in[0].data;
   a.W = (const float*)in[1].data;
   a.bias = (const float*)in[2].data;
@@ -372,7 +540,8 @@ Status xent_head_launch(const TensorDesc* in, int ni, TensorDesc* out, int no, c
   a.K = (int)in[0].shape[1];
   a.C = (int)in[1].shape[0];
   a.inv_batch = 1.0f / (float)a.B;
-  const unsigned grid = (unsigned)a.B;  // one row per workgroup
+  // one row per workgroup, and one more for the step counter
+  const unsigned grid = (unsigned)a.B + (step ? 1u : 0u);
   const int q = (a.K / 4 + 63) / 64;
   hipStream_t s = as_stream(stream);
   if (q <= 1)
@@ -384,6 +553,20 @@ Status xent_head_launch(const TensorDesc* in, int ni, TensorDesc* out, int no, c
   else
     xent_head_go<8>(a, grid, s);
   return launch_status("xent_head");
+}
+
+Status xent_head_launch(const TensorDesc* in, int ni, TensorDesc* out, int no, const void* at, void*,
+                        size_t, void* stream) {
+  if (!xent_head_sup(in, ni, out, no, at)) return Status::InvalidArgument;
+  return xent_head_run(in, out, nullptr, 0, nullptr, AdamWArgs{}, stream);
+}
+
+Status xent_head_step_launch(const TensorDesc* in, int ni, TensorDesc* out, int no, const void* at, void*,
+                             size_t, void* stream) {
+  XhstAttr x;
+  if (!xent_head_step_sup(in, ni, out, no, at) || !read_xhst(at, &x)) return Status::InvalidArgument;
+  return xent_head_run(in, out, (int32_t*)out[6].data, x.inc, x.scal ? (float*)out[7].data : nullptr, x.aw,
+                       stream);
 }
 
 // ===========================================================================
@@ -401,18 +584,28 @@ struct GroupJob {
   const int32_t* step_in;
   int32_t* step_out;
   int inc;  // step: out = in + inc (0 for the warmup copy)
+  float *P, *M, *V;  // GEMM / column sum with AdamW: the parameter it updates (else nullptr)
 };
 struct GroupArgs {
   int n;
   int start[kMaxJobs + 1];  // first workgroup of each job
   GroupJob job[kMaxJobs];
+  AdamWArgs aa;
+  const float* scal;        // the step's bias corrections {lr / bc1, 1 / bc2}
 };
 
 // Column sum over 64 columns: wave w adds rows w, w + 4, ... in order, the
 // four waves combine as (w0 + w1) + (w2 + w3).
-__device__ __forceinline__ void colsum_block(const GroupJob& j, int b, float* red) {
+// ADAM: apply AdamW to the parameter whose gradient the sums are.
+template <bool ADAM>
+__device__ __forceinline__ void colsum_block(const GroupJob& j, int b, float* red, const StoreAdamW& ad) {
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t n = (int64_t)b * 64 + lane;
+  AdamWLane ar;
+  if (ADAM && w == 0 && n < j.cols) {
+    ar.s = AdamWScalars{ad.scal[0], ad.scal[1]};
+    adamw_load(ad, n, 0, ar);
+  }
   float s = 0.0f;
   if (n < j.cols) {
     const float* p = j.x + n;
@@ -421,22 +614,36 @@ __device__ __forceinline__ void colsum_block(const GroupJob& j, int b, float* re
   }
   red[w * 64 + lane] = s;
   __syncthreads();
-  if (w == 0 && n < j.cols) j.out[n] = (red[lane] + red[64 + lane]) + (red[128 + lane] + red[192 + lane]);
+  if (w == 0 && n < j.cols) {
+    const float sum = (red[lane] + red[64 + lane]) + (red[128 + lane] + red[192 + lane]);
+    j.out[n] = sum;
+    if constexpr (ADAM) adamw_store(ad, n, 0, sum, ar);
+  }
 }
 
 __global__ __launch_bounds__(256) void grad_group_kernel(GroupArgs a) {
   __shared__ f32x4 red[256];
   const int blk = blockIdx.x;
+  // the job whose workgroup range holds blk (independent compares: the
+  // starts load together)
   int j = 0;
-  while (j + 1 < a.n && blk >= a.start[j + 1]) ++j;
+#pragma unroll
+  for (int k = 1; k < kMaxJobs; ++k) j += (k < a.n && blk >= a.start[k]) ? 1 : 0;
   const GroupJob& job = a.job[j];
   const int b = blk - a.start[j];
+  const StoreAdamW ad{job.P, job.M, job.V, a.scal, a.aa};
   switch (job.type) {
     case GJ_GEMM:
-      sg_block(job.gemm, b, red);
+      if (job.P)
+        sg_block<true>(job.gemm, b, red, ad);
+      else
+        sg_block<false>(job.gemm, b, red, ad);
       break;
     case GJ_COLSUM:
-      colsum_block(job, b, reinterpret_cast<float*>(red));
+      if (job.P)
+        colsum_block<true>(job, b, reinterpret_cast<float*>(red), ad);
+      else
+        colsum_block<false>(job, b, reinterpret_cast<float*>(red), ad);
       break;
     case GJ_MEAN:
       block_mean_f64(job.x, job.rows, job.out, reinterpret_cast<double*>(red));
@@ -478,13 +685,9 @@ bool read_group(const void* attr, int ni, int no, GroupRec* recs, int* n) {
   return true;
 }
 
-bool group_fill(const TensorDesc* in, int ni, const TensorDesc* out, int no, const void* attr,
-                GroupArgs* ga) {
-  if (!in || !out || ni < 1 || no < 1) return false;
-  GroupRec recs[kMaxJobs];
-  int n = 0;
-  if (!read_group(attr, ni, no, recs, &n)) return false;
-  GroupArgs a{};
+// The jobs of a group from their records: shapes, the small-GEMM plans, the
+// workgroup ranges, and that no job writes what another job reads or writes.
+bool group_build(const TensorDesc* in, const TensorDesc* out, const GroupRec* recs, int n, GroupArgs& a) {
   a.n = n;
   int blocks = 0;
   for (int k = 0; k < n; ++k) {
@@ -563,6 +766,97 @@ bool group_fill(const TensorDesc* in, int ni, const TensorDesc* out, int no, con
       if (recs[k].type == GJ_GEMM && overlap(w, span_of(in[recs[k].in1]))) return false;
     }
   }
+  return true;
+}
+
+bool group_fill(const TensorDesc* in, int ni, const TensorDesc* out, int no, const void* attr,
+                GroupArgs* ga) {
+  if (!in || !out || ni < 1 || no < 1) return false;
+  GroupRec recs[kMaxJobs];
+  int n = 0;
+  if (!read_group(attr, ni, no, recs, &n)) return false;
+  GroupArgs a{};
+  if (!group_build(in, out, recs, n, a)) return false;
+  if (ga) *ga = a;
+  return true;
+}
+
+// Schema GGRA: a gradient group whose GEMM / column-sum jobs may also apply
+// AdamW to the parameter their output is the gradient of, where each
+// gradient element is stored (the bits of adamw_step on that gradient).
+//   <i n> <fffff lr, beta1, beta2, eps, weight_decay> <i scalars input>,
+//   then n records <iiiiii iii iii>: the GGRP fields, then the P, M, V input
+//   indices and the P, M, V output indices (in place; -1 for a job without
+//   AdamW).  The scalars input holds the step's bias corrections {lr / bc1,
+//   1 / bc2} (2 fp32, written by the launch that advanced the step counter).
+// No step job: the counter is advanced by that earlier launch.
+struct GroupAdamRec {
+  int p_in, m_in, v_in, p_out, m_out, v_out;
+};
+bool group_adamw_fill(const TensorDesc* in, int ni, const TensorDesc* out, int no, const void* attr,
+                      GroupArgs* ga) {
+  if (!in || !out || ni < 1 || no < 1) return false;
+  const AttrBlob& b = blob(attr);
+  if (b.schema_id != AICF_SCHEMA_GGRA || !payload_ok(b, 28)) return false;
+  const int cnt = field<int32_t>(b, 0);
+  if (cnt < 1 || cnt > kMaxJobs || !payload_ok(b, 28 + 48 * (uint32_t)cnt)) return false;
+  const float lr = field<float>(b, 4), b1 = field<float>(b, 8), b2 = field<float>(b, 12);
+  const float eps = field<float>(b, 16), wd = field<float>(b, 20);
+  if (lr != lr || b1 != b1 || b2 != b2 || eps != eps || wd != wd) return false;
+  const int si = field<int32_t>(b, 24);
+  if (si < 0 || si >= ni || dt(in[si]) != DType::kF32 || numel_of(in[si]) != 2 || !in[si].contiguous) return false;
+  GroupRec recs[kMaxJobs];
+  GroupAdamRec ar[kMaxJobs];
+  for (int k = 0; k < cnt; ++k) {
+    const int o = 28 + 48 * k;
+    GroupRec r{field<int32_t>(b, o), field<int32_t>(b, o + 4), field<int32_t>(b, o + 8),
+               field<int32_t>(b, o + 12), field<int32_t>(b, o + 16), field<int32_t>(b, o + 20)};
+    if (r.type < GJ_GEMM || r.type > GJ_MEAN) return false;  // no step job: the updates read the counter
+    if (r.in0 < 0 || r.in0 >= ni || r.out0 < 0 || r.out0 >= no) return false;
+    if (r.type == GJ_GEMM && (r.in1 < 0 || r.in1 >= ni)) return false;
+    recs[k] = r;
+    ar[k] = GroupAdamRec{field<int32_t>(b, o + 24), field<int32_t>(b, o + 28), field<int32_t>(b, o + 32),
+                         field<int32_t>(b, o + 36), field<int32_t>(b, o + 40), field<int32_t>(b, o + 44)};
+  }
+  GroupArgs a{};
+  if (!group_build(in, out, recs, cnt, a)) return false;
+  // every tensor the launch writes, to check the updated ones against
+  const Span scal = span_of(in[si]);
+  for (int k = 0; k < cnt; ++k) {
+    if (overlap(span_of(out[recs[k].out0]), scal)) return false;
+    const GroupAdamRec& r = ar[k];
+    if (r.p_in < 0 && r.m_in < 0 && r.v_in < 0 && r.p_out < 0 && r.m_out < 0 && r.v_out < 0) continue;
+    if (recs[k].type != GJ_GEMM && recs[k].type != GJ_COLSUM) return false;
+    const int idx_in[3] = {r.p_in, r.m_in, r.v_in}, idx_out[3] = {r.p_out, r.m_out, r.v_out};
+    const TensorDesc& G = out[recs[k].out0];
+    // the gradient's element index is the parameter's: a row-major output
+    if (recs[k].type == GJ_GEMM && G.stride[0] != G.shape[1]) return false;
+    for (int x = 0; x < 3; ++x) {
+      if (idx_in[x] < 0 || idx_in[x] >= ni || idx_out[x] < 0 || idx_out[x] >= no) return false;
+      const TensorDesc &T = in[idx_in[x]], &To = out[idx_out[x]];
+      if (dt(T) != DType::kF32 || !T.contiguous || numel_of(T) != numel_of(G)) return false;
+      if (To.data != T.data || !same_shape(To, T)) return false;  // in place
+      const Span w = span_of(T);
+      if (overlap(w, scal)) return false;
+      // nothing else of the launch reads or writes it: the jobs' operands
+      // and outputs, and the other updated tensors
+      for (int l = 0; l < cnt; ++l) {
+        if (overlap(w, span_of(out[recs[l].out0])) || overlap(w, span_of(in[recs[l].in0]))) return false;
+        if (recs[l].type == GJ_GEMM && overlap(w, span_of(in[recs[l].in1]))) return false;
+        const GroupAdamRec& q = ar[l];
+        const int others[3] = {q.p_in, q.m_in, q.v_in};
+        for (int y = 0; y < 3; ++y) {
+          if (others[y] < 0 || (l == k && y == x)) continue;
+          if (others[y] >= ni || overlap(w, span_of(in[others[y]]))) return false;
+        }
+      }
+    }
+    a.job[k].P = (float*)in[r.p_in].data;
+    a.job[k].M = (float*)in[r.m_in].data;
+    a.job[k].V = (float*)in[r.v_in].data;
+  }
+  a.aa = AdamWArgs{lr, b1, b2, eps, wd, 1.0f - b1, 1.0f - b2, 1.0f - lr * wd};
+  a.scal = (const float*)in[si].data;
   if (ga) *ga = a;
   return true;
 }
@@ -577,6 +871,18 @@ Status grad_group_launch(const TensorDesc* in, int ni, TensorDesc* out, int no, 
   if (!group_fill(in, ni, out, no, attr, &a)) return Status::InvalidArgument;
   grad_group_kernel<<<(unsigned)a.start[a.n], 256, 0, as_stream(stream)>>>(a);
   return launch_status("grad_group");
+}
+
+bool grad_group_adamw_sup(const TensorDesc* in, int ni, const TensorDesc* out, int no, const void* attr) {
+  return group_adamw_fill(in, ni, out, no, attr, nullptr);
+}
+
+Status grad_group_adamw_launch(const TensorDesc* in, int ni, TensorDesc* out, int no, const void* attr, void*,
+                               size_t, void* stream) {
+  GroupArgs a;
+  if (!group_adamw_fill(in, ni, out, no, attr, &a)) return Status::InvalidArgument;
+  grad_group_kernel<<<(unsigned)a.start[a.n], 256, 0, as_stream(stream)>>>(a);
+  return launch_status("grad_group_adamw");
 }
 
 // ===========================================================================
@@ -747,9 +1053,91 @@ Status small_gemm_f32(const SmallGemm& g, hipStream_t s) {
   return launch_status("gemm_small");
 }
 
+// ===========================================================================
+// gemm_epilogue (bias+ReLU, bias, ReLU) on the small path with a second
+// output: a copy of B, written by the tiles that read it.  A step whose
+// gradient group updates B in place reads the copy instead (the input
+// gradient dX = dY . W next to AdamW on W), so the copy costs one write of B
+// and no read.
+// ===========================================================================
+namespace {
+
+bool gemm_bcopy_fill(const TensorDesc* in, int ni, const TensorDesc* out, int no, const void* attr,
+                     SmallGemm* pg) {
+  if (!in || !out || ni != 3 || no != 2 || !attr) return false;
+  const AttrBlob& b = blob(attr);
+  if (b.schema_id != AICF_SCHEMA_GEPI || !payload_ok(b, 12)) return false;
+  const bool ta = field<int32_t>(b, 0) != 0, tb = field<int32_t>(b, 4) != 0;
+  const int kind = field<int32_t>(b, 8);
+  if (kind != AICF_EPI_BIAS_RELU && kind != AICF_EPI_BIAS && kind != AICF_EPI_RELU) return false;
+  const TensorDesc &X = in[0], &Y = in[1], &bias = in[2], &O = out[0], &Bc = out[1];
+  for (const TensorDesc* t : {&X, &Y, &O, &Bc})
+    if (dt(*t) != DType::kF32 || t->rank != 2) return false;
+  for (const TensorDesc* t : {&X, &Y})
+    if (t->stride[0] < 0 || t->stride[1] < 0) return false;
+  if (O.stride[1] != 1 || O.stride[0] < O.shape[1]) return false;
+  SmallGemm g{};
+  g.A = (const float*)X.data;
+  g.B = (const float*)Y.data;
+  g.C = (float*)O.data;
+  g.M = ta ? X.shape[1] : X.shape[0];
+  g.K = ta ? X.shape[0] : X.shape[1];
+  g.a_m = ta ? X.stride[1] : X.stride[0];
+  g.a_k = ta ? X.stride[0] : X.stride[1];
+  const int64_t KB = tb ? Y.shape[1] : Y.shape[0];
+  g.N = tb ? Y.shape[0] : Y.shape[1];
+  g.b_k = tb ? Y.stride[1] : Y.stride[0];
+  g.b_n = tb ? Y.stride[0] : Y.stride[1];
+  g.c_m = O.stride[0];
+  if (KB != g.K || O.shape[0] != g.M || O.shape[1] != g.N) return false;
+  if (kind != AICF_EPI_RELU) {
+    if (dt(bias) != DType::kF32 || bias.rank != 1 || bias.shape[0] != g.N || bias.stride[0] <= 0) return false;
+    g.bias = (const float*)bias.data;
+    g.bias_s = bias.stride[0];
+  }
+  g.relu = kind != AICF_EPI_BIAS;
+  // the copy moves B's 16-byte K vectors: K-contiguous, 16-byte aligned rows,
+  // and the copy has B's layout
+  if (g.b_k != 1 || g.K % 4 || (g.N > 1 && g.b_n % 4) || !aligned(Y.data, 16) || !aligned(Bc.data, 16))
+    return false;
+  if (!same_shape(Bc, Y) || Bc.stride[0] != Y.stride[0] || Bc.stride[1] != Y.stride[1]) return false;
+  if (((g.M + 63) / 64) * ((g.N + 63) / 64) >= kSmallGemmMaxTiles64 || !small_gemm_ok(g)) return false;
+  // the written tensors touch nothing the kernel reads and not each other
+  for (const TensorDesc* w : {&O, &Bc}) {
+    if (views_overlap(*w, X) || views_overlap(*w, Y)) return false;
+    if (kind != AICF_EPI_RELU && views_overlap(*w, bias)) return false;
+  }
+  if (views_overlap(O, Bc)) return false;
+  g.bcopy = (float*)Bc.data;
+  if (pg) *pg = g;
+  return true;
+}
+
+bool gemm_bcopy_sup(const TensorDesc* in, int ni, const TensorDesc* out, int no, const void* attr) {
+  return gemm_bcopy_fill(in, ni, out, no, attr, nullptr);
+}
+
+Status gemm_bcopy_launch(const TensorDesc* in, int ni, TensorDesc* out, int no, const void* attr, void*, size_t,
+                         void* stream) {
+  SmallGemm g;
+  if (!gemm_bcopy_fill(in, ni, out, no, attr, &g)) return Status::InvalidArgument;
+  return small_gemm_f32(g, as_stream(stream));
+}
+
+}  // namespace
+
+KernelVariant make_gemm_small_bcopy_f32_variant() {
+  return make("gemm_small_bcopy_f32", gemm_bcopy_launch, gemm_bcopy_sup, AICF_SCHEMA_GEPI);
+}
 KernelVariant make_xent_head_f32_variant() { return make("xent_head_f32", xent_head_launch, xent_head_sup); }
+KernelVariant make_xent_head_step_f32_variant() {
+  return make("xent_head_step_f32", xent_head_step_launch, xent_head_step_sup, AICF_SCHEMA_XHST);
+}
 KernelVariant make_grad_group_f32_variant() {
   return make("grad_group_f32", grad_group_launch, grad_group_sup, AICF_SCHEMA_GGRP);
+}
+KernelVariant make_grad_group_adamw_f32_variant() {
+  return make("grad_group_adamw_f32", grad_group_adamw_launch, grad_group_adamw_sup, AICF_SCHEMA_GGRA);
 }
 KernelVariant make_adamw_multi_f32_variant() {
   return make("adamw_multi_f32", adamw_multi_launch, adamw_multi_sup, AICF_SCHEMA_ADAM);

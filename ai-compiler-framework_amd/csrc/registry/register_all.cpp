@@ -69,7 +69,10 @@ KernelVariant make_gemm_epilogue_bf16_f32out_variant();
 KernelVariant make_gemm_adamw_bf16_variant();
 // smallstep.hip
 KernelVariant make_xent_head_f32_variant();
+KernelVariant make_xent_head_step_f32_variant();
 KernelVariant make_grad_group_f32_variant();
+KernelVariant make_grad_group_adamw_f32_variant();
+KernelVariant make_gemm_small_bcopy_f32_variant();
 KernelVariant make_adamw_multi_f32_variant();
 // eltwise.hip / optim.hip (step tail)
 KernelVariant make_mse_colsum_variant();
@@ -108,6 +111,7 @@ void register_all_kernels_into(KernelRegistry& R) {
       "gemm_bias_relu_f32_naive_v0");
   reg(OpKind::GemmEpilogue, make_gemm_bias_relu_f32_naive_variant(), 0,
       "gemm_epilogue_f32_mfma_v0");
+  reg(OpKind::GemmEpilogue, make_gemm_small_bcopy_f32_variant(), 0, "gemm_small_bcopy_f32_v0");
 
   // BiasAdd (30 / 20 / 0)
   reg(OpKind::BiasAdd, make_bias_add_f16_vec2_variant(), 30, "bias_add_f16_vec2_v0");
@@ -172,7 +176,9 @@ void register_all_kernels_into(KernelRegistry& R) {
   reg(OpKind::Transpose, make_transpose_variant(), 0, "transpose2d_v0");
   reg(OpKind::GemmAdamW, make_gemm_adamw_bf16_variant(), 0, "gemm_adamw_bf16_v0");
   reg(OpKind::XentHead, make_xent_head_f32_variant(), 0, "xent_head_f32_v0");
+  reg(OpKind::XentHead, make_xent_head_step_f32_variant(), 0, "xent_head_step_f32_v0");
   reg(OpKind::GradGroup, make_grad_group_f32_variant(), 0, "grad_group_f32_v0");
+  reg(OpKind::GradGroup, make_grad_group_adamw_f32_variant(), 0, "grad_group_adamw_f32_v0");
   reg(OpKind::AdamWMulti, make_adamw_multi_f32_variant(), 0, "adamw_multi_f32_v0");
   reg(OpKind::MseColsum, make_mse_colsum_variant(), 0, "mse_colsum_v0");
   reg(OpKind::ColsumAdamW, make_colsum_adamw_f32_variant(), 0, "colsum_adamw_f32_v0");

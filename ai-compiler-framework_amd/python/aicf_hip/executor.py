@@ -32,6 +32,7 @@ import torch
 from aicf_cuda import _C
 
 from .ir import IRGraph
+from .lower import EPILOGUE_KINDS, epilogue_kind  # noqa: F401 (re-exported)
 from .plan import BindingPlan, allocate_static_env, bind_views
 
 
@@ -63,6 +64,7 @@ OPNAME_TO_KIND: Dict[str, int] = {
     "gemm_adamw": int(_C.OpKind.GemmAdamW), "xent_head": int(_C.OpKind.XentHead),
     "grad_group": int(_C.OpKind.GradGroup), "adamw_multi": int(_C.OpKind.AdamWMulti),
     "mse_colsum": int(_C.OpKind.MseColsum), "colsum_adamw": int(_C.OpKind.ColsumAdamW),
+    "grad_group_adamw": int(_C.OpKind.GradGroup), "gemm_epilogue_bcopy": int(_C.OpKind.GemmEpilogue),
 }
 
 
@@ -71,6 +73,8 @@ def _fourcc_le(tag: bytes) -> int:
 
 
 SCHEMA_ADAM = _fourcc_le(b"ADAM")
+SCHEMA_GGRA = _fourcc_le(b"GGRA")
+SCHEMA_XHST = _fourcc_le(b"XHST")
 SCHEMA_GEPI = _fourcc_le(b"GEPI")
 SCHEMA_BCOR = _fourcc_le(b"BCOR")
 SCHEMA_SGDS = _fourcc_le(b"SGDS")
@@ -83,37 +87,19 @@ SCHEMA_CADW = _fourcc_le(b"CADW")
 SCHEMA_GEMM = int.from_bytes(b"GEMM", "big")
 SCHEMA_RSUM = int.from_bytes(b"RSUM", "big")
 
-EPILOGUE_KINDS = {"bias_relu": 0, "bias": 1, "relu": 2, "bias_gelu": 3, "gelu": 4, "dgelu": 5}
-
-
-def epilogue_kind(attrs: Dict[str, Any]) -> int:
-    """GEPI kind from either the executor's `epilogue` attr (exec.py:223-252)
-    or StageC's epilogue_act / epilogue_bias pair."""
-    if "epilogue" in attrs:
-        e = str(attrs["epilogue"]).strip().lower().replace("+", "_")
-        e = {"biasrelu": "bias_relu", "bias_only": "bias", "biasonly": "bias",
-             "relu_only": "relu", "reluonly": "relu"}.get(e, e)
-        return EPILOGUE_KINDS.get(e, 0)
-    act = str(attrs.get("epilogue_act", "relu")).lower()
-    bias = bool(attrs.get("epilogue_bias", True))
-    if act == "dgelu":
-        cs = attrs.get("epilogue_colsum", False)
-        return 7 if cs == "partials" else 6 if cs else 5
-    if act == "gelu":
-        return 3 if bias else 4
-    if act in ("none", ""):
-        return 1
-    return 0 if bias else 2
 
 
 def warmup_attrs(op: str, attrs: Dict[str, Any]) -> Dict[str, Any]:
     """Attributes of an op under AICF_WARMUP=1 (exec.py:423-431): every Adam
-    update runs with lr 0, and a grad_group's step_inc job and mse_colsum's
-    step increment add 0 (the copy the warmup makes of step_inc)."""
-    if op in ("adam_step", "adamw_step", "gemm_adamw", "adamw_multi", "colsum_adamw"):
+    update runs with lr 0, and a grad_group's step_inc job and the step
+    increments of mse_colsum and xent_head add 0 (the copy the warmup makes
+    of step_inc)."""
+    if op in ("adam_step", "adamw_step", "gemm_adamw", "adamw_multi", "colsum_adamw", "grad_group_adamw"):
         return dict(attrs, lr=0.0)
     if op == "mse_colsum":  # its step_inc part adds 0
         return dict(attrs, step_inc=0)
+    if op == "xent_head" and "step_inc" in attrs:  # adds 0; the bias corrections it writes carry lr 0
+        return dict(attrs, step_inc=0, **({"lr": 0.0} if "lr" in attrs else {}))
     if op == "grad_group":
         return dict(attrs, jobs=[[j[0], j[1], j[2], j[3], 0 if j[0] == 3 else j[4], j[5]]
                                  for j in attrs.get("jobs", [])])
@@ -125,7 +111,7 @@ def pack_attrs(op: str, attrs: Dict[str, Any]) -> Tuple[int, bytes]:
     a = dict(attrs or {})
     if op == "gemm":
         return 0, struct.pack("<ii", int(bool(a.get("transA", False))), int(bool(a.get("transB", False))))
-    if op == "gemm_epilogue":
+    if op in ("gemm_epilogue", "gemm_epilogue_bcopy"):
         return SCHEMA_GEPI, struct.pack("<iii", int(bool(a.get("transA", False))),
                                         int(bool(a.get("transB", False))), epilogue_kind(a))
     if op == "gemm_adamw":
@@ -142,6 +128,17 @@ def pack_attrs(op: str, attrs: Dict[str, Any]) -> Tuple[int, bytes]:
     if op == "grad_group":
         jobs = [tuple(int(x) for x in j) for j in a.get("jobs", [])]
         return SCHEMA_GGRP, struct.pack("<i", len(jobs)) + b"".join(struct.pack("<iiiiii", *j) for j in jobs)
+    if op == "grad_group_adamw":
+        jobs = [tuple(int(x) for x in j) for j in a.get("jobs", [])]
+        head = struct.pack("<ifffffi", len(jobs), float(a.get("lr", 1e-3)), float(a.get("beta1", 0.9)),
+                           float(a.get("beta2", 0.999)), float(a.get("eps", 1e-8)),
+                           float(a.get("weight_decay", 0.0)), int(a["scalars_input"]))
+        return SCHEMA_GGRA, head + b"".join(struct.pack("<" + "i" * 12, *j) for j in jobs)
+    if op == "xent_head" and "step_inc" in a:
+        pay = struct.pack("<i", int(a["step_inc"]))
+        if "lr" in a:  # the step's AdamW bias corrections too
+            pay += struct.pack("<fff", float(a["lr"]), float(a.get("beta1", 0.9)), float(a.get("beta2", 0.999)))
+        return SCHEMA_XHST, pay
     if op in ("adam_step", "adamw_step", "adamw_multi"):
         vals = [float(a.get("lr", 1e-3)), float(a.get("beta1", 0.9)), float(a.get("beta2", 0.999)),
                 float(a.get("eps", 1e-8))]

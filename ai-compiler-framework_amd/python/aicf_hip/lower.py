@@ -53,7 +53,7 @@ _PRIMITIVES = {
     "sgd_step", "gelu", "gelu_bwd", "softmax_xent", "row_softmax", "row_reduce", "mse_loss",
     "adamw_step", "layernorm_fwd", "layernorm_bwd", "batchnorm_fwd", "batchnorm_bwd",
     "transpose", "gemm_adamw", "xent_head", "grad_group", "adamw_multi", "mse_colsum",
-    "colsum_adamw",
+    "colsum_adamw", "grad_group_adamw", "gemm_epilogue_bcopy",
 }
 
 _ALIASES = {"adamstep": "adam_step", "stepinc": "step_inc", "biascorr": "bias_corr",
@@ -61,6 +61,29 @@ _ALIASES = {"adamstep": "adam_step", "stepinc": "step_inc", "biascorr": "bias_co
             "linearbwd": "linear_bwd", "gelubwd": "gelu_bwd", "softmaxxent": "softmax_xent",
             "mseloss": "mse_loss", "adamwstep": "adamw_step", "rowsoftmax": "row_softmax",
             "rowreduce": "row_reduce"}
+
+
+EPILOGUE_KINDS = {"bias_relu": 0, "bias": 1, "relu": 2, "bias_gelu": 3, "gelu": 4, "dgelu": 5}
+
+
+def epilogue_kind(attrs: Dict[str, Any]) -> int:
+    """GEPI kind from either the executor's `epilogue` attr (exec.py:223-252)
+    or StageC's epilogue_act / epilogue_bias pair."""
+    if "epilogue" in attrs:
+        e = str(attrs["epilogue"]).strip().lower().replace("+", "_")
+        e = {"biasrelu": "bias_relu", "bias_only": "bias", "biasonly": "bias",
+             "relu_only": "relu", "reluonly": "relu"}.get(e, e)
+        return EPILOGUE_KINDS.get(e, 0)
+    act = str(attrs.get("epilogue_act", "relu")).lower()
+    bias = bool(attrs.get("epilogue_bias", True))
+    if act == "dgelu":
+        cs = attrs.get("epilogue_colsum", False)
+        return 7 if cs == "partials" else 6 if cs else 5
+    if act == "gelu":
+        return 3 if bias else 4
+    if act in ("none", ""):
+        return 1
+    return 0 if bias else 2
 
 
 def _item(op: str, inputs, outputs, attrs=None) -> Dict[str, Any]:
@@ -358,9 +381,13 @@ def pick_kernel_id(ir: IRGraph, it: Dict[str, Any]) -> Optional[str]:
     if op == "transpose":
         return "transpose2d_v0"
     if op == "xent_head":
-        return "xent_head_f32_v0"
+        return "xent_head_step_f32_v0" if len(ins) == 6 else "xent_head_f32_v0"
     if op == "grad_group":
         return "grad_group_f32_v0"
+    if op == "grad_group_adamw":
+        return "grad_group_adamw_f32_v0"
+    if op == "gemm_epilogue_bcopy":
+        return "gemm_small_bcopy_f32_v0"
     if op == "adamw_multi":
         return "adamw_multi_f32_v0"
     if op == "mse_colsum":
@@ -948,12 +975,203 @@ def fuse_adamw_multi(ir: IRGraph, lowered: Lowered) -> Lowered:
     return out
 
 
-def fuse_small_step(ir: IRGraph, lowered: Lowered, keep: Iterable[int] = ()) -> Lowered:
+def _bcopy_source(ir: IRGraph, lowered: Lowered, gi: int, P: int) -> Optional[int]:
+    """Index of the last op before lowered[gi] that can write a copy of P as
+    it reads it: a small fp32 gemm_epilogue (bias+ReLU, bias or ReLU) with
+    P as its B operand read K-contiguously (transB) in 16-byte vectors, and
+    nothing between it and lowered[gi] writes P."""
+    for k in range(gi - 1, -1, -1):
+        it = lowered[k]
+        if any(_base(ir, o) == P for o in it["outputs"]):
+            return None
+        if _kind(it) != "gemm_epilogue" or len(it["inputs"]) != 3 or len(it["outputs"]) != 1 or \
+                int(it["inputs"][1]) != P:
+            continue
+        a = it.get("attrs") or {}
+        if not bool(a.get("transB", False)) or epilogue_kind(a) not in (0, 1, 2):
+            continue
+        A, C = int(it["inputs"][0]), int(it["outputs"][0])
+        if not all(_f32(ir, v) for v in (A, P, C)) or _base(ir, C) == P or _base(ir, A) == P:
+            continue
+        N, K = (int(d) for d in ir.values[P].shape)
+        sa = ir.values[A].shape
+        M = int(sa[1] if bool(a.get("transA", False)) else sa[0])
+        if K % 4 or not _aligned16(ir, P) or ((M + 63) // 64) * ((N + 63) // 64) >= SMALL_GEMM_MAX_TILES64:
+            continue
+        return k
+    return None
+
+
+def _adamw_ok(ir: IRGraph, it: Dict[str, Any]) -> bool:
+    return (_kind(it) == "adamw_step" and len(it["inputs"]) == 5 and len(it["outputs"]) == 3
+            and [int(x) for x in it["outputs"]] == [int(it["inputs"][k]) for k in (0, 2, 3)]
+            and all(_f32(ir, int(v)) for v in it["inputs"][:4]))
+
+
+def fuse_adamw_into_group(ir: IRGraph, lowered: Lowered) -> Lowered:
+    """grad_group followed by adamw_step(P, G, M, V, step) -> (P, M, V) ops
+    whose G is the output of one of the group's GEMM or column-sum jobs ==>
+    grad_group_adamw: each update applied where its gradient is stored (the
+    bits of adamw_step).  Of the adamw_steps that follow the group directly,
+    those whose gradient the group computes move into it; the others stay
+    after it.  Conditions:
+      * same step and hyperparameters, distinct fp32 P, M, V buffers, G the
+        whole output of its job;
+      * the group's step_inc job leaves the group for the xent_head right
+        before it, which advances the counter and writes the advanced step's
+        bias corrections {lr / bc1, 1 / bc2} once (a new 2-float value the
+        updates read, the values adamw_step derives from the counter);
+      * no job reads P, M or V, except a GEMM job with P as its B operand:
+        that job reads a copy of P written by an earlier small gemm_epilogue
+        that reads P K-contiguously (gemm_epilogue_bcopy), when nothing in
+        between writes P."""
+    out = list(lowered)
+    gi = 0
+    while gi < len(out):
+        g = out[gi]
+        if _kind(g) != "grad_group":
+            gi += 1
+            continue
+        run = []
+        for it in out[gi + 1:]:
+            if not _adamw_ok(ir, it):
+                break
+            run.append(it)
+        res = _group_adamw(ir, out, gi, run) if run else None
+        if res is None:
+            gi += 1
+            continue
+        out = res
+        gi += 1
+    return out
+
+
+def _group_adamw(ir: IRGraph, lowered: Lowered, gi: int, run: Lowered) -> Optional[Lowered]:
+    g = lowered[gi]
+    gins, gouts = [int(v) for v in g["inputs"]], [int(v) for v in g["outputs"]]
+    jobs = [list(j) for j in g["attrs"]["jobs"]]
+    key = lambda it: tuple(sorted((it.get("attrs") or {}).items()))  # noqa: E731
+    step = int(run[0]["inputs"][4])
+    if any(int(it["inputs"][4]) != step or key(it) != key(run[0]) for it in run):
+        return None
+    # jobs as (type, [inputs], [output], f0, f1); the step job goes
+    jtup = []
+    step_job = None
+    for j in jobs:
+        typ = int(j[0])
+        ji = [gins[j[1]]] + ([gins[j[2]]] if typ == GJ_GEMM else [])
+        if typ == GJ_STEP:
+            if step_job is not None or gins[j[1]] != step or gouts[j[3]] != step:
+                return None
+            step_job = j
+            continue
+        if any(_base(ir, v) == _base(ir, step) for v in ji + [gouts[j[3]]]):
+            return None
+        jtup.append([typ, ji, gouts[j[3]], int(j[4]), int(j[5]), None])
+    # the step counter: advanced by the xent_head right before the group,
+    # which also derives the step's bias corrections once (a launch of its
+    # own would cost what the fusion saves)
+    h = lowered[gi - 1] if gi > 0 else None
+    if step_job is None or h is None or _kind(h) != "xent_head" or len(h["inputs"]) != 5 or \
+            any(_base(ir, v) == _base(ir, step) for v in list(h["inputs"]) + list(h["outputs"])):
+        return None
+    # the updates whose gradient is a GEMM or column-sum job's whole output
+    fused, rest = [], []
+    for it in run:
+        P, G, M, V = (int(v) for v in it["inputs"][:4])
+        hit = [t for t in jtup if t[2] == G and t[0] in (GJ_GEMM, GJ_COLSUM) and t[5] is None]
+        if len(hit) != 1 or tuple(ir.values[P].shape) != tuple(ir.values[G].shape) or \
+                any(_numel(ir, v) != _numel(ir, G) for v in (M, V)):
+            rest.append(it)
+            continue
+        hit[0][5] = (P, M, V)
+        fused.append(it)
+    out = list(lowered)
+    # a job that reads a moved update's P, M or V: a GEMM's B operand P can
+    # read a copy of P; otherwise that update stays behind
+    copies: Dict[int, tuple] = {}  # P -> (index of the op that copies it, the jobs that read it)
+    for it in list(fused):
+        P, M, V = (int(it["inputs"][k]) for k in (0, 2, 3))
+        bases = {_base(ir, v) for v in (P, M, V)}
+        readers = [(t, pos) for t in jtup for pos, v in enumerate(t[1]) if _base(ir, v) in bases]
+        ok = not any(_base(ir, t[2]) in bases for t in jtup)
+        ok = ok and all(t[0] == GJ_GEMM and pos == 1 and t[1][1] == P and _base(ir, P) == P
+                        for t, pos in readers)
+        k = _bcopy_source(ir, out, gi, P) if ok and readers else None
+        if not ok or (readers and k is None):
+            fused.remove(it)
+            rest.append(it)
+            for t in jtup:
+                if t[5] is not None and t[5][0] == P:
+                    t[5] = None
+            continue
+        if readers:
+            copies[P] = (k, readers)
+    rest = [it for it in run if it in rest]  # in their original order
+    pmv_bases = [_base(ir, int(it["inputs"][k])) for it in fused for k in (0, 2, 3)]
+    if not fused or len(set(pmv_bases)) != len(pmv_bases) or _base(ir, step) in pmv_bases:
+        return None
+    # the updates that stay behind touch none of the moved ones' buffers
+    if any(_base(ir, v) in pmv_bases for it in rest for v in it["inputs"]):
+        return None
+    if len({k for k, _ in copies.values()}) != len(copies):
+        return None
+    for P, (k, readers) in copies.items():
+        src = ir.values[P]
+        cv = ir.new_value(name=f"{src.name}.copy", shape=tuple(src.shape), dtype=src.dtype, device=src.device)
+        g0 = out[k]
+        out[k] = _item("gemm_epilogue_bcopy", list(g0["inputs"]), [int(g0["outputs"][0]), cv.id],
+                       dict(g0.get("attrs") or {}))
+        for t, pos in readers:
+            t[1][pos] = cv.id
+    # the head advances the counter and writes the step's bias corrections
+    # once ({lr / bc1, 1 / bc2}), which the group's updates read
+    hp = dict(run[0].get("attrs") or {})
+    sv = ir.values[step]
+    scal = ir.new_value(name=f"{sv.name}.adamw_scalars", shape=(2,), dtype="torch.float32", device=sv.device)
+    h = out[gi - 1]
+    out[gi - 1] = _item("xent_head", list(h["inputs"]) + [step], list(h["outputs"]) + [step, scal.id],
+                        dict(h.get("attrs") or {}, step_inc=int(step_job[4]), lr=float(hp.get("lr", 1e-3)),
+                             beta1=float(hp.get("beta1", 0.9)), beta2=float(hp.get("beta2", 0.999))))
+    item = _group_adamw_item(jtup, scal.id, hp)
+    n = len(run)
+    return out[:gi] + [item] + rest + out[gi + 1 + n:]
+
+
+def _group_adamw_item(jtup, scal: int, hp: Dict[str, Any]) -> Dict[str, Any]:
+    ins: List[int] = []
+    outs: List[int] = []
+
+    def idx(lst, v):
+        if v not in lst:
+            lst.append(v)
+        return lst.index(v)
+
+    recs = []
+    for typ, ji, jo, f0, f1, pmv in jtup:
+        r = [typ, idx(ins, ji[0]), idx(ins, ji[1]) if len(ji) > 1 else 0, idx(outs, jo), f0, f1]
+        if pmv is None:
+            r += [-1] * 6
+        else:
+            r += [idx(ins, v) for v in pmv] + [idx(outs, v) for v in pmv]
+        recs.append(r)
+    si = idx(ins, scal)
+    attrs = {"jobs": recs, "scalars_input": si, "lr": float(hp.get("lr", 1e-3)),
+             "beta1": float(hp.get("beta1", 0.9)), "beta2": float(hp.get("beta2", 0.999)),
+             "eps": float(hp.get("eps", 1e-8)), "weight_decay": float(hp.get("weight_decay", 0.0))}
+    return _item("grad_group_adamw", ins, outs, attrs)
+
+
+def fuse_small_step(ir: IRGraph, lowered: Lowered, keep: Iterable[int] = (), *,
+                    adamw_into_group: bool = True) -> Lowered:
     """StageF: drop_dead_saves -> fuse_xent_head -> group_small_jobs ->
-    fuse_adamw_multi.  keep: values the caller reads after the step."""
+    fuse_adamw_into_group (adamw_into_group) -> fuse_adamw_multi.  keep:
+    values the caller reads after the step."""
     low = drop_dead_saves(ir, lowered, keep)
     low = fuse_xent_head(ir, low)
     low = group_small_jobs(ir, low)
+    if adamw_into_group:
+        low = fuse_adamw_into_group(ir, low)
     low = fuse_adamw_multi(ir, low)
     assert not any(_kind(it) == "loss_mean" for it in low)
     return low
@@ -962,14 +1180,15 @@ def fuse_small_step(ir: IRGraph, lowered: Lowered, keep: Iterable[int] = ()) -> 
 def compile_lowered(ir: IRGraph, *, fuse: bool = True, fuse_bias: bool = False,
                     nt_layout: Any = False, nt_min_flops: float = 2.0 ** 30,
                     fuse_optimizer: bool = False, fuse_colsum: bool = False,
-                    fuse_small: bool = False, fuse_tail: bool = False,
+                    fuse_small: Any = False, fuse_tail: bool = False,
                     keep_values: Iterable[int] = ()) -> Lowered:
     """StageA -> StageC -> (StageC') -> (StageD) -> (StageE) -> (StageF) -> (StageG) -> StageB.
     nt_layout: False (no StageD), True / "all" (transpose every M/N-contiguous
     16-bit operand) or "cost" (transpose only where that is cheaper than
     reading it in place); fuse_colsum: StageC'; fuse_optimizer: StageE;
-    fuse_small: StageF; fuse_tail: StageG.  keep_values: value ids the caller
-    reads after a step, which the rewrites must keep writing."""
+    fuse_small: StageF (True; "four" leaves its AdamW updates in their own
+    launch); fuse_tail: StageG.  keep_values: value ids the caller reads
+    after a step, which the rewrites must keep writing."""
     low = lower_to_backend_ops(ir)
     if fuse:
         low = fuse_gemm_epilogue(ir, low, fuse_bias=fuse_bias)
@@ -981,7 +1200,7 @@ def compile_lowered(ir: IRGraph, *, fuse: bool = True, fuse_bias: bool = False,
     if fuse_optimizer:
         low = fuse_optimizer_into_gemms(ir, low)
     if fuse_small:
-        low = fuse_small_step(ir, low, keep_values)
+        low = fuse_small_step(ir, low, keep_values, adamw_into_group=fuse_small != "four")
     if fuse_tail:
         low = fuse_step_tail(ir, low)
     return apply_kernel_selection(ir, low)

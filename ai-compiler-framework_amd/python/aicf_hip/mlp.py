@@ -32,10 +32,13 @@ F32, BF16, I32 = "torch.float32", "torch.bfloat16", "torch.int32"
 # ============================================================ xent MLP (fp32)
 def build_mlp_xent(B: int = 64, din: int = 784, dh: int = 256, dout: int = 10, *,
                    lr: float = 1e-3, beta1: float = 0.9, beta2: float = 0.999,
-                   eps: float = 1e-8, device: str = "cuda:0", fuse_small: bool = False):
-    """fuse_small: StageF (the step in four launches: forward GEMM, xent
-    head, gradient group, multi-tensor AdamW); off, the lowering is the
-    reference pipeline's (17 ops)."""
+                   eps: float = 1e-8, device: str = "cuda:0", fuse_small=False):
+    """fuse_small: StageF, the step in three launches (forward GEMM that
+    also copies W0 for the input gradient, xent head that advances the step
+    counter, gradient group with each AdamW update applied where its gradient
+    is stored); "four": StageF with the updates in a multi-tensor AdamW
+    launch of their own; off, the lowering is the reference pipeline's (17
+    ops)."""
     ir = IRGraph(name=f"mlp_xent_{B}x{din}x{dh}x{dout}")
     nv = lambda n, s, dt=F32: ir.new_value(name=n, shape=s, dtype=dt, device=device)  # noqa: E731
     x = nv("x", (B, din))

@@ -201,33 +201,52 @@ def bench_c4(C, dtype="bf16", shapes=C4_SHAPES, acts=("none", "relu", "gelu"), i
 
 
 # C1: the reference MLP (fp32, B=64, 784->256(ReLU)->10, softmax-xent, Adam)
-def bench_c1(steps=200, warmup=5, fuse_small=True):
-    """Replayed-graph time of one C1 train step; fuse_small: the four-launch
-    lowering (StageF), else the reference pipeline's 17 ops."""
+C1_VARIANTS = {"three_launch": True, "four_launch": "four", "reference_lowering": False}
+
+
+def bench_c1(rounds=10, chunk=20, warm_s=STEP_WARM_S):
+    """Replayed-graph time of one C1 train step for each lowering (True: the
+    three-launch StageF plan, "four": its four-launch form, False: the
+    reference pipeline's 17 ops), each on a graph handle of its own, warmed
+    together for warm_s, then timed in `rounds` rounds of `chunk` replays
+    with the lowerings alternated (order reversed every other round), so
+    that clock and box state are shared."""
     import torch
 
     from aicf_hip import mlp
 
-    ir, lowered, plan = mlp.build_mlp_xent(fuse_small=fuse_small)
     data = mlp.init_mlp_xent()
-    params = {k: torch.from_numpy(v.copy()).cuda() for k, v in data.items() if "." in k}
-    inputs = {"x": torch.from_numpy(data["x"]).cuda(), "t": torch.from_numpy(data["t"]).cuda()}
-    ex = mlp.make_executor(ir, lowered, plan)
-    ex.build_env(inputs=inputs, params=params, reuse_static=False)
-    ex.capture(inputs=inputs, params=params, reuse_static=True)
-    gs = torch.cuda.current_stream()  # graph_launch replays on the caller's stream
-    ex.replay(warmup)
+    exs = {}
+    for k, fs in C1_VARIANTS.items():
+        ir, lowered, plan = mlp.build_mlp_xent(fuse_small=fs)
+        params = {n: torch.from_numpy(v.copy()).cuda() for n, v in data.items() if "." in n}
+        inputs = {"x": torch.from_numpy(data["x"]).cuda(), "t": torch.from_numpy(data["t"]).cuda()}
+        ex = mlp.make_executor(ir, lowered, plan, own_graph=True)
+        ex.build_env(inputs=inputs, params=params, reuse_static=False)
+        ex.capture(inputs=inputs, params=params, reuse_static=True)
+        exs[k] = (ex, lowered)
+    s = torch.cuda.current_stream()  # graph_launch replays on the caller's stream
+    for ex, _ in exs.values():
+        ex.replay(3)
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(gs)
-    ex.replay(steps)
-    e1.record(gs)
-    torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) * 1e3 / steps
-    loss = float(ex.value("loss").item())
-    ex.reset_graph()
-    return {"value": round(us, 2), "unit": "us/step", "steps_per_s": round(1e6 / us, 1),
-            "ops_per_step": len(lowered), "loss_after": loss}
+    _warm(lambda: [ex.replay(5) for ex, _ in exs.values()], warm_s)
+    tot = {k: 0.0 for k in exs}
+    names = list(exs)
+    for r in range(rounds):
+        for k in (names if r % 2 == 0 else names[::-1]):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            exs[k][0].replay(chunk)
+            e1.record(s)
+            torch.cuda.synchronize()
+            tot[k] += e0.elapsed_time(e1)
+    out = {}
+    for k, (ex, lowered) in exs.items():
+        us = tot[k] * 1e3 / (rounds * chunk)
+        out[k] = {"value": round(us, 2), "unit": "us/step", "steps_per_s": round(1e6 / us, 1),
+                  "ops_per_step": len(lowered), "loss_after": float(ex.value("loss").item())}
+        ex.close()
+    return out
 
 
 # ------------------------------------------------------------------ softmax
@@ -1377,8 +1396,8 @@ def stats_report(stats_csv, trace_csv, steps):
 def c1_trace_report(stats_csv, trace_csv):
     """Markdown summary of `rocprofv3 --kernel-trace --stats` over
     `bench.py --c1-only`: per-kernel totals, then the last replayed step of
-    the four-launch lowering and of the reference's 17-op lowering, launch by
-    launch."""
+    the three-launch lowering, of the four-launch one and of the reference's
+    17-op lowering, launch by launch."""
     import csv
 
     with open(stats_csv, newline="") as f:
@@ -1400,8 +1419,9 @@ def c1_trace_report(stats_csv, trace_csv):
         "gpurun_out/c1prof/c1_kernel_trace.csv",
         "```",
         "",
-        "Process contents: 5 warmup + 50 timed replays of the four-launch step (StageF), then the same for "
-        "the reference pipeline's 17-op lowering.",
+        "Process contents: the three-launch step (StageF), its four-launch form (AdamW in a launch of its "
+        "own) and the reference pipeline's 17-op lowering, each captured on a graph handle of its own; "
+        "warmed together, then 5 rounds of 10 replays each, alternated.",
         "",
         "| kernel | calls | avg us | % time |",
         "|---|---:|---:|---:|",
@@ -1409,13 +1429,23 @@ def c1_trace_report(stats_csv, trace_csv):
     for r in stats[:20]:
         lines.append(f"| `{short(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
                      f"{float(r['Percentage']):.2f} |")
-    fused_end = [i for i, r in enumerate(trace) if "adamw_multi" in r["Kernel_Name"]]
-    # the reference lowering's step ends with its four adamw_step launches
+    # the last step of each lowering in the kernel sequence (the lowerings
+    # are replayed alternated): three-launch = gemm, head, group not
+    # followed by adamw_multi; four-launch = the same followed by it
     ktr = [r for r in trace if "copyBuffer" not in r["Kernel_Name"]]
+    nm = [r["Kernel_Name"] for r in ktr]
+    three = four = None
+    for i in range(len(nm) - 2):
+        if "gemm_small" in nm[i] and "xent_head" in nm[i + 1] and "grad_group" in nm[i + 2]:
+            if i + 3 < len(nm) and "adamw_multi" in nm[i + 3]:
+                four = ktr[i:i + 4]
+            else:
+                three = ktr[i:i + 3]
+    # the reference lowering's step ends with its four adamw_step launches
     ad = [i for i, r in enumerate(ktr) if "adamw_vec4" in r["Kernel_Name"]
           and (i + 1 == len(ktr) or "adamw_vec4" not in ktr[i + 1]["Kernel_Name"])]
-    ref_step = ktr[ad[-2] + 1:ad[-1] + 1] if len(ad) >= 2 else []
-    for title, step in (("four-launch lowering", trace[fused_end[-1] - 3:fused_end[-1] + 1] if fused_end else []),
+    ref_step = ktr[ad[-1] - 17:ad[-1] + 1] if ad and ad[-1] >= 17 else []
+    for title, step in (("three-launch lowering", three or []), ("four-launch lowering", four or []),
                         ("reference 17-op lowering", ref_step)):
         if not step:
             continue
@@ -1513,7 +1543,7 @@ def main():
         streaming_only(C)
         return
     if args.c1_only:
-        print(json.dumps({"four_launch": bench_c1(steps=50), "reference_lowering": bench_c1(steps=50, fuse_small=False)}))
+        print(json.dumps(bench_c1(rounds=5, chunk=10, warm_s=0.05)))
         return
     if args.vendor_compare:
         vendor_compare(C, args.vendor_set)
@@ -1637,8 +1667,11 @@ def main():
             "note": "the headline plan and each variant on graph handles of their own, warmed together, then "
                     "10 rounds of 10 replays each with the variants alternated (order reversed every other round)"}
         log(f"[bench] mlp variants alternated {alt}")
-        c1 = bench_c1()
-        c1["reference_lowering"] = bench_c1(fuse_small=False)
+        c1v = bench_c1()
+        c1 = dict(c1v["three_launch"], four_launch=c1v["four_launch"],
+                  reference_lowering=c1v["reference_lowering"],
+                  note="each lowering on a graph handle of its own, warmed together, then 10 rounds of 20 "
+                       "replays with the lowerings alternated")
         comps["c1_mlp_fp32_64x784x256x10_step"] = c1
         log(f"[bench] c1 {c1}")
         for dt, shapes in (("bf16", C4_SHAPES), ("fp32", C4_SHAPES)):

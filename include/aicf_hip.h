@@ -73,9 +73,12 @@ extern "C" {
 #define AICF_OP_GEMM_ADAMW 24   /* A, B, P, M, V, step -> P, M, V, Wb: AdamW on P with grad op(A).op(B) (schema GADW) */
 #define AICF_OP_XENT_HEAD 25     /* H, W, b, labels, S -> logits, dlogits, argmax, row loss, dH, dX: the
                                     classifier head of a ReLU MLP forward and backward (softmax xent,
-                                    dH = dlogits.W, dX = dH where S > 0) */
+                                    dH = dlogits.W, dX = dH where S > 0); with schema XHST a 6th
+                                    input and 7th output, the step counter, advanced in place (and
+                                    an 8th output, the step's AdamW bias corrections) */
 #define AICF_OP_GRAD_GROUP 26    /* independent small jobs in one launch: GEMMs, column sums, a loss
-                                    mean, the step counter (schema GGRP) */
+                                    mean, the step counter (schema GGRP); or GEMMs, column sums and
+                                    the mean with AdamW applied where a gradient is stored (GGRA) */
 #define AICF_OP_ADAMW_MULTI 27   /* (P, G, M, V) x T, step -> (P, M, V) x T: AdamW over T tensors (schema ADAM) */
 #define AICF_OP_MSE_COLSUM 28    /* pred, target, step -> dPred, loss, loss partials, column partials of
                                     dPred [P, N], step (+1): MSE loss and gradient, the gradient's
@@ -106,6 +109,14 @@ extern "C" {
 #define AICF_SCHEMA_GADW 0x57444147u /* appended: b"GADW" little-endian, <ii fffff> transA, transB, lr, b1, b2, eps, wd */
 #define AICF_SCHEMA_MSCS 0x5343534Du /* appended: b"MSCS" little-endian, <f i> gradient scale (<= 0: 2/n), step += i (0 or 1) */
 #define AICF_SCHEMA_CADW 0x57444143u /* appended: b"CADW" little-endian, <i fffff> T, lr, b1, b2, eps, wd */
+#define AICF_SCHEMA_GGRA 0x41524747u /* appended: b"GGRA" little-endian, <i n> <fffff> lr, b1, b2, eps, wd,
+                                       <i> input holding the step's bias corrections {lr/bc1, 1/bc2}
+                                       (2 f32), then n x <iiiiii iii iii>: the GGRP record (types 0-2),
+                                       the P, M, V input and P, M, V output indices of the parameter
+                                       the job's output is the gradient of (-1: none) */
+#define AICF_SCHEMA_XHST 0x54534858u /* appended: b"XHST" little-endian, <i> step += i (0 or 1), optionally
+                                       <fff> lr, b1, b2: an 8th output (2 f32) receives the advanced
+                                       step's AdamW bias corrections {lr/bc1, 1/bc2} */
 
 /* GEPI epilogue kinds.  0..2 are the values core_v2/exec.py:223-252 packs;
  * 3..7 are appended (no counterpart in the reference). */
@@ -119,6 +130,8 @@ extern "C" {
                                    workspace [P, N] with P >= M/256 (no reference counterpart) */
 #define AICF_EPI_DGELU_PARTIALS 7 /* as 5, plus output [M/256, N] f32: row t of it is the column sums of
                                      out's 256-row block t (finished by a later COLSUM_ADAMW) */
+/* Kinds 0..2 with a second output of B's shape and strides (fp32, small
+ * problems, K-contiguous B): that output receives a copy of B (appended). */
 
 /*
  * Replaces tensor_desc.hpp:88-158 (struct TensorDesc).  Field order, types

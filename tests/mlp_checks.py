@@ -86,9 +86,9 @@ class XentOracle:
 
 
 def xent_setup(seed: int = 0, device: str = "cuda:0", own_graph: bool = False, B=64, din=784,
-               dh=256, dout=10, fuse_small: bool = False):
+               dh=256, dout=10, fuse_small=False):
     """Executor, GPU inputs/params and oracle of the xent MLP from a seed
-    (fuse_small: the four-launch lowering)."""
+    (fuse_small: StageF, True for three launches, "four" for four)."""
     ir, lowered, plan = build_mlp_xent(B, din, dh, dout, device=device, fuse_small=fuse_small)
     data = init_mlp_xent(B, din, dh, dout, seed=seed)
     params = {k: torch.from_numpy(v.copy()).to(device) for k, v in data.items() if "." in k}
@@ -98,7 +98,7 @@ def xent_setup(seed: int = 0, device: str = "cuda:0", own_graph: bool = False, B
 
 
 def check_mlp_small(device: str = "cuda:0", verbose: bool = False, B=64, din=784, dh=256,
-                    dout=10, fuse_small: bool = False) -> Dict[str, object]:
+                    dout=10, fuse_small=False) -> Dict[str, object]:
     """Runs one eager step and two captured+replayed steps of the xent MLP and
     checks loss, argmax, every gradient and every updated parameter against
     the CPU oracle (fp64 chain for loss/grads; the reference-exact AdamW

@@ -1,9 +1,10 @@
-"""StageF (the small-step lowering) and the host-side contracts of its three
-ops, without a GPU: the reference MLP's step lowers to four launches whose
-jobs are independent, the unfused values the oracle reads are all produced,
-the AICF_WARMUP rewrite reaches the fused ops, and supported() refuses what
-the kernels cannot run (overlapping group jobs, aliasing Adam buffers,
-heads wider than the kernel) before any launch."""
+"""StageF (the small-step lowering) and the host-side contracts of its ops,
+without a GPU: the reference MLP's step lowers to three launches (four with
+the AdamW updates in a launch of their own) whose jobs are independent, the
+unfused values the oracle reads are all produced, the AICF_WARMUP rewrite
+reaches the fused ops, and supported() refuses what the kernels cannot run
+(overlapping group jobs, aliasing Adam buffers, heads wider than the
+kernel, updates of a tensor another job reads) before any launch."""
 from __future__ import annotations
 
 import struct
@@ -16,8 +17,11 @@ from aicf_cuda import abi
 OK, INV, NOTIMPL = abi.STATUS_OK, abi.STATUS_INVALID_ARGUMENT, abi.STATUS_NOT_IMPLEMENTED
 F32, I32 = abi.DTYPE_F32, abi.DTYPE_I32
 GGRP = int.from_bytes(b"GGRP", "little")
+GGRA = int.from_bytes(b"GGRA", "little")
+XHST = int.from_bytes(b"XHST", "little")
+GEPI = int.from_bytes(b"GEPI", "little")
 ADAM = int.from_bytes(b"ADAM", "little")
-XENT_HEAD, GRAD_GROUP, ADAMW_MULTI = 25, 26, 27
+GEMM_EPILOGUE, XENT_HEAD, GRAD_GROUP, ADAMW_MULTI = 17, 25, 26, 27
 MB = 1 << 24  # spacing of fake device addresses: every call below is rejected on the host
 
 
@@ -41,14 +45,50 @@ def call(lib, kind, ins, outs, schema=0, payload=b"", kid=None):
     return lib.aicf_dispatch_by_id_v0(kind, kid.encode(), ia, len(ins), oa, len(outs), bp, None)
 
 
-def _fused():
+def _fused(fuse_small=True):
     from aicf_hip import mlp
 
-    return mlp.build_mlp_xent(fuse_small=True)
+    return mlp.build_mlp_xent(fuse_small=fuse_small)
+
+
+def test_reference_step_lowers_to_three_launches():
+    ir, lowered, _ = _fused()
+    assert [(it["op"], it["kernel_id"]) for it in lowered] == [
+        ("gemm_epilogue_bcopy", "gemm_small_bcopy_f32_v0"), ("xent_head", "xent_head_step_f32_v0"),
+        ("grad_group_adamw", "grad_group_adamw_f32_v0")]
+    name = {v.id: v.name for v in ir.values.values()}
+    fwd, head, g = lowered
+    # the forward GEMM writes the copy of 0.W that the input gradient reads
+    assert [name[v] for v in fwd["outputs"]] == ["relu0_out", "0.W.copy"]
+    # the head advances the step counter in place and writes the step's
+    # AdamW bias corrections, which the group reads
+    assert name[head["inputs"][5]] == name[head["outputs"][6]] == "opt.step" and head["attrs"]["step_inc"] == 1
+    assert name[head["outputs"][7]] == "opt.step.adamw_scalars"
+    assert (head["attrs"]["lr"], head["attrs"]["beta1"], head["attrs"]["beta2"]) == (1e-3, 0.9, 0.999)
+    ins, outs = g["inputs"], g["outputs"]
+    jobs = g["attrs"]["jobs"]
+    assert sorted(j[0] for j in jobs) == [0, 0, 0, 1, 1, 2]  # dW1, dx, dW0 | db1, db0 | loss mean; no step job
+    upd = {name[outs[j[3]]]: [name[ins[j[6 + k]]] for k in range(3)] for j in jobs if j[6] >= 0}
+    assert upd == {"d_2.W": ["2.W", "opt.m.2.W", "opt.v.2.W"], "d_2.b": ["2.b", "opt.m.2.b", "opt.v.2.b"],
+                   "d_0.W": ["0.W", "opt.m.0.W", "opt.v.0.W"], "d_0.b": ["0.b", "opt.m.0.b", "opt.v.0.b"]}
+    for j in jobs:  # in place
+        if j[6] >= 0:
+            assert [ins[j[6 + k]] for k in range(3)] == [outs[j[9 + k]] for k in range(3)]
+    dx = [j for j in jobs if name[outs[j[3]]] == "d_x"][0]
+    assert name[ins[dx[2]]] == "0.W.copy"
+    assert name[ins[g["attrs"]["scalars_input"]]] == "opt.step.adamw_scalars"
+    assert "opt.step" not in {name[v] for v in list(ins) + list(outs)}
+    written = {name[v] for it in lowered for v in it["outputs"]}
+    for k in ("loss", "pred", "row_loss", "logits", "dY", "d_relu0_out", "d_lin0_out", "d_x", "opt.step",
+              "d_0.W", "d_0.b", "d_2.W", "d_2.b", "0.W", "0.b", "2.W", "2.b"):
+        assert k in written, k
+    # nothing in the group reads a tensor it updates
+    upd_ids = {ins[j[6 + k]] for j in jobs if j[6] >= 0 for k in range(3)}
+    assert not upd_ids & {ins[j[1]] for j in jobs} and not upd_ids & {ins[j[2]] for j in jobs if j[0] == 0}
 
 
 def test_reference_step_lowers_to_four_launches():
-    ir, lowered, _ = _fused()
+    ir, lowered, _ = _fused("four")
     assert [(it["op"], it["kernel_id"]) for it in lowered] == [
         ("gemm_epilogue", "gemm_bias_relu_f32_naive_v0"), ("xent_head", "xent_head_f32_v0"),
         ("grad_group", "grad_group_f32_v0"), ("adamw_multi", "adamw_multi_f32_v0")]
@@ -64,20 +104,26 @@ def test_reference_step_lowers_to_four_launches():
     assert lowered[1]["inputs"][0] == lowered[1]["inputs"][4] == lowered[0]["outputs"][0]
 
 
-def test_group_jobs_are_independent():
-    ir, lowered, _ = _fused()
+@pytest.mark.parametrize("fuse_small", [True, "four"])
+def test_group_jobs_are_independent(fuse_small):
+    ir, lowered, _ = _fused(fuse_small)
     from aicf_hip.lower import _base
 
     g = lowered[2]
     ins, outs = g["inputs"], g["outputs"]
     jobs = g["attrs"]["jobs"]
     for a, ja in enumerate(jobs):
-        wa = _base(ir, outs[ja[3]])
+        wa = {_base(ir, outs[ja[3]])}
+        if len(ja) == 12 and ja[6] >= 0:
+            wa |= {_base(ir, ins[ja[6 + k]]) for k in range(3)}
         for b, jb in enumerate(jobs):
             if a == b:
                 continue
             reads = {_base(ir, ins[jb[1]])} | ({_base(ir, ins[jb[2]])} if jb[0] == 0 else set())
-            assert wa not in reads and wa != _base(ir, outs[jb[3]]), (ja, jb)
+            writes = {_base(ir, outs[jb[3]])}
+            if len(jb) == 12 and jb[6] >= 0:
+                writes |= {_base(ir, ins[jb[6 + k]]) for k in range(3)}
+            assert not wa & reads and not wa & writes, (ja, jb)
 
 
 def test_unfused_lowering_is_the_reference_one():
@@ -87,10 +133,34 @@ def test_unfused_lowering_is_the_reference_one():
     assert len(lowered) == 17 and lowered[1]["op"] == "copy_saved"
 
 
-def test_warmup_rewrites_reach_the_fused_ops():
+def test_warmup_rewrites_reach_the_three_launch_ops():
     from aicf_hip.executor import pack_attrs, warmup_attrs
 
     _, lowered, _ = _fused()
+    head, g = lowered[1], lowered[2]
+    wh = warmup_attrs("xent_head", head["attrs"])
+    assert (wh["step_inc"], wh["lr"]) == (0, 0.0) and (head["attrs"]["step_inc"], head["attrs"]["lr"]) == (1, 1e-3)
+    assert warmup_attrs("xent_head", {}) == {}  # the plain head has no step part
+    assert warmup_attrs("grad_group_adamw", g["attrs"])["lr"] == 0.0 and g["attrs"]["lr"] == pytest.approx(1e-3)
+    schema, pay = pack_attrs("xent_head", head["attrs"])
+    assert schema == XHST and struct.unpack("<ifff", pay) == (1, pytest.approx(1e-3), pytest.approx(0.9),
+                                                              pytest.approx(0.999))
+    assert struct.unpack("<i", pack_attrs("xent_head", {"step_inc": 0})[1]) == (0,)
+    assert pack_attrs("xent_head", {})[0] == 0
+    schema, pay = pack_attrs("grad_group_adamw", g["attrs"])
+    n = len(g["attrs"]["jobs"])
+    assert schema == GGRA and len(pay) == 28 + 48 * n
+    cnt, lr, b1, b2, eps, wd, si = struct.unpack_from("<ifffffi", pay)
+    assert (cnt, si) == (n, g["attrs"]["scalars_input"]) and (b1, wd) == (pytest.approx(0.9), 0.0)
+    assert [list(struct.unpack_from("<" + "i" * 12, pay, 28 + 48 * k)) for k in range(n)] == g["attrs"]["jobs"]
+    schema, pay = pack_attrs("gemm_epilogue_bcopy", lowered[0]["attrs"])
+    assert schema == GEPI and struct.unpack("<iii", pay) == (0, 1, 0)
+
+
+def test_warmup_rewrites_reach_the_fused_ops():
+    from aicf_hip.executor import pack_attrs, warmup_attrs
+
+    _, lowered, _ = _fused("four")
     g, a = lowered[2], lowered[3]
     wg = warmup_attrs("grad_group", g["attrs"])
     assert [j[4] for j in wg["jobs"] if j[0] == 3] == [0]
@@ -104,11 +174,12 @@ def test_warmup_rewrites_reach_the_fused_ops():
     assert schema == ADAM and struct.unpack("<fffff", pay)[0] == pytest.approx(1e-3)
 
 
-def test_fused_lowering_round_trips_through_the_text_dump():
+@pytest.mark.parametrize("fuse_small", [True, "four"])
+def test_fused_lowering_round_trips_through_the_text_dump(fuse_small):
     from aicf_hip.interchange import lowered_from_text
     from aicf_hip.lower import lowered_to_text
 
-    ir, lowered, _ = _fused()
+    ir, lowered, _ = _fused(fuse_small)
     text = lowered_to_text(lowered, ir.name)
     assert lowered_from_text(text) == lowered
 
@@ -121,6 +192,9 @@ def test_head_fusion_needs_the_pattern():
     _, lowered, _ = mlp.build_mlp_xent(B=64, din=784, dh=256, dout=40, fuse_small=True)
     ops = [it["op"] for it in lowered]
     assert "xent_head" not in ops and "softmax_xent" in ops and "adamw_multi" in ops
+    # with no head to take the step counter the updates stay in adamw_multi
+    # (a step_inc launch of their own would cost what the fusion saves)
+    assert "grad_group_adamw" not in ops and "gemm_epilogue_bcopy" not in ops
 
 
 def _group_payload(jobs):
@@ -219,10 +293,10 @@ def _view_params(ir, names, elem_offset):
         off += int(np.prod(v.shape))
 
 
-def _relower(ir):
+def _relower(ir, fuse_small=True):
     from aicf_hip.lower import compile_lowered
 
-    return compile_lowered(ir, fuse_small=True)
+    return compile_lowered(ir, fuse_small=fuse_small)
 
 
 def test_small_step_keeps_unaligned_views_off_the_vector_kernels():
@@ -233,8 +307,11 @@ def test_small_step_keeps_unaligned_views_off_the_vector_kernels():
 
     ir, low, _ = mlp.build_mlp_xent(fuse_small=True)
     _view_params(ir, ["2.W"], 4)  # 16 bytes: still aligned
-    ops = [it["op"] for it in _relower(ir)]
+    ops = [it["op"] for it in _relower(ir, "four")]
     assert "xent_head" in ops and ops.count("adamw_multi") == 1 and "adamw_step" not in ops
+    # the group's updates take any offset
+    ops = [it["op"] for it in _relower(ir)]
+    assert ops == ["gemm_epilogue_bcopy", "xent_head", "grad_group_adamw"]
     ir, low, _ = mlp.build_mlp_xent(fuse_small=True)
     _view_params(ir, ["2.W"], 1)
     ops = [it["op"] for it in _relower(ir)]
@@ -299,3 +376,135 @@ def test_xent_head_refuses_partially_overlapping_outputs(lib):
     o = outs()
     o[3] = d((B,), ptr=MB + 4096)  # row loss inside H
     assert call(lib, XENT_HEAD, ins, o, kid=kid) == INV
+
+
+def _ggra_payload(jobs, scalars_input, lr=1e-3, b1=0.9, b2=0.999, eps=1e-8, wd=0.0):
+    head = struct.pack("<ifffffi", len(jobs), lr, b1, b2, eps, wd, scalars_input)
+    return head + b"".join(struct.pack("<" + "i" * 12, *j) for j in jobs)
+
+
+def _ggra_case():
+    """A GEMM dW = dY^T . X (16 x 32) with AdamW on W, a column sum db of dY
+    with AdamW on b, and a dX = dY . Wc job reading a copy Wc of W."""
+    dY, X = d((64, 16), ptr=1 * MB), d((64, 32), ptr=2 * MB)
+    W, Wm, Wv = d((16, 32), ptr=3 * MB), d((16, 32), ptr=4 * MB), d((16, 32), ptr=5 * MB)
+    b, bm, bv = d((16,), ptr=6 * MB), d((16,), ptr=7 * MB), d((16,), ptr=8 * MB)
+    Wc, scal = d((16, 32), ptr=9 * MB), d((2,), ptr=10 * MB)
+    dW, db, dX = d((16, 32), ptr=11 * MB), d((16,), ptr=12 * MB), d((64, 32), ptr=13 * MB)
+    ins = [dY, X, W, Wm, Wv, b, bm, bv, Wc, scal]
+    outs = [dW, W, Wm, Wv, db, b, bm, bv, dX]
+    jobs = [[0, 0, 1, 0, 1, 0, 2, 3, 4, 1, 2, 3],
+            [1, 0, 0, 4, 0, 0, 5, 6, 7, 5, 6, 7],
+            [0, 0, 8, 8, 0, 0, -1, -1, -1, -1, -1, -1]]
+    return ins, outs, jobs, 9
+
+
+def test_grad_group_adamw_refuses_what_would_race(lib, monkeypatch):
+    kid = "grad_group_adamw_f32_v0"
+    ins, outs, jobs, si = _ggra_case()
+
+    def ok(ins=ins, outs=outs, jobs=jobs, si=si, schema=GGRA, **hp):
+        return call(lib, GRAD_GROUP, ins, outs, schema, _ggra_payload(jobs, si, **hp), kid)
+
+    # the well-formed case passes every host check: it only fails at the
+    # launch, which this container cannot do (no GPU)
+    assert ok() != INV
+    # the copy job reads W itself while W is updated: refused
+    j = [list(x) for x in jobs]
+    j[2][2] = 2
+    assert ok(jobs=j) == INV
+    # AdamW on the loss-mean type, or on a step job in the group
+    j = [list(x) for x in jobs]
+    j[1][0] = 2
+    assert ok(jobs=j) == INV
+    j = [list(x) for x in jobs] + [[3, 9, 0, 9, 1, 0] + [-1] * 6]
+    assert ok(ins=ins, outs=outs + [ins[9]], jobs=j) == INV
+    # not in place: the P output is another buffer
+    o = list(outs)
+    o[1] = d((16, 32), ptr=20 * MB)
+    assert ok(outs=o) == INV
+    # M of the wrong size, an update overlapping another job's output
+    i2 = list(ins)
+    i2[3] = d((16, 31), ptr=4 * MB)
+    o2 = list(outs)
+    o2[2] = i2[3]
+    assert ok(ins=i2, outs=o2) == INV
+    i3, o3 = list(ins), list(outs)
+    i3[6] = o3[6] = d((16,), ptr=13 * MB + 64)  # b's M inside dX
+    assert ok(ins=i3, outs=o3) == INV
+    # the bias corrections overlapping an updated tensor, of the wrong type or
+    # size; a NaN hyperparameter, the GGRP schema, an index out of range
+    i4 = list(ins)
+    i4[9] = d((2,), ptr=6 * MB + 4)
+    assert ok(ins=i4) == INV
+    for bad in (d((2,), I32, ptr=10 * MB), d((3,), ptr=10 * MB)):
+        i4[9] = bad
+        assert ok(ins=i4) == INV
+    assert ok(lr=float("nan")) == INV
+    assert ok(schema=GGRP) == INV
+    j = [list(x) for x in jobs]
+    j[0][8] = 10
+    assert ok(jobs=j) == INV
+    # a GEMM output that is not row-major contiguous
+    o5 = list(outs)
+    o5[0] = d((16, 32), ptr=11 * MB, stride=(64, 1))
+    assert ok(outs=o5) == INV
+
+
+def test_xent_head_step_refuses_bad_counters(lib):
+    kid = "xent_head_step_f32_v0"
+    B, K, C = 64, 256, 10
+    step = d((), I32, ptr=20 * MB)
+    ins = [d((B, K), ptr=MB), d((C, K), ptr=2 * MB), d((C,), ptr=3 * MB), d((B,), I32, ptr=4 * MB),
+           d((B, K), ptr=5 * MB), step]
+    outs = [d((B, C), ptr=6 * MB), d((B, C), ptr=7 * MB), d((B,), I32, ptr=8 * MB), d((B,), ptr=9 * MB),
+            d((B, K), ptr=10 * MB), d((B, K), ptr=11 * MB), step]
+    inc1 = struct.pack("<i", 1)
+    assert call(lib, XENT_HEAD, ins, outs, XHST, inc1, kid) != INV
+    assert call(lib, XENT_HEAD, ins, outs, XHST, struct.pack("<i", 2), kid) == INV
+    assert call(lib, XENT_HEAD, ins, outs, GGRP, inc1, kid) == INV
+    assert call(lib, XENT_HEAD, ins[:5], outs[:6], XHST, inc1, kid) == INV
+    o = list(outs)
+    o[6] = d((), I32, ptr=21 * MB)  # not in place
+    assert call(lib, XENT_HEAD, ins, o, XHST, inc1, kid) == INV
+    # with the hyperparameters an 8th output takes the bias corrections
+    hp = inc1 + struct.pack("<fff", 1e-3, 0.9, 0.999)
+    scal = d((2,), ptr=22 * MB)
+    assert call(lib, XENT_HEAD, ins, outs + [scal], XHST, hp, kid) != INV
+    assert call(lib, XENT_HEAD, ins, outs, XHST, hp, kid) == INV
+    assert call(lib, XENT_HEAD, ins, outs + [scal], XHST, inc1, kid) == INV
+    assert call(lib, XENT_HEAD, ins, outs + [d((3,), ptr=22 * MB)], XHST, hp, kid) == INV
+    assert call(lib, XENT_HEAD, ins, outs + [d((2,), ptr=9 * MB)], XHST, hp, kid) == INV  # over the row loss
+    nan = inc1 + struct.pack("<fff", float("nan"), 0.9, 0.999)
+    assert call(lib, XENT_HEAD, ins, outs + [scal], XHST, nan, kid) == INV
+    i2, o2 = list(ins), list(outs)
+    i2[5] = o2[6] = d((), I32, ptr=9 * MB + 8)  # inside the row loss
+    assert call(lib, XENT_HEAD, i2, o2, XHST, inc1, kid) == INV
+    i3, o3 = list(ins), list(outs)
+    i3[5] = o3[6] = d((2,), I32, ptr=20 * MB)  # not a scalar
+    assert call(lib, XENT_HEAD, i3, o3, XHST, inc1, kid) == INV
+
+
+def test_gemm_bcopy_refuses_what_it_cannot_copy(lib):
+    kid = "gemm_small_bcopy_f32_v0"
+    M, N, K = 64, 256, 784
+    A, W, b = d((M, K), ptr=MB), d((N, K), ptr=4 * MB), d((N,), ptr=8 * MB)
+    C, Wc = d((M, N), ptr=9 * MB), d((N, K), ptr=12 * MB)
+
+    def run(ins, outs, ta=0, tb=1, kind=0, schema=GEPI):
+        return call(lib, GEMM_EPILOGUE, ins, outs, schema, struct.pack("<iii", ta, tb, kind), kid)
+
+    assert run([A, W, b], [C, Wc]) != INV
+    assert run([A, W, b], [C, Wc], kind=2) != INV  # ReLU without bias
+    assert run([A, d((K, N), ptr=4 * MB), b], [C, d((K, N), ptr=12 * MB)], tb=0) == INV  # B not K-contiguous
+    assert run([A, W, b], [C, Wc], kind=3) == INV  # GELU is not the small path's
+    assert run([A, W, b], [C, d((N, K - 4), ptr=12 * MB)]) == INV  # copy of another shape
+    assert run([A, W, b], [C, d((N, K), ptr=MB + 64)]) == INV  # copy over A
+    assert run([A, W, b], [C, d((N, K), ptr=12 * MB + 4)]) == INV  # unaligned copy
+    assert run([d((M, 786), ptr=MB), d((N, 786), ptr=4 * MB), b], [C, d((N, 786), ptr=12 * MB)]) == INV  # K % 4
+    assert run([A, W, b], [C]) == INV  # no copy output
+    big = d((8192, K), ptr=16 * MB)
+    assert run([big, W, b], [d((8192, N), ptr=40 * MB), Wc]) == INV  # not a small problem
+    # the general epilogue variants refuse the two-output call
+    assert call(lib, GEMM_EPILOGUE, [A, W, b], [C, Wc], GEPI, struct.pack("<iii", 0, 1, 0),
+                "gemm_bias_relu_f32_naive_v0") == INV
