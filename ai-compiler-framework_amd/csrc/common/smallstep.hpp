@@ -23,9 +23,9 @@ struct SmallGemm {
   int64_t M, N, K;
   int relu;           // relu(acc + bias)
   // nullptr, or a copy of B written at B's element offsets (B[k * b_k +
-  // n * b_n] -> bcopy[k * b_k + n * b_n]) by the tiles of the first row of
-  // tiles, which read all of B; needs K-contiguous B (b_k == 1, 16-byte
-  // aligned rows)
+  // n * b_n] -> bcopy[k * b_k + n * b_n]) from the loads of B the tiles make
+  // anyway, shared out over the rows of tiles; needs K-contiguous B (b_k ==
+  // 1, 16-byte aligned rows)
   float* bcopy;
 };
 

@@ -60,17 +60,31 @@ struct SgJob {
   int splits;      // waves per tile (K split): 1, 2, 4 or 8
   int tpb;         // tiles per workgroup: waves / splits
   int avec, bvec;  // 16-byte loads along K (K-contiguous, aligned operand)
+  int a_bytes, b_bytes;  // byte ranges of A and B read through buffer loads (< 2^31)
 };
 
-__device__ __forceinline__ f32x4 sg_load(const float* row, int64_t sk, int64_t k, int64_t K, bool ok,
-                                         bool vec) {
-  f32x4 v = {0.f, 0.f, 0.f, 0.f};
-  if (!ok || k >= K) return v;
-  if (vec) return *reinterpret_cast<const f32x4*>(row + k);  // K % 4 == 0: all four in range
+// Elements k .. k + 3 of row `row` of an operand (zero past K or for a lane
+// without a row), as buffer loads: a lane with nothing to read passes an
+// offset past the buffer's range and the load returns zeros.  No branch and
+// no select after the load: the compiler would wait for each load before the
+// next one (a divergent branch around the loads, or a select of their
+// results), one round trip per load instead of one per batch.
+constexpr int kOutOfRange = (int)0x80000000u;  // past every buffer's range (< 2^31 bytes)
+template <bool VEC>
+__device__ __forceinline__ f32x4 sg_load(__amdgpu_buffer_rsrc_t rs, int64_t row, int64_t sm, int64_t sk, int64_t k,
+                                         int64_t K, bool ok) {
+  if constexpr (VEC) {  // K % 4 == 0: the four are in range together
+    const int off = ok && k < K ? (int)((row * sm + k) * 4) : kOutOfRange;
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+  } else {
+    f32x4 v;
 #pragma unroll
-  for (int c = 0; c < 4; ++c)
-    if (k + c < K) v[c] = row[(k + c) * sk];
-  return v;
+    for (int c = 0; c < 4; ++c) {
+      const int off = ok && k + c < K ? (int)((row * sm + (k + c) * sk) * 4) : kOutOfRange;
+      v[c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0));
+    }
+    return v;
+  }
 }
 
 // One 16 x 16 tile over the K blocks split, split + splits, ...  Lane
@@ -78,31 +92,38 @@ __device__ __forceinline__ f32x4 sg_load(const float* row, int64_t sk, int64_t k
 // it holds k = 16 kb + 4 q + c (c = 0..3) and feeds component c to the c-th
 // MFMA of the block, so k slot q of that MFMA carries the same k for A and
 // B.  Accumulator element i is C[m0 + 4 q + i][n0 + r].
+// The K-block loop and m0, n0, split are wave-uniform, so only the row and
+// K-range tests of sg_load differ between lanes.
+template <bool AV, bool BV>
 __device__ __forceinline__ f32x4 sg_tile(const SgJob& j, int64_t m0, int64_t n0, int split, int lane) {
   const int r = lane & 15, q = lane >> 4;
   const int64_t m = m0 + r, n = n0 + r;
   const bool mok = m < j.g.M, nok = n < j.g.N;
-  const float* ar = j.g.A + (mok ? m : 0) * j.g.a_m;
-  const float* br = j.g.B + (nok ? n : 0) * j.g.b_n;
-  // the first row of tiles reads all of B: it also writes B's copy
-  const bool snap = j.g.bcopy != nullptr && m0 == 0 && nok;
+  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void*)j.g.A, 0, j.a_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc((void*)j.g.B, 0, j.b_bytes, 0x00020000);
+  // every row of tiles reads all of B: the copy of B is shared out, the
+  // wave of row of tiles mt writing the u-th K block it reads when u % MT
+  // == mt (MT rows of tiles)
+  const bool snap = j.g.bcopy != nullptr && nok;
   float* bc = snap ? j.g.bcopy + n * j.g.b_n : nullptr;
+  const int MT = (int)((j.g.M + 15) / 16), mt = (int)(m0 / 16);
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int kb0 = split; kb0 < j.kb; kb0 += j.splits * kNB) {
+  for (int kb0 = split, ub = 0; kb0 < j.kb; kb0 += j.splits * kNB, ub += kNB) {
     f32x4 a[kNB], b[kNB];
 #pragma unroll
     for (int u = 0; u < kNB; ++u) {
       const int kb = kb0 + u * j.splits;
+      if (kb >= j.kb) break;  // uniform across the wave
       const int64_t k = (int64_t)kb * 16 + 4 * q;
-      a[u] = sg_load(ar, j.g.a_k, k, j.g.K, mok && kb < j.kb, j.avec);
-      b[u] = sg_load(br, j.g.b_k, k, j.g.K, nok && kb < j.kb, j.bvec);
+      a[u] = sg_load<AV>(ra, m, j.g.a_m, j.g.a_k, k, j.g.K, mok);
+      b[u] = sg_load<BV>(rb, n, j.g.b_n, j.g.b_k, k, j.g.K, nok);
     }
 #pragma unroll
     for (int u = 0; u < kNB; ++u) {
       if (kb0 + u * j.splits >= j.kb) break;  // uniform across the wave
 #pragma unroll
       for (int c = 0; c < 4; ++c) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u][c], b[u][c], acc, 0, 0, 0);
-      if (snap) {  // K % 4 == 0 (16-byte loads of B): the four are in range together
+      if (snap && (ub + u) % MT == mt) {  // K % 4 == 0 (16-byte loads of B): the four are in range together
         const int64_t k = (int64_t)(kb0 + u * j.splits) * 16 + 4 * q;
         if (k < j.g.K) *reinterpret_cast<f32x4*>(bc + k) = b[u];
       }
@@ -142,7 +163,8 @@ __device__ __forceinline__ void adamw_store(const StoreAdamW& ad, int64_t i, int
   ad.V[i] = r.v[x];
 }
 
-// The elements sg_store writes for this lane: C[m0 + 4 q + i][n0 + r].
+// The elements sg_store writes for this lane: C[m0 + 4 q + i][n0 + r]
+// (branch-free, as sg_load; element 0 stands in for those outside C).
 __device__ __forceinline__ void sg_adamw_prefetch(const SmallGemm& g, int64_t m0, int64_t n0, int lane,
                                                   const StoreAdamW& ad, AdamWLane& r) {
   const int rr = lane & 15, q = lane >> 4;
@@ -151,20 +173,17 @@ __device__ __forceinline__ void sg_adamw_prefetch(const SmallGemm& g, int64_t m0
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int64_t m = m0 + 4 * q + i;
-    if (n < g.N && m < g.M)
-      adamw_load(ad, m * g.c_m + n, i, r);
-    else
-      r.p[i] = r.m[i] = r.v[i] = 0.0f;
+    adamw_load(ad, (n < g.N && m < g.M) ? m * g.c_m + n : 0, i, r);
   }
 }
 
+// bv: the bias of column n0 + r, loaded before the tile's K loop.
 template <bool ADAM>
-__device__ __forceinline__ void sg_store(const SmallGemm& g, int64_t m0, int64_t n0, int lane, f32x4 acc,
+__device__ __forceinline__ void sg_store(const SmallGemm& g, int64_t m0, int64_t n0, int lane, f32x4 acc, float bv,
                                          const StoreAdamW& ad, AdamWLane& ar) {
   const int r = lane & 15, q = lane >> 4;
   const int64_t n = n0 + r;
   if (n >= g.N) return;
-  const float bv = g.bias ? g.bias[n * g.bias_s] : 0.0f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int64_t m = m0 + 4 * q + i;
@@ -183,7 +202,7 @@ __device__ __forceinline__ void sg_store(const SmallGemm& g, int64_t m0, int64_t
 // output is row-major contiguous, so its element index is the parameter's).
 template <bool ADAM>
 __device__ __forceinline__ void sg_block(const SgJob& j, int blk, f32x4* red, const StoreAdamW& ad) {
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int tile = blk * j.tpb + w / j.splits;
   const int split = w % j.splits;
   const bool live = tile < j.tiles;
@@ -192,8 +211,18 @@ __device__ __forceinline__ void sg_block(const SgJob& j, int blk, f32x4* red, co
   AdamWLane ar;
   const bool upd = ADAM && live && split == 0;
   if (upd) sg_adamw_prefetch(j.g, m0, n0, lane, ad, ar);
+  float bv = 0.0f;
+  if (j.g.bias && live && split == 0) {  // wave-uniform: no divergent branch around the load
+    const int64_t n = n0 + (lane & 15);
+    bv = j.g.bias[(n < j.g.N ? n : 0) * j.g.bias_s];
+  }
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  if (live) acc = sg_tile(j, m0, n0, split, lane);
+  if (live) {
+    if (j.avec)
+      acc = j.bvec ? sg_tile<true, true>(j, m0, n0, split, lane) : sg_tile<true, false>(j, m0, n0, split, lane);
+    else
+      acc = j.bvec ? sg_tile<false, true>(j, m0, n0, split, lane) : sg_tile<false, false>(j, m0, n0, split, lane);
+  }
   if (j.splits > 1) {
     red[w * 64 + lane] = acc;
     __syncthreads();
@@ -202,7 +231,7 @@ __device__ __forceinline__ void sg_block(const SgJob& j, int blk, f32x4* red, co
   } else if (!live) {
     return;
   }
-  sg_store<ADAM>(j.g, m0, n0, lane, acc, ad, ar);
+  sg_store<ADAM>(j.g, m0, n0, lane, acc, bv, ad, ar);
 }
 
 template <int NWAVE>
@@ -214,6 +243,12 @@ __global__ __launch_bounds__(64 * NWAVE) void gemm_small_kernel(SgJob j) {
 // nwave 4, or 8 for the standalone kernel when K is long enough for 8 splits
 // (32 or more K blocks): each wave then has at most 8 blocks, one batch of
 // loads in flight.
+// Bytes from an operand's first element to the end of its last one (rows x
+// K with row stride sr and K stride sk, in floats).
+int64_t sg_range_bytes(int64_t rows, int64_t sr, int64_t K, int64_t sk) {
+  return ((rows - 1) * sr + (K - 1) * sk + 1) * 4;
+}
+
 SgJob sg_plan(const SmallGemm& g, int nwave = 4) {
   SgJob j{};
   j.g = g;
@@ -224,6 +259,8 @@ SgJob sg_plan(const SmallGemm& g, int nwave = 4) {
   j.tpb = nwave / j.splits;
   j.avec = g.a_k == 1 && g.K % 4 == 0 && (g.M == 1 || g.a_m % 4 == 0) && aligned(g.A, 16);
   j.bvec = g.b_k == 1 && g.K % 4 == 0 && (g.N == 1 || g.b_n % 4 == 0) && aligned(g.B, 16);
+  j.a_bytes = (int)sg_range_bytes(g.M, g.a_m, g.K, g.a_k);
+  j.b_bytes = (int)sg_range_bytes(g.N, g.b_n, g.K, g.b_k);
   return j;
 }
 int sg_blocks(const SgJob& j) { return (j.tiles + j.tpb - 1) / j.tpb; }
@@ -256,52 +293,88 @@ struct XentHeadArgs {
   AdamWArgs aw;
 };
 
-// Sums over the wave of x[c] for every class c < CM, in log2(CM) exchange
-// steps that halve the classes a lane carries (it keeps one half and adds
-// its partner's copy of that half), then plain exchanges between the lanes
-// left with the same class.  Lane l returns the sum of class l >> (6 -
-// log2 CM).  Every class is summed in one fixed order.
-template <int CM>
-__device__ __forceinline__ float class_sums(float (&x)[CM], int lane) {
-#pragma unroll
-  for (int n = CM, mask = 32; n > 1; n >>= 1, mask >>= 1) {
-    const bool up = (lane & mask) != 0;
-#pragma unroll
-    for (int i = 0; i < n / 2; ++i) {
-      const float send = up ? x[i] : x[i + n / 2];
-      const float keep = up ? x[i + n / 2] : x[i];
-      x[i] = keep + __shfl_xor(send, mask, 64);
-    }
+// The value v of the exchange partner of this lane at level BIT: the lane
+// with bit BIT flipped (BIT 5, 4: v_permlane32_swap / v_permlane16_swap),
+// the lane mirrored in its row of 16 (BIT 3, lane ^ 15) or of 8 (BIT 2,
+// lane ^ 7), or the lane with bit 1 or 0 flipped (quad_perm).  Every partner
+// differs from the lane in bit BIT and agrees with it in the bits above, and
+// all of them are VALU lane moves (no LDS round trip).
+template <int BIT>
+__device__ __forceinline__ float xpartner(float v, int lane) {
+  const unsigned u = __float_as_uint(v);
+  if constexpr (BIT == 5) {
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return __uint_as_float(lane < 32 ? r[1] : r[0]);
+  } else if constexpr (BIT == 4) {
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return __uint_as_float((lane & 16) ? r[0] : r[1]);
+  } else {
+    constexpr int ctrl = BIT == 3 ? 0x140 : BIT == 2 ? 0x141 : BIT == 1 ? 0x4E : 0xB1;
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, (int)u, ctrl, 0xF, 0xF, false));
   }
-  float v = x[0];
+}
+
+// Sum over the wave, the same bits in every lane (each level adds a lane's
+// value and its partner's, in either order the same IEEE sum).
+template <int BIT = 5>
+__device__ __forceinline__ float wave_sum_perm(float v, int lane) {
+  if constexpr (BIT < 0) {
+    return v;
+  } else {
+    return wave_sum_perm<BIT - 1>(v + xpartner<BIT>(v, lane), lane);
+  }
+}
+
+// Sums over the wave of x[c] for every class c < N (16 or 32), in log2(N)
+// levels that halve the classes a lane carries (it keeps the half its bit
+// BIT selects and adds its partner's copy of that half), then the levels
+// left add the partners that carry the same class.  Lane l returns the sum
+// of class l >> (6 - log2 N), every class summed in one fixed order.
+template <int N, int BIT = 5, int CM>
+__device__ __forceinline__ float class_sums(float (&x)[CM], int lane) {
+  if constexpr (N > 1) {
+    const bool up = ((lane >> BIT) & 1) != 0;
 #pragma unroll
-  for (int mask = 32 / CM; mask > 0; mask >>= 1) v += __shfl_xor(v, mask, 64);
-  return v;
+    for (int i = 0; i < N / 2; ++i) {
+      const float send = up ? x[i] : x[i + N / 2];
+      const float keep = up ? x[i + N / 2] : x[i];
+      x[i] = keep + xpartner<BIT>(send, lane);
+    }
+    return class_sums<N / 2, BIT - 1>(x, lane);
+  } else {
+    return wave_sum_perm<BIT>(x[0], lane);
+  }
 }
 
 __device__ __forceinline__ float readlane_f(float v, int l) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
 
+// The step counter's workgroup: advance it and write the advanced step's
+// bias corrections (two fp64 powers).
+__device__ __forceinline__ void head_counter(int32_t* step, int inc, float* scal, AdamWArgs aw) {
+  const int t = step[0] + inc;
+  step[0] = t;
+  if (scal) {
+    const AdamWScalars sc = adamw_scalars_at(t, aw);
+    scal[0] = sc.step;
+    scal[1] = sc.ibc2;
+  }
+}
+
 // Q: 16-byte vectors per lane along K (K <= 256 Q); CM: classes (C <= CM,
 // 16 or 32).  One wave (one row) per workgroup, so that the rows spread over
 // as many CUs as there are rows.  With Q x CM <= 16 the lane's slice of W is
 // loaded once, together with the row, and serves both the logits and dH.
+// After class_sums, lane l carries class l >> SH: the softmax terms are
+// computed once per class there, and every lane reads the ones it needs.
 template <int Q, int CM>
 __global__ __launch_bounds__(64) void xent_head_kernel(XentHeadArgs a) {
   static_assert(CM == 16 || CM == 32, "class_sums maps 64 lanes onto 16 or 32 classes");
-  constexpr int SH = CM == 16 ? 2 : 1;  // lane l carries class l >> SH after class_sums
+  constexpr int SH = CM == 16 ? 2 : 1;
   const int lane = threadIdx.x;
   if (blockIdx.x == a.B) {  // the step counter's workgroup (launched only with a counter)
-    if (lane == 0) {
-      const int t = a.step[0] + a.inc;
-      a.step[0] = t;
-      if (a.scal) {
-        const AdamWScalars sc = adamw_scalars_at(t, a.aw);
-        a.scal[0] = sc.step;
-        a.scal[1] = sc.ibc2;
-      }
-    }
+    if (lane == 0) head_counter(a.step, a.inc, a.scal, a.aw);
     return;
   }
   const int64_t row = blockIdx.x;
@@ -336,12 +409,12 @@ __global__ __launch_bounds__(64) void xent_head_kernel(XentHeadArgs a) {
     sv[q] = idx < K4 ? sr[idx] : f32x4{0.f, 0.f, 0.f, 0.f};
   }
   const int mycls = lane >> SH;
-  const float mybias = mycls < a.C ? a.bias[mycls] : 0.0f;
+  const bool mine = mycls < a.C;
+  const float mybias = mine ? a.bias[mycls] : 0.0f;
   const int lab = a.labels[row];
+  const bool valid = lab >= 0 && lab < a.C;
 
-  // logits: each lane's partial dot products, the class sums, then every
-  // lane reads all logits from the lanes that hold them (the same bits
-  // everywhere)
+  // logits: each lane's partial dot products, then the class sums
   float x[CM];
 #pragma unroll
   for (int c = 0; c < CM; ++c) {
@@ -361,50 +434,40 @@ __global__ __launch_bounds__(64) void xent_head_kernel(XentHeadArgs a) {
     }
     x[c] = p;
   }
-  const float zmine = class_sums<CM>(x, lane) + mybias;
-  float z[CM];
-#pragma unroll
-  for (int c = 0; c < CM; ++c) z[c] = readlane_f(zmine, c << SH);
+  const float z = class_sums<CM>(x, lane) + mybias;  // logit of class mycls
 
-  // softmax cross-entropy of the row (first index of the maximum)
-  float M = z[0];
+  // softmax cross-entropy of the row: the maximum and its first index over
+  // the classes in order, the exponentials per class, their sum over the wave
+  float M = readlane_f(z, 0);
   int am = 0;
 #pragma unroll
-  for (int c = 1; c < CM; ++c)
-    if (c < a.C && z[c] > M) {
-      M = z[c];
-      am = c;
+  for (int c = 1; c < CM; ++c) {
+    if (c < a.C) {
+      const float zc = readlane_f(z, c << SH);
+      if (zc > M) {
+        M = zc;
+        am = c;
+      }
     }
-  float e[CM];
-  float S = 0.0f;
-#pragma unroll
-  for (int c = 0; c < CM; ++c) {
-    e[c] = c < a.C ? __expf(z[c] - M) : 0.0f;
-    S += e[c];
   }
+  const float e = mine ? __expf(z - M) : 0.0f;
+  const float S = wave_sum_perm((lane & ((1 << SH) - 1)) == 0 ? e : 0.0f, lane);
   const float invS = 1.0f / S;
-  float zl = 0.0f, zv = 0.0f, dv = 0.0f;
-  float d[CM];
-#pragma unroll
-  for (int c = 0; c < CM; ++c) {
-    d[c] = (e[c] * invS - (c == lab ? 1.0f : 0.0f)) * a.inv_batch;
-    if (c == lab) zl = z[c];
-    if (c == lane) {
-      zv = z[c];
-      dv = d[c];
-    }
-  }
-  if (lane < a.C) {
-    a.logits[row * a.C + lane] = zv;
-    a.dlogits[row * a.C + lane] = dv;
+  const float dz = (e * invS - (mycls == lab ? 1.0f : 0.0f)) * a.inv_batch;
+  if (mine && (lane & ((1 << SH) - 1)) == 0) {
+    a.logits[row * a.C + mycls] = z;
+    a.dlogits[row * a.C + mycls] = dz;
   }
   if (lane == 0) {
     a.argmax[row] = am;
-    const bool valid = lab >= 0 && lab < a.C;
+    const float zl = readlane_f(z, (valid ? lab : 0) << SH);
     a.row_loss[row] = valid ? ((M - zl) + logf(S)) : __builtin_nanf("");  // as softmax_xent
   }
 
   // dH = dlogits . W and the ReLU backward against the saved output
+  float d[CM];
+#pragma unroll
+  for (int c = 0; c < CM; ++c) d[c] = c < a.C ? readlane_f(dz, c << SH) : 0.0f;
   f32x4* dhr = reinterpret_cast<f32x4*>(a.dH + row * a.K);
   f32x4* dxr = reinterpret_cast<f32x4*>(a.dX + row * a.K);
 #pragma unroll
@@ -1036,6 +1099,10 @@ bool small_gemm_ok(const SmallGemm& g) {
   if (!g.A || !g.B || !g.C || g.M < 1 || g.N < 1 || g.K < 1) return false;
   if (g.M > INT32_MAX / 2 || g.N > INT32_MAX / 2 || g.K > INT32_MAX / 2) return false;
   if (g.a_m < 0 || g.a_k < 0 || g.b_k < 0 || g.b_n < 0 || g.c_m < g.N) return false;
+  // the operands are read through buffer loads with 32-bit byte offsets
+  if (g.a_m > INT32_MAX || g.a_k > INT32_MAX || g.b_k > INT32_MAX || g.b_n > INT32_MAX) return false;
+  if (sg_range_bytes(g.M, g.a_m, g.K, g.a_k) > INT32_MAX || sg_range_bytes(g.N, g.b_n, g.K, g.b_k) > INT32_MAX)
+    return false;
   const int64_t tiles = ((g.M + 15) / 16) * ((g.N + 15) / 16);
   return tiles <= INT32_MAX / 4;
 }
