@@ -240,15 +240,15 @@ __global__ __launch_bounds__(64 * NWAVE) void gemm_small_kernel(SgJob j) {
   sg_block<false>(j, blockIdx.x, red, StoreAdamW{});
 }
 
-// nwave 4, or 8 for the standalone kernel when K is long enough for 8 splits
-// (32 or more K blocks): each wave then has at most 8 blocks, one batch of
-// loads in flight.
 // Bytes from an operand's first element to the end of its last one (rows x
 // K with row stride sr and K stride sk, in floats).
 int64_t sg_range_bytes(int64_t rows, int64_t sr, int64_t K, int64_t sk) {
   return ((rows - 1) * sr + (K - 1) * sk + 1) * 4;
 }
 
+// nwave 4, or 8 for the standalone kernel when K is long enough for 8 splits
+// (32 or more K blocks): each wave then has at most 8 blocks, one batch of
+// loads in flight.
 SgJob sg_plan(const SmallGemm& g, int nwave = 4) {
   SgJob j{};
   j.g = g;
