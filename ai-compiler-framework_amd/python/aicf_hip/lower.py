@@ -869,7 +869,7 @@ def _job_of(ir: IRGraph, it: Dict[str, Any]) -> Optional[tuple]:
         ta, tb = bool(attrs.get("transA", False)), bool(attrs.get("transB", False))
         M = sa[1] if ta else sa[0]
         N = sb[0] if tb else sb[1]
-        if ((M + 63) // 64) * ((N + 63) // 64) >= SMALL_GEMM_MAX_TILES64:
+        if ((M + 63) // 64) * ((N + 63) // 64) >= SMALL_GEMM_MAX_TILES64 or not _small_gemm_ranges_ok(ir, ins):
             return None
         return (GJ_GEMM, ins, outs, int(ta), int(tb))
     if k == "reduce_sum" and len(ins) == 1 and len(outs) == 1 and int(attrs.get("axis", 0)) == 0 \
@@ -880,6 +880,13 @@ def _job_of(ir: IRGraph, it: Dict[str, Any]) -> Optional[tuple]:
     if k == "step_inc" and len(ins) == 1 and len(outs) == 1 and ins == outs:
         return (GJ_STEP, ins, outs, 1, 0)
     return None
+
+
+def _small_gemm_ranges_ok(ir: IRGraph, operands) -> bool:
+    """The small GEMM reads its operands through buffer loads with 32-bit
+    byte offsets: each operand (contiguous, fp32) spans fewer than 2^31
+    bytes."""
+    return all(4 * _numel(ir, int(v)) < 2 ** 31 for v in operands)
 
 
 def _group_item(jobs: List[tuple]) -> Dict[str, Any]:
@@ -996,7 +1003,8 @@ def _bcopy_source(ir: IRGraph, lowered: Lowered, gi: int, P: int) -> Optional[in
         N, K = (int(d) for d in ir.values[P].shape)
         sa = ir.values[A].shape
         M = int(sa[1] if bool(a.get("transA", False)) else sa[0])
-        if K % 4 or not _aligned16(ir, P) or ((M + 63) // 64) * ((N + 63) // 64) >= SMALL_GEMM_MAX_TILES64:
+        if K % 4 or not _aligned16(ir, P) or ((M + 63) // 64) * ((N + 63) // 64) >= SMALL_GEMM_MAX_TILES64 \
+                or not _small_gemm_ranges_ok(ir, (A, P)):
             continue
         return k
     return None

@@ -224,6 +224,9 @@ def test_grad_group_refuses_conflicting_jobs(lib):
     # GEMM shapes must chain
     jobs = [(0, 0, 1, 0, 0, 0)]
     assert call(lib, GRAD_GROUP, [A, d((31, 16), ptr=2 * MB)], [C2], GGRP, _group_payload(jobs), kid) == INV
+    # an operand spanning 2^31 bytes or more (the small GEMM's buffer offsets are 32-bit)
+    wide_a, wide_b = d((16, 1 << 27), ptr=1 << 40), d((1 << 27, 16), ptr=1 << 42)
+    assert call(lib, GRAD_GROUP, [wide_a, wide_b], [d((16, 16), ptr=3 * MB)], GGRP, _group_payload(jobs), kid) == INV
 
 
 def test_adamw_multi_refuses_aliasing_and_bad_layouts(lib):
@@ -508,3 +511,19 @@ def test_gemm_bcopy_refuses_what_it_cannot_copy(lib):
     # the general epilogue variants refuse the two-output call
     assert call(lib, GEMM_EPILOGUE, [A, W, b], [C, Wc], GEPI, struct.pack("<iii", 0, 1, 0),
                 "gemm_bias_relu_f32_naive_v0") == INV
+
+
+def test_group_jobs_refuse_operands_past_32_bit_offsets():
+    """The small GEMM reads through 32-bit buffer offsets: a GEMM whose
+    operand spans 2^31 bytes or more stays out of the group (the host check
+    of the kernel refuses it too)."""
+    from aicf_hip.ir import IRGraph
+    from aicf_hip.lower import _job_of
+
+    ir = IRGraph(name="wide")
+    nv = lambda n, s: ir.new_value(name=n, shape=s, dtype="torch.float32", device="cpu").id  # noqa: E731
+    a, b, c = nv("a", (16, 1 << 27)), nv("b", (1 << 27, 16)), nv("c", (16, 16))
+    it = {"op": "gemm", "inputs": [a, b], "outputs": [c], "attrs": {}}
+    assert _job_of(ir, it) is None  # 16 x 2^27 floats = 8 GiB
+    a2, b2 = nv("a2", (16, 1 << 20)), nv("b2", (1 << 20, 16))
+    assert _job_of(ir, {"op": "gemm", "inputs": [a2, b2], "outputs": [c], "attrs": {}}) is not None
