@@ -332,6 +332,16 @@ PYBIND11_MODULE(_C, m) {
       "graph_launch_h",
       [](uint64_t h) { hip_check(aicf_graph_launch_h(h, current_stream()), "hipGraphLaunch"); },
       py::arg("handle"));
+  // n replays in one call (not in the reference binding): for graphs of a
+  // few microseconds the per-call interpreter overhead would otherwise set
+  // the replay rate
+  m.def(
+      "graph_launch_h_n",
+      [](uint64_t h, int64_t n) {
+        void* s = current_stream();
+        for (int64_t i = 0; i < n; ++i) hip_check(aicf_graph_launch_h(h, s), "hipGraphLaunch");
+      },
+      py::arg("handle"), py::arg("n"));
   m.def("graph_reset_h", [](uint64_t h) { hip_check(aicf_graph_reset_h(h), "graph_reset"); },
         py::arg("handle"));
   m.def("graph_stream_h", [](uint64_t h) -> uint64_t { return aicf_graph_stream_h(h); },

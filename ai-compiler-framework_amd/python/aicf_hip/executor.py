@@ -177,6 +177,7 @@ class PlannedExecutor:
         self.opts = opts or ExecOptions()
         self.env: Dict[int, torch.Tensor] = {}
         self._captured = False
+        self._steps = 1  # passes over the ops per captured graph (capture(steps=...))
         self._own_graph = bool(own_graph)
         self._handle: Optional[int] = None
         # resolve kinds and pack attributes once; the per-op host work in the
@@ -298,7 +299,15 @@ class PlannedExecutor:
 
     @torch.no_grad()
     def capture(self, *, inputs: Dict[str, Any], params: Dict[str, Any],
-                reuse_static: bool = True) -> Dict[int, torch.Tensor]:
+                reuse_static: bool = True, steps: int = 1) -> Dict[int, torch.Tensor]:
+        """Binds and captures the lowered ops into the graph.  steps > 1
+        (not in the reference executor): the graph holds that many
+        consecutive passes over the ops, and one replay advances as many
+        steps (for steps of a few microseconds, where a graph launch's own
+        cost is a large part of a replay)."""
+        if int(steps) < 1:
+            raise ValueError("[exec] capture: steps must be >= 1")
+        self._steps = int(steps)
         self.build_env(inputs=inputs, params=params, reuse_static=reuse_static)
         self._capture_env()
         return self.env
@@ -325,13 +334,15 @@ class PlannedExecutor:
                 self._handle = int(_C.graph_create())
             s = int(_C.graph_begin_h(self._handle))
             try:
-                self._execute_lowered(stream=s)
+                for _ in range(self._steps):
+                    self._execute_lowered(stream=s)
             finally:
                 _C.graph_end_h(self._handle)
         else:
             s = int(_C.graph_begin())
             try:
-                self._execute_lowered(stream=s)
+                for _ in range(self._steps):
+                    self._execute_lowered(stream=s)
             finally:
                 _C.graph_end()
         self._captured = True
@@ -343,11 +354,15 @@ class PlannedExecutor:
         if not self._captured:
             raise RuntimeError("[exec] replay called before capture()")
         if self._handle is not None:
-            for _ in range(int(n)):
-                _C.graph_launch_h(self._handle)
+            _C.graph_launch_h_n(self._handle, int(n))
         else:
             for _ in range(int(n)):
                 _C.graph_launch()
+
+    @property
+    def steps_per_replay(self) -> int:
+        """Steps one replay advances (capture(steps=...))."""
+        return self._steps
 
     @property
     def graph_handle(self) -> Optional[int]:

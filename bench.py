@@ -201,50 +201,56 @@ def bench_c4(C, dtype="bf16", shapes=C4_SHAPES, acts=("none", "relu", "gelu"), i
 
 
 # C1: the reference MLP (fp32, B=64, 784->256(ReLU)->10, softmax-xent, Adam)
-C1_VARIANTS = {"three_launch": True, "four_launch": "four", "reference_lowering": False}
+# lowering (fuse_small) and steps per captured graph
+C1_VARIANTS = {"three_launch": (True, 1), "four_launch": ("four", 1), "reference_lowering": (False, 1),
+               "three_launch_10_steps_per_replay": (True, 10)}
 
 
-def bench_c1(rounds=10, chunk=20, warm_s=STEP_WARM_S):
+def bench_c1(rounds=10, chunk=100, warm_s=STEP_WARM_S):
     """Replayed-graph time of one C1 train step for each lowering (True: the
     three-launch StageF plan, "four": its four-launch form, False: the
     reference pipeline's 17 ops), each on a graph handle of its own, warmed
-    together for warm_s, then timed in `rounds` rounds of `chunk` replays
+    together for warm_s, then timed in `rounds` rounds of `chunk` steps
     with the lowerings alternated (order reversed every other round), so
-    that clock and box state are shared."""
+    that clock and box state are shared.  The last variant captures ten
+    consecutive steps per graph: a graph launch costs ~4 us of GPU time of
+    its own, a fifth of this step."""
     import torch
 
     from aicf_hip import mlp
 
     data = mlp.init_mlp_xent()
     exs = {}
-    for k, fs in C1_VARIANTS.items():
+    for k, (fs, per) in C1_VARIANTS.items():
         ir, lowered, plan = mlp.build_mlp_xent(fuse_small=fs)
         params = {n: torch.from_numpy(v.copy()).cuda() for n, v in data.items() if "." in n}
         inputs = {"x": torch.from_numpy(data["x"]).cuda(), "t": torch.from_numpy(data["t"]).cuda()}
         ex = mlp.make_executor(ir, lowered, plan, own_graph=True)
         ex.build_env(inputs=inputs, params=params, reuse_static=False)
-        ex.capture(inputs=inputs, params=params, reuse_static=True)
+        ex.capture(inputs=inputs, params=params, reuse_static=True, steps=per)
         exs[k] = (ex, lowered)
     s = torch.cuda.current_stream()  # graph_launch replays on the caller's stream
     for ex, _ in exs.values():
         ex.replay(3)
     torch.cuda.synchronize()
-    _warm(lambda: [ex.replay(5) for ex, _ in exs.values()], warm_s)
+    _warm(lambda: [ex.replay(max(1, 10 // ex.steps_per_replay)) for ex, _ in exs.values()], warm_s)
     tot = {k: 0.0 for k in exs}
     names = list(exs)
     for r in range(rounds):
         for k in (names if r % 2 == 0 else names[::-1]):
+            ex = exs[k][0]
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record(s)
-            exs[k][0].replay(chunk)
+            ex.replay(max(1, chunk // ex.steps_per_replay))
             e1.record(s)
             torch.cuda.synchronize()
-            tot[k] += e0.elapsed_time(e1)
+            tot[k] += e0.elapsed_time(e1) / (max(1, chunk // ex.steps_per_replay) * ex.steps_per_replay)
     out = {}
     for k, (ex, lowered) in exs.items():
-        us = tot[k] * 1e3 / (rounds * chunk)
+        us = tot[k] * 1e3 / rounds
         out[k] = {"value": round(us, 2), "unit": "us/step", "steps_per_s": round(1e6 / us, 1),
-                  "ops_per_step": len(lowered), "loss_after": float(ex.value("loss").item())}
+                  "ops_per_step": len(lowered), "steps_per_replay": ex.steps_per_replay,
+                  "loss_after": float(ex.value("loss").item())}
         ex.close()
     return out
 
@@ -1421,7 +1427,7 @@ def c1_trace_report(stats_csv, trace_csv):
         "",
         "Process contents: the three-launch step (StageF), its four-launch form (AdamW in a launch of its "
         "own) and the reference pipeline's 17-op lowering, each captured on a graph handle of its own; "
-        "warmed together, then 5 rounds of 10 replays each, alternated.",
+        "warmed together, then 5 rounds of 20 steps each, alternated.",
         "",
         "| kernel | calls | avg us | % time |",
         "|---|---:|---:|---:|",
@@ -1543,7 +1549,7 @@ def main():
         streaming_only(C)
         return
     if args.c1_only:
-        print(json.dumps(bench_c1(rounds=5, chunk=10, warm_s=0.05)))
+        print(json.dumps(bench_c1(rounds=5, chunk=20, warm_s=0.05)))
         return
     if args.vendor_compare:
         vendor_compare(C, args.vendor_set)
@@ -1670,8 +1676,9 @@ def main():
         c1v = bench_c1()
         c1 = dict(c1v["three_launch"], four_launch=c1v["four_launch"],
                   reference_lowering=c1v["reference_lowering"],
-                  note="each lowering on a graph handle of its own, warmed together, then 10 rounds of 20 "
-                       "replays with the lowerings alternated")
+                  ten_steps_per_replay=c1v["three_launch_10_steps_per_replay"],
+                  note="each lowering on a graph handle of its own, warmed together, then 10 rounds of 100 "
+                       "steps with the lowerings alternated; value: one step per graph replay")
         comps["c1_mlp_fp32_64x784x256x10_step"] = c1
         log(f"[bench] c1 {c1}")
         for dt, shapes in (("bf16", C4_SHAPES), ("fp32", C4_SHAPES)):

@@ -421,3 +421,29 @@ def test_xent_head_step_variant_matches_the_plain_head(C):
         assert torch.equal(u, v)
     want = (np.float32(2e-3) / np.float32(1 - 0.8 ** 8), 1 / np.float32(1 - 0.99 ** 8))
     assert np.allclose(scal.cpu().numpy(), want, rtol=1e-6), (scal, want)
+
+
+def test_graph_of_several_steps_matches_single_step_replays(C):
+    """capture(steps=3): one replay of the three-launch step's graph advances
+    three steps, bit-identical to three replays of the one-step graph
+    (replayed with the C++ n-launch loop); steps < 1 is refused."""
+    import mlp_checks
+
+    runs = {}
+    for per, replays in ((1, 6), (3, 2)):
+        ex, inputs, params, orc_state, data = mlp_checks.xent_setup(5, fuse_small=True)
+        ex.build_env(inputs=inputs, params=params, reuse_static=False)
+        ex.capture(inputs=inputs, params=params, reuse_static=True, steps=per)
+        assert ex.steps_per_replay == per
+        ex.replay(replays)
+        torch.cuda.synchronize()
+        runs[per] = {k: p.detach().cpu().clone() for k, p in params.items()}
+        runs[per]["loss"] = ex.value("loss").detach().cpu().clone()
+        runs[per]["step"] = int(ex.value("opt.step").item())
+        with pytest.raises(ValueError):
+            ex.capture(inputs=inputs, params=params, reuse_static=True, steps=0)
+        ex.reset_graph()
+    assert runs[1]["step"] == runs[3]["step"] == 6
+    for k in runs[1]:
+        if k != "step":
+            assert torch.equal(runs[1][k], runs[3][k]), k
