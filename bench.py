@@ -563,8 +563,10 @@ def build_step(B, D, L, fuse_optimizer=True, fuse_colsum=True, fuse_tail=True):
 
 def step_gemm_times(ex, iters, warmup=2):
     """Average ms per launch of each GEMM op of the step, HIP events on
-    torch's current stream around `iters` launches of the op on the step's own
-    tensors, after one eager pass over the step (so every activation holds
+    torch's current stream around a captured graph of `iters` launches of the
+    op on the step's own tensors (back to back on the device, as in the
+    step's own graph, rather than at the rate the host issues eager
+    launches), after one eager pass over the step (so every activation holds
     this step's values; the AdamW over the biases, which no GEMM reads, is
     left out)."""
     import torch
@@ -578,7 +580,8 @@ def step_gemm_times(ex, iters, warmup=2):
     for i, (op, _kind, kid, _ins, outs, attrs) in enumerate(ex.ops):
         if op not in STEP_GEMM_OPS:
             continue
-        ms = time_launches(lambda i=i: ex.launch_op(i, stream=s.cuda_stream), iters, warmup, s)
+        ms = time_launches(lambda i=i: ex.launch_op(i, stream=torch.cuda.current_stream().cuda_stream),
+                           iters, warmup, graph=True)
         res.append({"op": i, "kernel_id": kid, "role": gemm_role(op, attrs, len(outs)), "ms": ms})
     return res
 
@@ -1396,7 +1399,7 @@ def stats_report(stats_csv, trace_csv, steps):
         if g_step:
             lines += ["", f"GEMM launches of the last replayed step: {len(g_step)}, mean "
                       f"{sum(g_step) / len(g_step):.1f} us (the roofline's avg_ms is the same mean over "
-                      "the eager launches)."]
+                      "graphs of 10 launches of each GEMM op)."]
         if g_roof:
             lines.append(f"GEMM launches after the replays (roofline measurement): {len(g_roof)}, mean "
                          f"{sum(g_roof) / len(g_roof):.1f} us.")
@@ -1582,8 +1585,8 @@ def main():
                           "(bias+GELU+Z, bias, dX+dGELU, dX, dW+AdamW epilogues)",
                 "shape": [B, D, D], "flops_per_launch": flops, "avg_ms": round(avg_ms, 4),
                 "per_role_avg_ms": {k: round(sum(v) / len(v), 4) for k, v in per_role.items()},
-                "measured": "HIP events around 10 launches of each GEMM op of the step on the step's "
-                            "own tensors (torch's current stream), after the timed replays"}
+                "measured": "HIP events (torch's current stream) around a captured graph of 10 launches of "
+                            "each GEMM op of the step on the step's own tensors, after the timed replays"}
     log(f"[bench] roofline step gemms {times}")
     ceils = {f: bench_mfma_ceiling(form=f) for f in (16, 32)}
     ceil = max(ceils.values(), key=lambda c: c["tflops"])
