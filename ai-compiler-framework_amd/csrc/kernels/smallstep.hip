@@ -246,16 +246,17 @@ int64_t sg_range_bytes(int64_t rows, int64_t sr, int64_t K, int64_t sk) {
   return ((rows - 1) * sr + (K - 1) * sk + 1) * 4;
 }
 
-// nwave 4, or 8 for the standalone kernel when K is long enough for 8 splits
-// (32 or more K blocks): each wave then has at most 8 blocks, one batch of
-// loads in flight.
+// nwave 4, or 8 / 16 for the standalone kernel when K is long enough for 8
+// splits (32 or more K blocks) / 16 splits (48 or more): each wave then has
+// at most 8 blocks, one batch of loads in flight, and with 16 waves at most
+// 4 (64 x 784 x 256, the MLP's first layer: 0.1 us less per launch).
 SgJob sg_plan(const SmallGemm& g, int nwave = 4) {
   SgJob j{};
   j.g = g;
   j.tn = (int)((g.N + 15) / 16);
   j.tiles = (int)((g.M + 15) / 16) * j.tn;
   j.kb = (int)((g.K + 15) / 16);
-  j.splits = (nwave == 8 && j.kb >= 32) ? 8 : j.kb >= 16 ? 4 : j.kb >= 8 ? 2 : 1;
+  j.splits = (nwave == 16 && j.kb >= 48) ? 16 : (nwave >= 8 && j.kb >= 32) ? 8 : j.kb >= 16 ? 4 : j.kb >= 8 ? 2 : 1;
   j.tpb = nwave / j.splits;
   j.avec = g.a_k == 1 && g.K % 4 == 0 && (g.M == 1 || g.a_m % 4 == 0) && aligned(g.A, 16);
   j.bvec = g.b_k == 1 && g.K % 4 == 0 && (g.N == 1 || g.b_n % 4 == 0) && aligned(g.B, 16);
@@ -1110,7 +1111,10 @@ bool small_gemm_ok(const SmallGemm& g) {
 Status small_gemm_f32(const SmallGemm& g, hipStream_t s) {
   if (!small_gemm_ok(g)) return Status::InvalidArgument;
   const int kb = (int)((g.K + 15) / 16);
-  if (kb >= 32) {  // long K: eight waves split it
+  if (kb >= 48) {  // long K: sixteen waves split it
+    const SgJob j = sg_plan(g, 16);
+    gemm_small_kernel<16><<<(unsigned)sg_blocks(j), 1024, 0, s>>>(j);
+  } else if (kb >= 32) {  // eight waves
     const SgJob j = sg_plan(g, 8);
     gemm_small_kernel<8><<<(unsigned)sg_blocks(j), 512, 0, s>>>(j);
   } else {
