@@ -365,8 +365,8 @@ def test_grad_group_adamw_bit_identical_to_adamw_step(C, M, N, K):
 @pytest.mark.parametrize("M,N,K", [(64, 256, 784), (5, 33, 12), (100, 40, 516)])
 def test_gemm_bcopy_writes_b_and_the_same_c(C, M, N, K):
     """gemm_small_bcopy_f32_v0: C bit-identical to the plain small-GEMM
-    epilogue on the same call, and the second output is B exactly (K-blocks
-    over 4 and 8 waves, N and K tails)."""
+    epilogue on the same call, and the second output is B exactly (K split
+    over 1, 8 and 16 waves, N and K tails)."""
     r = np.random.default_rng(M * N + K)
     A = g(r.standard_normal((M, K)).astype(np.float32))
     W = g(r.standard_normal((N, K)).astype(np.float32))
