@@ -676,6 +676,13 @@ Status launch_rows(const RowArgs& a, void* stream) {
     row_reg_kernel<LPR, VPT, MODE><<<(unsigned)((R + RPB - 1) / RPB), THREADS, 0, s>>>(a);  \
     return launch_status("row_kernel");                                                      \
   }
+  if constexpr (MODE == MODE_SOFTMAX) {
+    // C = 8192 softmax: one wave per row, 64 lanes x 32 vectors (6.06 ->
+    // 6.11 TB/s against 128 x 16, three alternated rounds; cross-entropy,
+    // with more registers live per element, drops to 5.3 TB/s this way and
+    // keeps 128 x 16)
+    ROW_CASE(64, 32)
+  }
   if constexpr (MODE == MODE_SOFTMAX || MODE == MODE_XENT) {
     // C = 8192 with a row output: 128 lanes x 16 vectors (softmax 5.98 ->
     // 6.09 TB/s, xent 5.47 -> 5.73; the row statistics are merged over 128
