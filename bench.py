@@ -561,14 +561,15 @@ def build_step(B, D, L, fuse_optimizer=True, fuse_colsum=True, fuse_tail=True):
     return ex
 
 
-def step_gemm_times(ex, iters, warmup=2):
+def step_gemm_times(ex, iters, warmup=2, graph=True, warm_s=WARM_S):
     """Average ms per launch of each GEMM op of the step, HIP events on
     torch's current stream around a captured graph of `iters` launches of the
     op on the step's own tensors (back to back on the device, as in the
     step's own graph, rather than at the rate the host issues eager
     launches), after one eager pass over the step (so every activation holds
     this step's values; the AdamW over the biases, which no GEMM reads, is
-    left out)."""
+    left out).  graph=False: eager launches instead (the counter runs, which
+    count dispatches)."""
     import torch
 
     s = torch.cuda.current_stream()
@@ -581,7 +582,7 @@ def step_gemm_times(ex, iters, warmup=2):
         if op not in STEP_GEMM_OPS:
             continue
         ms = time_launches(lambda i=i: ex.launch_op(i, stream=torch.cuda.current_stream().cuda_stream),
-                           iters, warmup, graph=True)
+                           iters, warmup, graph=graph, warm_s=warm_s)
         res.append({"op": i, "kernel_id": kid, "role": gemm_role(op, attrs, len(outs)), "ms": ms})
     return res
 
@@ -824,13 +825,13 @@ CALIB_KIB = CALIB_ELEMS * 2 / 1024
 
 def roofline_only(C, B, D, L, launches):
     """The roofline kernel family alone: one eager pass over the step, then
-    `launches` launches of each of the step's GEMM ops on its own tensors,
-    then 3 calibration copies of known size; the program profiled by the
-    FETCH_SIZE / WRITE_SIZE passes."""
+    4 warm-up and `launches` timed launches of each of the step's GEMM ops on
+    its own tensors, then 3 calibration copies of known size; the program
+    profiled by the FETCH_SIZE / WRITE_SIZE passes."""
     import torch
 
     ex = build_step(B, D, L)
-    t = step_gemm_times(ex, iters=launches, warmup=0)
+    t = step_gemm_times(ex, iters=launches, warmup=0, graph=False, warm_s=0.0)
     x = torch.ones(CALIB_ELEMS, device="cuda", dtype=torch.bfloat16)
     y = torch.empty_like(x)
     for _ in range(3):
@@ -1143,8 +1144,8 @@ def pmc_report(fetch_csv, write_csv, mfma_csv=None, trace_csv=None):
         "<mfma counter_collection.csv> <mfma kernel_trace.csv>",
         "```",
         "",
-        "`--roofline-only` builds the step, runs it once eagerly, launches each of its 12 GEMM ops 5 "
-        "more times on the step's own tensors, then 3 calibration copies.",
+        "`--roofline-only` builds the step, runs it once eagerly, launches each of its 12 GEMM ops 9 "
+        "more times on the step's own tensors (4 warm-up launches, then 5 timed), then 3 calibration copies.",
         "",
         f"calibration copy (copy_bf16_v0, {CALIB_KIB:.0f} KiB read + written): "
         f"FETCH_SIZE {mean(fe['copy']):.0f} KiB -> factor {f_r:.4f}; "
