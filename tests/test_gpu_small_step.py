@@ -35,7 +35,7 @@ def g(a, dt=None):
 
 
 SMALL = [(64, 256, 784), (256, 784, 64), (64, 784, 256), (10, 256, 64), (1, 1, 1), (17, 33, 5),
-         (100, 3, 1000), (31, 47, 130), (48, 16, 4096)]
+         (100, 3, 1000), (31, 47, 130), (48, 16, 4096), (7, 19, 803), (33, 9, 517)]
 
 
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
